@@ -1,0 +1,174 @@
+#!/usr/bin/env python3
+"""MoE block forward throughput on one MI355X.
+
+Workload (the headline): N = 16384 tokens (B=64,
+T=256), C = 1024, E = 16 experts, top-k = 2, SwiGLU hidden H = 2816, bf16
+activations and weights with fp32 accumulation, router bias ~ N(0,1)
+(skewed expert load).  A step is one MoELayer forward over the N tokens,
+inputs already resident in HBM.  Synthetic seeded data (mgpt_amd.workload).
+
+Prints one JSON line: tokens/s (value), ms/step, the roofline of the
+dominant kernel (the gate/up grouped GEMM, MFMA-bound) measured with HIP
+events inside the timed region, and the reference CPU path timed on a
+bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
+
+
+def cpu_baseline(cfg, sample_tokens: int, reps: int):
+    """The reference's own CPU MoE forward (oracle/_ref/ref_driver, built from
+    the unmodified reference sources), single-threaded as the reference is,
+    on `sample_tokens` tokens of the workload's shape."""
+    drv = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
+    if not os.path.exists(drv):
+        return None
+    cmd = [drv, "bench", str(sample_tokens), str(cfg.C), str(cfg.H), str(cfg.E), str(cfg.k),
+           str(reps)]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    if r.returncode != 0:
+        return {"error": r.stderr[-500:]}
+    res = json.loads(r.stdout.strip().splitlines()[-1])
+    try:
+        model = [l.split(":", 1)[1].strip() for l in open("/proc/cpuinfo")
+                 if l.startswith("model name")][0]
+    except Exception:
+        model = "unknown"
+    return {
+        "value": round(res["tokens_per_s"], 3), "unit": "tokens/s", "cores": 1,
+        "kind": "reference",
+        "sample": (f"{sample_tokens} of {cfg.N} tokens at the workload's shape "
+                   f"(C={cfg.C}, E={cfg.E}, k={cfg.k}, H={cfg.H}), fp32 reference CPU path "
+                   f"(MoELayer::forward_into), 1 warmup + median of {reps}; "
+                   f"1 thread of {os.cpu_count()} visible cores, {model}"),
+        "median_s": res["median_s"],
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg3")
+    ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "expert-parallel multi-GPU path is a design note, not implemented", file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    from mgpt_amd import workload as wl
+    from mgpt_amd.moe import MoELayer
+
+    cfg = wl.CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    t0 = time.time()
+    inp = wl.make_inputs(cfg, seed=20261201)
+    layer = MoELayer(cfg.C, cfg.H, cfg.E, cfg.k, act=cfg.act, weights=cfg.weights)
+    layer.load_parameters(inp.params(raw=True))
+    dt = torch.float32 if cfg.act == "f32" else torch.bfloat16
+    x = torch.from_numpy(inp.x).to(dev).to(dt)
+    y = torch.empty_like(x)
+    del inp
+    print(f"setup {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    for _ in range(args.warmup):
+        layer.forward_into(x, y)
+    torch.cuda.synchronize()
+    counts = layer.get_expert_counts()
+
+    layer.set_profiling(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    start.record()
+    for _ in range(args.steps):
+        layer.forward_into(x, y)
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms_per_step = start.elapsed_time(stop) / args.steps
+    stages = layer.stage_times()
+    n_prof = stages.pop("forwards")
+    layer.set_profiling(False)
+
+    N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
+    A = N * k
+    a = 2 if cfg.act == "bf16" else 4
+    w = {"bf16": 2, "fp8": 1, "f32": 4}[cfg.weights]
+    gateup_flops = 4.0 * A * C * H
+    down_flops = 2.0 * A * H * C
+    t_gu = stages["gemm_gateup"] * 1e-3
+    t_dn = stages["gemm_down"] * 1e-3
+    gu_tflops = gateup_flops / t_gu / 1e12
+    gemm_tflops = (gateup_flops + down_flops) / (t_gu + t_dn) / 1e12
+    permute_bytes = 2.0 * A * C * a + 8 * A
+    combine_bytes = A * C * a + N * C * a + 8 * A
+    router_bytes = N * C * a + C * E * 4 + 8 * A
+    hbm = {
+        "router_topk_GBs": router_bytes / (stages["router_topk"] * 1e-3) / 1e9,
+        "permute_GBs": permute_bytes / (stages["permute"] * 1e-3) / 1e9,
+        "combine_GBs": combine_bytes / (stages["combine"] * 1e-3) / 1e9,
+    }
+    total_flops = 2.0 * N * C * E + 6.0 * A * C * H
+    result = {
+        "metric": METRIC,
+        "value": round(N / (ms_per_step * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.act == "bf16" else "f32",
+        "data": "synthetic (seeded; mgpt_amd.workload)",
+        "config": {"workload": f"{cfg.name}: MoE block forward N={N} (B={cfg.B},T={cfg.T}) "
+                               f"C={C} E={E} k={k} H={H} act={cfg.act} weights={cfg.weights} "
+                               f"router_bias={cfg.router_bias}",
+                   "N": N, "C": C, "E": E, "k": k, "H": H, "global_batch": cfg.B,
+                   "seq_len": cfg.T, "parallelism": "single GPU"},
+        "layer_tflops": round(total_flops / (ms_per_step * 1e-3) / 1e12, 2),
+        "expert_gemm_tflops": round(gemm_tflops, 2),
+        "expert_gemm_mfma_frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        "stage_ms": {kk: round(v, 4) for kk, v in stages.items()},
+        "stage_ms_forwards_averaged": n_prof,
+        "hbm_frac": {kk.replace("_GBs", ""): round(v / PEAK_HBM_GBS, 4) for kk, v in hbm.items()},
+        "expert_counts_max_over_mean": round(max(counts) / (sum(counts) / len(counts)), 3),
+        "roofline": {
+            "kernel": "grouped_gemm gate/up + SwiGLU epilogue",
+            "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        print("cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_tokens, N), args.cpu_reps)
+    print(json.dumps(result))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

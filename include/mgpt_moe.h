@@ -1,0 +1,151 @@
+/*
+ * mgpt_moe.h -- C ABI of the MI355X (gfx950) Mixture-of-Experts block forward.
+ *
+ * Drop-in device path for mgpt's MoELayer (mrtcemberci/mgpt,
+ * src/main/neuralnetwork/layers/MoELayer.{h,cpp}).  The engine's C++ layer
+ * keeps its public API and calls these functions instead of the cuda_ops::
+ * free functions it uses today (src/main/utils/cuda_ops.h:7-110).  Plain C:
+ * no HIP, torch or C++ types cross the boundary.  Streams are passed as
+ * `void*` holding a hipStream_t (NULL = the default stream); every device
+ * pointer is a HIP device address.
+ *
+ * Semantics follow the reference CPU path exactly for routing (router
+ * logits, clamped softmax, top-k with the lower-expert-id tie rule, expert
+ * counts, and the stable expert-major permutation of flat assignment ids
+ * i = t*k + j); expert outputs are within the precision of the configured
+ * dtypes (fp32: 1e-5 relative; bf16: 2e-2; fp8 e4m3 weights: 6e-2).
+ *
+ * All functions return an mgpt_status; none exits the process.  After a
+ * nonzero status, mgpt_moe_last_error() describes it (per host thread).
+ * A handle is not safe for concurrent use from several host threads; use one
+ * handle per concurrent stream.
+ */
+#ifndef MGPT_MOE_H
+#define MGPT_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum mgpt_status {
+  MGPT_OK = 0,
+  MGPT_ERR_INVALID_ARGUMENT = 1,   /* null pointer, bad size, bad shape */
+  MGPT_ERR_UNSUPPORTED = 2,        /* valid but not built for (e.g. C % 64 != 0) */
+  MGPT_ERR_WORKSPACE_TOO_SMALL = 3,
+  MGPT_ERR_NOT_READY = 4,          /* forward before parameters were loaded */
+  MGPT_ERR_HIP = 5,                /* a HIP runtime call failed */
+  MGPT_ERR_OUT_OF_MEMORY = 6
+} mgpt_status;
+
+typedef enum mgpt_dtype {
+  MGPT_DTYPE_F32 = 0,
+  MGPT_DTYPE_BF16 = 1,
+  MGPT_DTYPE_FP8_E4M3 = 2          /* OCP E4M3FN, per-output-channel fp32 scale */
+} mgpt_dtype;
+
+/* Shape and precision of one MoE block.  Replaces the constructor arguments
+ * MoELayer(int embed_dim, int hidden_dim, int num_experts, int top_k)
+ * (layers/MoELayer.cpp:4-12; hidden_dim -1 means 4*embed_dim as in
+ * layers/SwiGLU.cpp:4-9). */
+typedef struct mgpt_moe_config {
+  int embed_dim;     /* C: multiple of 64 */
+  int hidden_dim;    /* H: > 0, or -1 for 4*C */
+  int num_experts;   /* E: 1..64 */
+  int top_k;         /* k: 1..min(E, 8) */
+  int act_dtype;     /* x and y: MGPT_DTYPE_F32 or MGPT_DTYPE_BF16 */
+  int weight_dtype;  /* F32 (act F32 only), BF16 or FP8_E4M3 (act BF16 only) */
+} mgpt_moe_config;
+
+typedef struct mgpt_moe mgpt_moe;   /* opaque handle; owns packed weights */
+
+/* Creates a handle on the current HIP device.  Replaces the MoELayer
+ * constructor (layers/MoELayer.cpp:4-12). */
+int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out);
+
+/* Frees the handle and its device memory. */
+int mgpt_moe_destroy(mgpt_moe* h);
+
+/* Loads the 2 + 6E fp32 parameters in MoELayer::get_parameters() order
+ * (layers/MoELayer.cpp:225-236, layers/SwiGLU.cpp:98-103,
+ * layers/LinearLayer.cpp:87-89), each in reference layout:
+ *   W_r [C,E], b_r [1,E], then for each expert e:
+ *   W_gate [C,H], b_gate [1,H], W_up [C,H], b_up [1,H], W_down [H,C], b_down [1,C].
+ * `params_on_device` = 1 if the pointers are device addresses, 0 for host.
+ * The library copies and packs them (transposed tiles; bf16 rounding or
+ * per-output-channel e4m3 quantisation for the expert weights; the router
+ * stays fp32).  Replaces Layer::to(Device::CUDA) (layers/Layer.h:46-51) for
+ * this layer.  Synchronous with respect to `stream`'s prior work. */
+int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params,
+                             int num_params, int params_on_device, void* stream);
+
+/* Device workspace needed by mgpt_moe_forward for num_tokens tokens.
+ * Replaces MoELayer::get_footprint (layers/MoELayer.cpp:238-251) for the
+ * forward pass; the caller may carve it from its Scratchpad arena. */
+int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes);
+
+/* y[N,C] = MoE(x[N,C]) on `stream`, no host synchronisation.  x and y are
+ * act_dtype, row-major, device memory; y must not alias x.  The workspace
+ * (>= mgpt_moe_workspace_bytes) holds the routing of this call until the
+ * next call that uses it.  num_tokens = 0 is a no-op.  Replaces
+ * MoELayer::forward_into (layers/MoELayer.cpp:28-128) on the device. */
+int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/* Device views of the routing produced by the last mgpt_moe_forward into
+ * `workspace` (valid once that call has completed on its stream):
+ *   topk_idx [N,k] int32, topk_p [N,k] fp32 (descending p; raw clamped
+ *   softmax probabilities, not renormalised), counts [E] int32,
+ *   perm [N*k] int32 (slot -> flat assignment id t*k+j, expert-major,
+ *   ascending flat id within an expert), slot_of [N*k] int32 (its inverse).
+ * Replaces the reference's cached_top_indices, cached_top_probs,
+ * cached_expert_counts and cached_sorted_token_ids (layers/MoELayer.h:18-28),
+ * which it stores as float; these are int32. */
+typedef struct mgpt_moe_routing {
+  int32_t* topk_idx;
+  float* topk_p;
+  int32_t* counts;
+  int32_t* perm;
+  int32_t* slot_of;
+} mgpt_moe_routing;
+int mgpt_moe_get_routing(const mgpt_moe* h, int num_tokens, void* workspace,
+                         mgpt_moe_routing* out);
+
+/* Copies the per-expert token counts of the last forward to host memory,
+ * waiting for that forward to finish.  Replaces MoELayer::get_expert_counts
+ * (layers/MoELayer.h:39), which returns them as float. */
+int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
+
+/* Measurement (no counterpart in the reference): while enabled, each
+ * forward records HIP events on its stream at the stage boundaries (into a
+ * ring of the last 64 forwards; enabling resets it).  mgpt_moe_stage_times
+ * waits for the last profiled forward and returns the mean stage durations
+ * in ms over the recorded forwards: [0] router+top-k, [1] dispatch scan,
+ * [2] permute, [3] gate/up GEMM + SwiGLU, [4] down GEMM, [5] combine; if
+ * n > 6, ms[6] receives the number of forwards averaged. */
+#define MGPT_MOE_NUM_STAGES 6
+int mgpt_moe_set_profiling(mgpt_moe* h, int enable);
+int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n);
+
+/* fp8 handles only: copies expert `expert`'s quantised weight `which`
+ * (0 = W_gate, 1 = W_up, 2 = W_down) to host in reference layout [in,out]
+ * as e4m3 bytes, with its per-output-channel scales [out].  For tests of
+ * the quantiser; no counterpart in the reference. */
+int mgpt_moe_export_fp8(const mgpt_moe* h, int expert, int which,
+                        uint8_t* q_host, float* scale_host);
+
+/* Diagnostic (no counterpart in the reference): evaluates the router's
+ * device expf -- the GPU restatement of the host C library's expf that the
+ * reference's softmax calls (utils/Tensor.cpp:873) -- on n device floats,
+ * so tests can compare it bit for bit with the host expf. */
+int mgpt_moe_device_expf(const float* d_in, float* d_out, int n, void* stream);
+
+/* Description of the last error on this host thread ("" if none). */
+const char* mgpt_moe_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MGPT_MOE_H */

@@ -1,0 +1,119 @@
+// common.hpp -- shared device helpers for the gfx950 MoE kernels.
+//
+// All sources are compiled with -ffp-contract=off, so a * b + c is two
+// correctly rounded operations unless fma() is written explicitly; the
+// router's bit-exactness relies on that.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mgpt {
+
+typedef uint16_t bf16_t;   // bfloat16 bit pattern
+typedef uint8_t fp8_t;     // OCP E4M3FN bit pattern
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+constexpr int kMaxExperts = 64;
+constexpr int kMaxTopK = 8;
+// Tokens per router / permute block: one block owns the flat assignment
+// range [b*kRouterTokens*k, (b+1)*kRouterTokens*k).
+constexpr int kRouterTokens = 64;
+
+// Grouped-GEMM epilogues (gemm.hip).
+enum Epilogue { kEpiGateUp = 0, kEpiDown = 1 };
+
+__device__ __forceinline__ float bf16_to_f32(bf16_t v) {
+  return __uint_as_float(((uint32_t)v) << 16);
+}
+
+// Round-to-nearest-even float -> bfloat16 (NaN stays NaN).
+__host__ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+  uint32_t u;
+#ifdef __HIP_DEVICE_COMPILE__
+  u = __float_as_uint(f);
+#else
+  __builtin_memcpy(&u, &f, 4);
+#endif
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (bf16_t)((u | 0x00400000u) >> 16);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+template <typename T> struct ActTraits;
+template <> struct ActTraits<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+};
+template <> struct ActTraits<bf16_t> {
+  static __device__ __forceinline__ float load(const bf16_t* p) { return bf16_to_f32(*p); }
+};
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return bf16_to_f32(v); }
+__device__ __forceinline__ void store_act(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_act(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    int t = __shfl_up(v, d, kWave);
+    if (l >= d) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, kWave);
+  return v;
+}
+
+// Which expert segment an m-tile belongs to.  Grouped GEMMs launch a grid
+// over an upper bound of m-tiles; each block derives its expert, the
+// segment's first row and its end row from the per-expert counts (E <= 64),
+// so no host round-trip is needed.  Returns false for blocks past the last
+// tile.  Must be called by every thread of the block (uses shared memory).
+struct TileInfo {
+  int expert;
+  int row0;     // first row of this m-tile (global slot index)
+  int row_end;  // one past the last row of the expert's segment
+};
+
+template <int BM>
+__device__ __forceinline__ bool find_tile(const int32_t* __restrict__ counts, int E,
+                                          int mtile, TileInfo* out) {
+  __shared__ int s_info[4];
+  if (threadIdx.x < kWave) {
+    const int l = lane_id();
+    int cnt = (l < E) ? counts[l] : 0;
+    int tiles = (cnt + BM - 1) / BM;
+    int rows_incl = wave_incl_scan(cnt);
+    int tiles_incl = wave_incl_scan(tiles);
+    int tiles_excl = tiles_incl - tiles;
+    bool mine = (l < E) && (mtile >= tiles_excl) && (mtile < tiles_incl);
+    unsigned long long m = __ballot(mine);
+    int owner = m ? (__ffsll((long long)m) - 1) : 0;
+    int row0 = __shfl((rows_incl - cnt) + (mtile - tiles_excl) * BM, owner, kWave);
+    int rend = __shfl(rows_incl, owner, kWave);
+    if (l == 0) {
+      s_info[0] = m ? owner : -1;
+      s_info[1] = row0;
+      s_info[2] = rend;
+    }
+  }
+  __syncthreads();
+  out->expert = s_info[0];
+  out->row0 = s_info[1];
+  out->row_end = s_info[2];
+  return out->expert >= 0;
+}
+
+}  // namespace mgpt

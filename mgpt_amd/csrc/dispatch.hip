@@ -1,0 +1,157 @@
+// dispatch.hip -- expert counts, per-block bases and the stable permutation.
+//
+// Reference: histogram utils/Tensor.cpp:1336-1352, host exclusive scan
+// layers/MoELayer.cpp:61-80, gather utils/Tensor.cpp:1354-1383.  The
+// reference CPU path assigns slots by walking the flat assignment ids
+// i = t*k + j in ascending order and taking slot = offsets[e]++, so each
+// expert's segment holds its assignments in ascending i.  Here that order is
+// rebuilt as a counting sort that needs no host round-trip:
+//   counts[e]      = sum over router blocks b of hist[e][b]
+//   base[e][b]     = offset[e] + sum_{b' < b} hist[e][b']      (scan kernel)
+//   slot(i)        = base[e][block(i)] + #{i' < i in block(i) : e(i') = e}
+// The within-block rank comes from wave ballots over 64 consecutive ids at
+// a time (6 ballots give the lanes holding the same expert id, E <= 64).
+// The permute kernel then copies each token's row once from HBM into all k
+// of its slots with 16-byte loads and stores.
+#include "common.hpp"
+
+namespace mgpt {
+namespace {
+
+// One block per expert: exclusive scan of hist[e][0..nb) -> base[e][.],
+// total -> counts[e].  (offset[e] is added by the consumers, which read the
+// E <= 64 counts themselves.)
+__global__ __launch_bounds__(256) void expert_scan_kernel(const int32_t* __restrict__ hist, int nb,
+                                                          int32_t* __restrict__ base,
+                                                          int32_t* __restrict__ counts) {
+  __shared__ int s_wave[4];
+  __shared__ int s_carry;
+  const int e = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int w = tid / kWave;
+  if (tid == 0) s_carry = 0;
+  __syncthreads();
+  for (int b0 = 0; b0 < nb; b0 += 256) {
+    const int b = b0 + tid;
+    const int v = (b < nb) ? hist[(size_t)e * nb + b] : 0;
+    const int incl = wave_incl_scan(v);
+    if (lane_id() == kWave - 1) s_wave[w] = incl;
+    __syncthreads();
+    int pre = s_carry;
+    for (int i = 0; i < w; ++i) pre += s_wave[i];
+    if (b < nb) base[(size_t)e * nb + b] = pre + incl - v;
+    __syncthreads();
+    if (tid == 255) s_carry = pre + incl;
+    __syncthreads();
+  }
+  if (tid == 0) counts[e] = s_carry;
+}
+
+// 16-byte vector of activations.
+struct alignas(16) V16 {
+  uint32_t w[4];
+};
+
+// One block per router block (kRouterTokens tokens = kRouterTokens*k flat ids).
+template <typename ActT>
+__global__ __launch_bounds__(256) void permute_kernel(
+    const ActT* __restrict__ x, const int32_t* __restrict__ topk_idx,
+    const int32_t* __restrict__ counts, const int32_t* __restrict__ base, int nb, int N, int C,
+    int E, int k, int32_t* __restrict__ perm, int32_t* __restrict__ slot_of,
+    ActT* __restrict__ xg) {
+  __shared__ int s_base[kMaxExperts];
+  __shared__ int s_run[kMaxExperts];
+  __shared__ int s_slot[kRouterTokens * kMaxTopK];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int tok0 = b * kRouterTokens;
+  const int ntok = min(kRouterTokens, N - tok0);
+  const int nflat = ntok * k;
+  const size_t flat0 = (size_t)tok0 * k;
+
+  for (int f = tid; f < kRouterTokens * kMaxTopK; f += 256) s_slot[f] = -1;
+  if (tid < kWave) {
+    // Exclusive offsets of the experts, then this block's bases.
+    const int l = tid;
+    const int cnt = (l < E) ? counts[l] : 0;
+    const int excl = wave_incl_scan(cnt) - cnt;
+    if (l < E) {
+      s_base[l] = excl + base[(size_t)l * nb + b];
+      s_run[l] = 0;
+    }
+  }
+  __syncthreads();
+  if (tid < kWave) {
+    const int l = tid;
+    const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (kWave - l));
+    for (int f0 = 0; f0 < nflat; f0 += kWave) {
+      const int f = f0 + l;
+      int e = (f < nflat) ? topk_idx[flat0 + f] : -1;
+      // Ids outside [0, E) are skipped, as the reference's histogram and
+      // gather skip them (utils/Tensor.cpp:1348, :1368).
+      const bool valid = e >= 0 && e < E;
+      if (!valid) e = 0;
+      unsigned long long match = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 6; ++bit) {
+        const unsigned long long on = __ballot(valid && ((e >> bit) & 1));
+        match &= ((e >> bit) & 1) ? on : ~on;
+      }
+      if (valid) {
+        const int run = s_run[e];
+        const int rank = run + __popcll(match & lt);
+        const int slot = s_base[e] + rank;
+        s_slot[f] = slot;
+        perm[slot] = (int32_t)(flat0 + f);
+        slot_of[flat0 + f] = slot;
+        // The highest lane of each expert group advances the running count.
+        if ((match >> l) == 1ull) s_run[e] = run + __popcll(match);
+      }
+    }
+  }
+  __syncthreads();
+  // Row copy: wave w handles tokens w, w+4, ...; 16-byte chunks across lanes.
+  const int w = tid / kWave;
+  const int l = lane_id();
+  const int chunks = C * (int)sizeof(ActT) / 16;
+  for (int r = w; r < ntok; r += 4) {
+    const V16* src = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C);
+    for (int q = l; q < chunks; q += kWave) {
+      const V16 v = src[q];
+      for (int j = 0; j < k; ++j) {
+        const int slot = s_slot[r * k + j];
+        if (slot < 0) continue;
+        V16* dst = reinterpret_cast<V16*>(xg + (size_t)slot * C);
+        dst[q] = v;
+      }
+    }
+  }
+}
+
+}  // namespace
+
+hipError_t launch_expert_scan(const int32_t* hist, int nb, int E, int32_t* base, int32_t* counts,
+                              hipStream_t stream) {
+  hipLaunchKernelGGL(expert_scan_kernel, dim3(E), dim3(256), 0, stream, hist, nb, base, counts);
+  return hipGetLastError();
+}
+
+template <typename ActT>
+hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t* counts,
+                          const int32_t* base, int N, int C, int E, int k, int32_t* perm,
+                          int32_t* slot_of, ActT* xg, hipStream_t stream) {
+  const int nb = (N + kRouterTokens - 1) / kRouterTokens;
+  if (nb == 0) return hipSuccess;
+  hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb), dim3(256), 0, stream, x, topk_idx, counts,
+                     base, nb, N, C, E, k, perm, slot_of, xg);
+  return hipGetLastError();
+}
+
+template hipError_t launch_permute<float>(const float*, const int32_t*, const int32_t*,
+                                          const int32_t*, int, int, int, int, int32_t*, int32_t*,
+                                          float*, hipStream_t);
+template hipError_t launch_permute<bf16_t>(const bf16_t*, const int32_t*, const int32_t*,
+                                           const int32_t*, int, int, int, int, int32_t*,
+                                           int32_t*, bf16_t*, hipStream_t);
+
+}  // namespace mgpt

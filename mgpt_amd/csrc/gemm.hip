@@ -1,0 +1,275 @@
+// gemm.hip -- grouped expert GEMMs on CDNA4 matrix cores.
+//
+// Reference: per expert e with count_e > 0, SwiGLU::forward_into
+// (layers/SwiGLU.cpp:23-50): g = X_e W_g + b_g, u = X_e W_u + b_u,
+// h = silu(g) * u (utils/Tensor.cpp:1986-2004), y_e = h W_d + b_d, run by a
+// host loop over experts (layers/MoELayer.cpp:94-118).  Here each product is
+// one launch over all experts: the rows of X are expert-contiguous segments
+// (dispatch.hip), the grid covers an upper bound of m-tiles, and each block
+// finds its expert from the device-side counts (common.hpp find_tile).
+//
+// Operands: A = activations [rows][K] (bf16 or fp32, K contiguous);
+// B = packed weights [E][Npad][K] (K contiguous, so both MFMA operands are
+// read as 16-byte K-runs); C = A . B^T.  Tiles: block BM x BN x BK with 4
+// waves in a WM x WN grid; each wave owns (BM/WM) x (BN/WN) made of 32x32
+// MFMA tiles: v_mfma_f32_32x32x16_bf16 for bf16 (and fp8 weights, which are
+// widened to bf16 exactly while being staged into LDS), v_mfma_f32_32x32x2_f32
+// for fp32.  Global -> register -> LDS double buffering: the next K-slab is
+// fetched while the current one feeds the MFMAs; one barrier per slab.
+//
+// Epilogues: GATEUP (B rows interleaved in 64-row groups [32 gate | 32 up]
+// for the same 32 hidden units, so a wave's two adjacent 32x32 tiles hold
+// g and u of the same (row, h) in the same lane) computes
+// h = silu(g*s_g + b_g) * (u*s_u + b_u) and stores bf16/fp32 h;
+// DOWN stores o = acc*s + b_d in the activation dtype.
+#include "common.hpp"
+
+namespace mgpt {
+
+namespace {
+
+template <typename AT> struct KSlab;
+template <> struct KSlab<bf16_t> { static constexpr int BK = 64; };
+template <> struct KSlab<float> { static constexpr int BK = 32; };
+
+struct alignas(16) U4 {
+  uint32_t x, y, z, w;
+};
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// e4m3 byte pair -> two bf16 in one dword (exact: every e4m3 value is a bf16 value).
+template <bool HI>
+__device__ __forceinline__ uint32_t e4m3x2_to_bf16x2(uint32_t packed_bytes) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  bf16x2_t v = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)packed_bytes, 1.0f, HI);
+  uint32_t r;
+  __builtin_memcpy(&r, &v, 4);
+  return r;
+}
+
+template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
+__global__ __launch_bounds__(256) void grouped_gemm_kernel(
+    const AT* __restrict__ A, const WT* __restrict__ B, const float* __restrict__ wscale,
+    const float* __restrict__ bias0, const float* __restrict__ bias1,
+    const int32_t* __restrict__ counts, int E, int K, int Npad, int n_store, int bias_ld,
+    OutT* __restrict__ out, int ldo) {
+  constexpr int BK = KSlab<AT>::BK;
+  constexpr int PAD = 16 / (int)sizeof(AT);
+  constexpr int LDK = BK + PAD;
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 32, TN = WTN / 32;
+  static_assert(WM * WN == 4, "4 waves");
+  static_assert(TM >= 1 && TN >= 1, "wave tile >= 32x32");
+  static_assert(EPI != kEpiGateUp || (TN % 2 == 0), "gate/up pairs");
+  constexpr bool kF32 = sizeof(AT) == 4;
+  constexpr bool kFp8 = sizeof(WT) == 1;
+  // 16-byte chunks per K-slab row, and per-thread chunk counts.
+  constexpr int A_CPR = BK * (int)sizeof(AT) / 16;             // 8
+  constexpr int B_CPR = BK * (int)sizeof(WT) / 16;             // 8 (bf16/f32) or 4 (fp8)
+  constexpr int A_CH = BM * A_CPR / 256;
+  constexpr int B_CH = BN * B_CPR / 256;
+  static_assert(A_CH >= 1 && B_CH >= 1, "tile too small for 256 threads");
+
+  __shared__ __attribute__((aligned(16))) AT sA[2][BM][LDK];
+  __shared__ __attribute__((aligned(16))) AT sB[2][BN][LDK];
+
+  TileInfo ti;
+  if (!find_tile<BM>(counts, E, blockIdx.y, &ti)) return;
+  const int e = ti.expert;
+  const int n0 = blockIdx.x * BN;
+  const int tid = threadIdx.x;
+  const int w = tid / kWave, lane = lane_id();
+  const int wm = w / WN, wn = w % WN;
+
+  const AT* Ablk = A + (size_t)ti.row0 * K;
+  const WT* Bblk = B + ((size_t)e * Npad + n0) * K;
+
+  U4 ra[A_CH], rb[B_CH];
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+    const char* abase = reinterpret_cast<const char*>(Ablk + (size_t)kt * BK);
+    const char* bbase = reinterpret_cast<const char*>(Bblk + (size_t)kt * BK);
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int q = tid + 256 * i;
+      const int r = q / A_CPR, c = q % A_CPR;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(abase + (size_t)r * K * sizeof(AT) + c * 16);
+      ra[i].x = v.x; ra[i].y = v.y; ra[i].z = v.z; ra[i].w = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) {
+      const int q = tid + 256 * i;
+      const int r = q / B_CPR, c = q % B_CPR;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(bbase + (size_t)r * K * sizeof(WT) + c * 16);
+      rb[i].x = v.x; rb[i].y = v.y; rb[i].z = v.z; rb[i].w = v.w;
+    }
+  };
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int q = tid + 256 * i;
+      const int r = q / A_CPR, c = q % A_CPR;
+      *reinterpret_cast<U4*>(reinterpret_cast<char*>(&sA[buf][r][0]) + c * 16) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) {
+      const int q = tid + 256 * i;
+      const int r = q / B_CPR, c = q % B_CPR;
+      if constexpr (kFp8) {
+        // 16 e4m3 bytes -> 16 bf16 (32 bytes) at element offset c*16.
+        U4 lo, hi;
+        lo.x = e4m3x2_to_bf16x2<false>(rb[i].x); lo.y = e4m3x2_to_bf16x2<true>(rb[i].x);
+        lo.z = e4m3x2_to_bf16x2<false>(rb[i].y); lo.w = e4m3x2_to_bf16x2<true>(rb[i].y);
+        hi.x = e4m3x2_to_bf16x2<false>(rb[i].z); hi.y = e4m3x2_to_bf16x2<true>(rb[i].z);
+        hi.z = e4m3x2_to_bf16x2<false>(rb[i].w); hi.w = e4m3x2_to_bf16x2<true>(rb[i].w);
+        U4* dst = reinterpret_cast<U4*>(&sB[buf][r][c * 16]);
+        dst[0] = lo;
+        dst[1] = hi;
+      } else {
+        *reinterpret_cast<U4*>(reinterpret_cast<char*>(&sB[buf][r][0]) + c * 16) = rb[i];
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int KT = K / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+    if constexpr (!kF32) {
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8 af[TM], bfr[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const bf16x8*>(
+              &sA[cur][wm * WTM + i * 32 + lrow][ks * 16 + lhalf * 8]);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8*>(
+              &sB[cur][wn * WTN + j * 32 + lrow][ks * 16 + lhalf * 8]);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < BK / 2; ++ks) {
+        float af[TM], bfr[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = sA[cur][wm * WTM + i * 32 + lrow][ks * 2 + lhalf];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bfr[j] = sB[cur][wn * WTN + j * 32 + lrow][ks * 2 + lhalf];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < KT) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue.  Accumulator register v of a 32x32 tile holds row
+  // 8*(v/4) + 4*(lane/32) + v%4 and column lane%32.
+  const int row_base = ti.row0 + wm * WTM;
+  if constexpr (EPI == kEpiGateUp) {
+#pragma unroll
+    for (int q = 0; q < TN / 2; ++q) {
+      const int prow = n0 + wn * WTN + q * 64 + lrow;   // packed row of the gate column
+      const int hcol = (n0 + wn * WTN) / 2 + q * 32 + lrow;
+      const float sg = kFp8 ? wscale[(size_t)e * Npad + prow] : 1.0f;
+      const float su = kFp8 ? wscale[(size_t)e * Npad + prow + 32] : 1.0f;
+      const float bg = bias0[(size_t)e * bias_ld + hcol];
+      const float bu = bias1[(size_t)e * bias_ld + hcol];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = row_base + i * 32 + 8 * (v / 4) + 4 * lhalf + (v % 4);
+          if (row < ti.row_end) {
+            float g = acc[i][2 * q][v];
+            float u = acc[i][2 * q + 1][v];
+            if (kFp8) { g = g * sg; u = u * su; }
+            g = g + bg;
+            u = u + bu;
+            const float ex = kF32 ? expf(-g) : __expf(-g);
+            const float hv = (g / (1.0f + ex)) * u;
+            store_act(out + (size_t)row * ldo + hcol, hv);
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int col = n0 + wn * WTN + j * 32 + lrow;
+      if (col >= n_store) continue;
+      const float s = kFp8 ? wscale[(size_t)e * Npad + col] : 1.0f;
+      const float b = bias0[(size_t)e * bias_ld + col];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = row_base + i * 32 + 8 * (v / 4) + 4 * lhalf + (v % 4);
+          if (row < ti.row_end) {
+            float o = acc[i][j][v];
+            if (kFp8) o = o * s;
+            store_act(out + (size_t)row * ldo + col, o + b);
+          }
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Host launcher.  max_mtiles must bound sum_e ceil(count_e / BM) (the
+// caller uses ceil(A / BM) + E); surplus blocks exit after find_tile.
+template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
+hipError_t launch_grouped_gemm(const AT* A, const WT* B, const float* wscale, const float* bias0,
+                               const float* bias1, const int32_t* counts, int E, int K, int Npad,
+                               int n_store, int bias_ld, OutT* out, int ldo, int max_mtiles,
+                               hipStream_t stream) {
+  if (max_mtiles <= 0) return hipSuccess;
+  dim3 grid(Npad / BN, max_mtiles);
+  hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WM, WN, AT, WT, EPI, OutT>), grid, dim3(256), 0,
+                     stream, A, B, wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out,
+                     ldo);
+  return hipGetLastError();
+}
+
+#define MGPT_INST_GEMM(BM, BN, WM, WN, AT, WT, EPI, OT)                                     \
+  template hipError_t launch_grouped_gemm<BM, BN, WM, WN, AT, WT, EPI, OT>(                 \
+      const AT*, const WT*, const float*, const float*, const float*, const int32_t*, int, int, \
+      int, int, int, OT*, int, int, hipStream_t);
+
+// Large-M tiles (prefill-shaped segments).
+MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, bf16_t, kEpiGateUp, bf16_t)
+MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, bf16_t, kEpiDown, bf16_t)
+MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, fp8_t, kEpiGateUp, bf16_t)
+MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, fp8_t, kEpiDown, bf16_t)
+// Small-M tiles (decode-shaped segments of a few rows per expert).
+MGPT_INST_GEMM(32, 256, 1, 4, bf16_t, bf16_t, kEpiGateUp, bf16_t)
+MGPT_INST_GEMM(32, 256, 1, 4, bf16_t, bf16_t, kEpiDown, bf16_t)
+MGPT_INST_GEMM(32, 256, 1, 4, bf16_t, fp8_t, kEpiGateUp, bf16_t)
+MGPT_INST_GEMM(32, 256, 1, 4, bf16_t, fp8_t, kEpiDown, bf16_t)
+// fp32 path.
+MGPT_INST_GEMM(64, 128, 2, 2, float, float, kEpiGateUp, float)
+MGPT_INST_GEMM(64, 128, 2, 2, float, float, kEpiDown, float)
+
+}  // namespace mgpt

@@ -1,0 +1,560 @@
+// moe_capi.hip -- the C ABI (include/mgpt_moe.h): handle, parameter packing,
+// workspace layout and the forward pipeline.
+//
+// Forward = 6 stream-ordered launches and no host synchronisation:
+//   router+top-k -> per-expert scan -> permute -> gate/up GEMM (+SwiGLU)
+//   -> down GEMM -> combine.
+// The reference's blocking device-to-host copy of the expert counts and the
+// host prefix sum (layers/MoELayer.cpp:61-80) are replaced by device-side
+// scans; the per-expert host loop of GEMM launches (:94-118) by one grouped
+// launch per projection.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/mgpt_moe.h"
+#include "common.hpp"
+
+namespace mgpt {
+// kernels (router.hip, dispatch.hip, gemm.hip, combine.hip, pack.hip)
+template <typename ActT>
+hipError_t launch_router(const ActT*, const float*, const float*, int, int, int, int, int32_t*,
+                         float*, int32_t*, hipStream_t);
+hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
+hipError_t launch_expert_scan(const int32_t*, int, int, int32_t*, int32_t*, hipStream_t);
+template <typename ActT>
+hipError_t launch_permute(const ActT*, const int32_t*, const int32_t*, const int32_t*, int, int,
+                          int, int, int32_t*, int32_t*, ActT*, hipStream_t);
+template <typename ActT>
+hipError_t launch_combine(const ActT*, const int32_t*, const float*, const int32_t*, int, int, int,
+                          ActT*, hipStream_t);
+template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
+hipError_t launch_grouped_gemm(const AT*, const WT*, const float*, const float*, const float*,
+                               const int32_t*, int, int, int, int, int, OutT*, int, int,
+                               hipStream_t);
+template <typename DT>
+hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
+hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
+hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
+}  // namespace mgpt
+
+using namespace mgpt;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                  \
+  do {                                                                                 \
+    hipError_t _e = (expr);                                                            \
+    if (_e != hipSuccess)                                                              \
+      return fail(MGPT_ERR_HIP, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(_e), \
+                  __FILE__, __LINE__);                                                 \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+constexpr int kRowPad = 128;   // rows of slack after activation buffers (GEMM tile overrun)
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+struct Layout {
+  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, xg, hbuf, obuf, total;
+};
+
+}  // namespace
+
+struct mgpt_moe {
+  int C, H, E, k, Hp, Cp;
+  int act, wdt;
+  int device;
+  float* wr_t = nullptr;   // [E][C]
+  float* br = nullptr;     // [E]
+  void* wgu = nullptr;     // [E][2Hp][C] of bf16 / fp8 / f32
+  void* wd = nullptr;      // [E][Cp][Hp]
+  float* sgu = nullptr;    // fp8 scales [E][2Hp] (packed-row order)
+  float* sd = nullptr;     // fp8 scales [E][Cp]
+  float* bg = nullptr;     // [E][Hp]
+  float* bu = nullptr;     // [E][Hp]
+  float* bd = nullptr;     // [E][Cp]
+  bool loaded = false;
+  // Profiling ring: forward i records its stage boundaries into slot
+  // i % kProfSlots; stage_times averages over the recorded slots.
+  static constexpr int kProfSlots = 64;
+  bool profiling = false;
+  hipEvent_t ev[kProfSlots][MGPT_MOE_NUM_STAGES + 1] = {};
+  int prof_count = 0;
+  hipEvent_t done = nullptr;
+  bool done_valid = false;
+  const int32_t* last_counts = nullptr;
+
+  size_t act_bytes() const { return act == MGPT_DTYPE_BF16 ? 2 : 4; }
+  size_t w_bytes() const { return wdt == MGPT_DTYPE_FP8_E4M3 ? 1 : (wdt == MGPT_DTYPE_BF16 ? 2 : 4); }
+  // h (SwiGLU output) is kept in the activation dtype.
+  Layout layout(int N) const {
+    Layout L{};
+    const size_t A = (size_t)N * k;
+    const size_t nb = ((size_t)N + kRouterTokens - 1) / kRouterTokens;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+      size_t o = off;
+      off = align_up(off + bytes, kAlign);
+      return o;
+    };
+    L.topk_idx = take(A * 4);
+    L.topk_p = take(A * 4);
+    L.slot_of = take(A * 4);
+    L.perm = take(A * 4);
+    L.hist = take(nb * E * 4);
+    L.base = take(nb * E * 4);
+    L.counts = take((size_t)E * 4);
+    L.xg = take((A + kRowPad) * C * act_bytes());
+    L.hbuf = take((A + kRowPad) * Hp * act_bytes());
+    L.obuf = take((A + kRowPad) * C * act_bytes());
+    L.total = off;
+    return L;
+  }
+};
+
+namespace {
+
+int check_config(const mgpt_moe_config* c) {
+  if (!c) return fail(MGPT_ERR_INVALID_ARGUMENT, "config is null");
+  const int H = c->hidden_dim == -1 ? 4 * c->embed_dim : c->hidden_dim;
+  if (c->embed_dim <= 0 || H <= 0 || c->num_experts <= 0 || c->top_k <= 0 ||
+      c->top_k > c->num_experts)
+    return fail(MGPT_ERR_INVALID_ARGUMENT,
+                "invalid shape: embed_dim=%d hidden_dim=%d num_experts=%d top_k=%d",
+                c->embed_dim, c->hidden_dim, c->num_experts, c->top_k);
+  if (c->embed_dim % 64 != 0)
+    return fail(MGPT_ERR_UNSUPPORTED, "embed_dim %d is not a multiple of 64", c->embed_dim);
+  if (c->num_experts > kMaxExperts)
+    return fail(MGPT_ERR_UNSUPPORTED, "num_experts %d > %d", c->num_experts, kMaxExperts);
+  if (c->top_k > kMaxTopK)
+    return fail(MGPT_ERR_UNSUPPORTED, "top_k %d > %d", c->top_k, kMaxTopK);
+  const bool f32 = c->act_dtype == MGPT_DTYPE_F32 && c->weight_dtype == MGPT_DTYPE_F32;
+  const bool bf = c->act_dtype == MGPT_DTYPE_BF16 &&
+                  (c->weight_dtype == MGPT_DTYPE_BF16 || c->weight_dtype == MGPT_DTYPE_FP8_E4M3);
+  if (!f32 && !bf)
+    return fail(MGPT_ERR_UNSUPPORTED, "unsupported dtype pair act=%d weight=%d", c->act_dtype,
+                c->weight_dtype);
+  return MGPT_OK;
+}
+
+void free_weights(mgpt_moe* h) {
+  void* ptrs[] = {h->wr_t, h->br, h->wgu, h->wd, h->sgu, h->sd, h->bg, h->bu, h->bd};
+  for (void* p : ptrs)
+    if (p) (void)hipFree(p);
+  h->wr_t = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
+  h->wgu = h->wd = nullptr;
+  h->loaded = false;
+}
+
+// Tile choice for the bf16 grouped GEMMs: decode-shaped (few rows per
+// expert) segments use 32-row tiles so the MFMAs are not mostly padding.
+bool small_m(const mgpt_moe* h, int N) { return (size_t)N * h->k < (size_t)64 * h->E; }
+
+}  // namespace
+
+extern "C" {
+
+const char* mgpt_moe_last_error(void) { return g_last_error.c_str(); }
+
+int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
+  if (!out) return fail(MGPT_ERR_INVALID_ARGUMENT, "out is null");
+  *out = nullptr;
+  int rc = check_config(cfg);
+  if (rc) return rc;
+  mgpt_moe* h = new (std::nothrow) mgpt_moe();
+  if (!h) return fail(MGPT_ERR_OUT_OF_MEMORY, "host allocation failed");
+  h->C = cfg->embed_dim;
+  h->H = cfg->hidden_dim == -1 ? 4 * cfg->embed_dim : cfg->hidden_dim;
+  h->E = cfg->num_experts;
+  h->k = cfg->top_k;
+  h->act = cfg->act_dtype;
+  h->wdt = cfg->weight_dtype;
+  h->Hp = round_up(h->H, 128);
+  h->Cp = round_up(h->C, 256);
+  hipError_t e = hipGetDevice(&h->device);
+  if (e == hipSuccess) {
+    for (auto& slot : h->ev)
+      for (auto& ev : slot)
+        if (e == hipSuccess) e = hipEventCreate(&ev);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&h->done, hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    mgpt_moe_destroy(h);
+    return fail(MGPT_ERR_HIP, "device setup failed: %s", hipGetErrorString(e));
+  }
+  *out = h;
+  return MGPT_OK;
+}
+
+int mgpt_moe_destroy(mgpt_moe* h) {
+  if (!h) return MGPT_OK;
+  free_weights(h);
+  for (auto& slot : h->ev)
+    for (auto& ev : slot)
+      if (ev) (void)hipEventDestroy(ev);
+  if (h->done) (void)hipEventDestroy(h->done);
+  delete h;
+  return MGPT_OK;
+}
+
+int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_params,
+                             int params_on_device, void* stream_ptr) {
+  if (!h || !params) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle or params");
+  if (num_params != 2 + 6 * h->E)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "expected %d parameters (2 + 6*E), got %d",
+                2 + 6 * h->E, num_params);
+  for (int i = 0; i < num_params; ++i)
+    if (!params[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "parameter %d is null", i);
+  hipStream_t st = (hipStream_t)stream_ptr;
+  HIP_TRY(hipSetDevice(h->device));
+  free_weights(h);
+  const int C = h->C, H = h->H, E = h->E, Hp = h->Hp, Cp = h->Cp;
+  const size_t wb = h->w_bytes();
+  const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
+  const bool bf = h->wdt == MGPT_DTYPE_BF16;
+  HIP_TRY(hipMalloc(&h->wr_t, sizeof(float) * E * C));
+  HIP_TRY(hipMalloc(&h->br, sizeof(float) * E));
+  HIP_TRY(hipMalloc(&h->wgu, wb * E * 2 * Hp * C));
+  HIP_TRY(hipMalloc(&h->wd, wb * E * Cp * Hp));
+  HIP_TRY(hipMalloc(&h->bg, sizeof(float) * E * Hp));
+  HIP_TRY(hipMalloc(&h->bu, sizeof(float) * E * Hp));
+  HIP_TRY(hipMalloc(&h->bd, sizeof(float) * E * Cp));
+  if (fp8) {
+    HIP_TRY(hipMalloc(&h->sgu, sizeof(float) * E * 2 * Hp));
+    HIP_TRY(hipMalloc(&h->sd, sizeof(float) * E * Cp));
+  }
+  HIP_TRY(hipMemsetAsync(h->wgu, 0, wb * E * 2 * Hp * C, st));
+  HIP_TRY(hipMemsetAsync(h->wd, 0, wb * E * Cp * Hp, st));
+
+  // Host parameters are staged through one device buffer of the largest size.
+  struct DevBuf {
+    float* p = nullptr;
+    ~DevBuf() {
+      if (p) (void)hipFree(p);
+    }
+  } stage_buf, tmp_buf;
+  const size_t max_elems = std::max<size_t>((size_t)C * std::max(H, E), (size_t)H * C);
+  HIP_TRY(hipMalloc(&stage_buf.p, sizeof(float) * max_elems));
+  if (fp8)
+    HIP_TRY(hipMalloc(&tmp_buf.p,
+                      sizeof(float) * std::max<size_t>((size_t)2 * Hp * C, (size_t)Cp * Hp)));
+  float* stage = stage_buf.p;
+  float* fp32tmp = tmp_buf.p;   // fp8: packed fp32 before quantisation
+  int rc = MGPT_OK;
+  auto src = [&](int i, size_t n) -> const float* {
+    if (params_on_device) return params[i];
+    hipError_t e = hipMemcpyAsync(stage, params[i], sizeof(float) * n, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) {
+      rc = fail(MGPT_ERR_HIP, "parameter %d upload failed: %s", i, hipGetErrorString(e));
+      return nullptr;
+    }
+    return stage;
+  };
+  auto pack = [&](const float* s, int Kin, int Nout, void* dst, int ldd, int mode, int off) {
+    hipError_t e;
+    if (bf)
+      e = launch_pack_transpose<bf16_t>(s, Kin, Nout, (bf16_t*)dst, ldd, mode, off, st);
+    else
+      e = launch_pack_transpose<float>(s, Kin, Nout, (float*)dst, ldd, mode, off, st);
+    if (e != hipSuccess) rc = fail(MGPT_ERR_HIP, "pack failed: %s", hipGetErrorString(e));
+  };
+  do {
+    const float* s = src(0, (size_t)C * E);
+    if (!s) break;
+    if (launch_pack_transpose<float>(s, C, E, h->wr_t, C, 0, 0, st) != hipSuccess) {
+      rc = fail(MGPT_ERR_HIP, "router pack failed");
+      break;
+    }
+    s = src(1, E);
+    if (!s) break;
+    HIP_TRY(hipMemcpyAsync(h->br, s, sizeof(float) * E, hipMemcpyDeviceToDevice, st));
+    for (int e = 0; e < E && rc == MGPT_OK; ++e) {
+      const int p = 2 + 6 * e;
+      const size_t gu_off = (size_t)e * 2 * Hp * C;
+      const size_t d_off = (size_t)e * Cp * Hp;
+      if (fp8) HIP_TRY(hipMemsetAsync(fp32tmp, 0, sizeof(float) * 2 * Hp * C, st));
+      for (int which = 0; which < 2 && rc == MGPT_OK; ++which) {   // gate, up
+        if (!(s = src(p + 2 * which, (size_t)C * H))) break;
+        if (fp8) {
+          if (launch_pack_transpose<float>(s, C, H, fp32tmp, C, 1, 32 * which, st) != hipSuccess)
+            rc = fail(MGPT_ERR_HIP, "pack failed");
+        } else {
+          pack(s, C, H, (char*)h->wgu + gu_off * h->w_bytes(), C, 1, 32 * which);
+        }
+        if (!(s = src(p + 2 * which + 1, H))) break;
+        HIP_TRY(launch_pad_row(s, H, (which ? h->bu : h->bg) + (size_t)e * Hp, Hp, st));
+      }
+      if (rc) break;
+      if (fp8)
+        HIP_TRY(launch_quantize_rows(fp32tmp, 2 * Hp, C, (uint8_t*)h->wgu + gu_off,
+                                     h->sgu + (size_t)e * 2 * Hp, st));
+      if (!(s = src(p + 4, (size_t)H * C))) break;
+      if (fp8) {
+        HIP_TRY(hipMemsetAsync(fp32tmp, 0, sizeof(float) * Cp * Hp, st));
+        if (launch_pack_transpose<float>(s, H, C, fp32tmp, Hp, 0, 0, st) != hipSuccess)
+          rc = fail(MGPT_ERR_HIP, "pack failed");
+        HIP_TRY(launch_quantize_rows(fp32tmp, Cp, Hp, (uint8_t*)h->wd + d_off,
+                                     h->sd + (size_t)e * Cp, st));
+      } else {
+        pack(s, H, C, (char*)h->wd + d_off * h->w_bytes(), Hp, 0, 0);
+      }
+      if (!(s = src(p + 5, C))) break;
+      HIP_TRY(launch_pad_row(s, C, h->bd + (size_t)e * Cp, Cp, st));
+      // Host sources are staged through one buffer: finish before reuse.
+      if (!params_on_device) HIP_TRY(hipStreamSynchronize(st));
+    }
+  } while (0);
+  hipError_t se = hipStreamSynchronize(st);
+  if (rc) {
+    free_weights(h);
+    return rc;
+  }
+  if (se != hipSuccess) {
+    free_weights(h);
+    return fail(MGPT_ERR_HIP, "parameter packing failed: %s", hipGetErrorString(se));
+  }
+  h->loaded = true;
+  return MGPT_OK;
+}
+
+int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes) {
+  if (!h || !bytes || num_tokens < 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle/bytes or negative num_tokens");
+  *bytes = h->layout(num_tokens).total;
+  return MGPT_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+template <typename ActT>
+int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream_t st) {
+  const Layout L = h->layout(N);
+  const int C = h->C, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
+  const int nb = (N + kRouterTokens - 1) / kRouterTokens;
+  const size_t A = (size_t)N * k;
+  int32_t* idx = (int32_t*)(ws + L.topk_idx);
+  float* topp = (float*)(ws + L.topk_p);
+  int32_t* slot_of = (int32_t*)(ws + L.slot_of);
+  int32_t* perm = (int32_t*)(ws + L.perm);
+  int32_t* hist = (int32_t*)(ws + L.hist);
+  int32_t* base = (int32_t*)(ws + L.base);
+  int32_t* counts = (int32_t*)(ws + L.counts);
+  ActT* xg = (ActT*)(ws + L.xg);
+  ActT* hb = (ActT*)(ws + L.hbuf);
+  ActT* ob = (ActT*)(ws + L.obuf);
+  const bool prof = h->profiling;
+  hipEvent_t* evs = h->ev[h->prof_count % mgpt_moe::kProfSlots];
+  auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
+
+  HIP_TRY(mark(0));
+  HIP_TRY(launch_router<ActT>(x, h->wr_t, h->br, N, C, E, k, idx, topp, hist, st));
+  HIP_TRY(mark(1));
+  HIP_TRY(launch_expert_scan(hist, nb, E, base, counts, st));
+  HIP_TRY(mark(2));
+  HIP_TRY(launch_permute<ActT>(x, idx, counts, base, N, C, E, k, perm, slot_of, xg, st));
+  HIP_TRY(mark(3));
+  if constexpr (sizeof(ActT) == 4) {
+    const int mt = (int)((A + 63) / 64) + E;
+    HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiGateUp, float>(
+        xg, (const float*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp,
+        mt, st)));
+    HIP_TRY(mark(4));
+    HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiDown, float>(
+        hb, (const float*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
+        st)));
+  } else {
+    const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
+    if (small_m(h, N)) {
+      const int mt = (int)((A + 31) / 32) + E;
+      if (fp8) {
+        HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
+            xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
+            Hp, mt, st)));
+        HIP_TRY(mark(4));
+        HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiDown, bf16_t>(
+            hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
+            st)));
+      } else {
+        HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiGateUp, bf16_t>(
+            xg, (const bf16_t*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp,
+            hb, Hp, mt, st)));
+        HIP_TRY(mark(4));
+        HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiDown, bf16_t>(
+            hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
+            mt, st)));
+      }
+    } else {
+      const int mt = (int)((A + 127) / 128) + E;
+      if (fp8) {
+        HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
+            xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
+            Hp, mt, st)));
+        HIP_TRY(mark(4));
+        HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, fp8_t, kEpiDown, bf16_t>(
+            hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
+            st)));
+      } else {
+        HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiGateUp, bf16_t>(
+            xg, (const bf16_t*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp,
+            hb, Hp, mt, st)));
+        HIP_TRY(mark(4));
+        HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiDown, bf16_t>(
+            hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
+            mt, st)));
+      }
+    }
+  }
+  HIP_TRY(mark(5));
+  HIP_TRY(launch_combine<ActT>(ob, idx, topp, slot_of, N, C, k, y, st));
+  HIP_TRY(mark(6));
+  if (prof) ++h->prof_count;
+  HIP_TRY(hipEventRecord(h->done, st));
+  h->done_valid = true;
+  h->last_counts = counts;
+  return MGPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
+  if (num_tokens < 0) return fail(MGPT_ERR_INVALID_ARGUMENT, "negative num_tokens");
+  if (num_tokens == 0) return MGPT_OK;
+  if (!x || !y || !workspace) return fail(MGPT_ERR_INVALID_ARGUMENT, "null x, y or workspace");
+  if (((uintptr_t)x | (uintptr_t)y) % 16 != 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "x and y must be 16-byte aligned");
+  if ((uintptr_t)workspace % kAlign != 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
+  const size_t need = h->layout(num_tokens).total;
+  if (workspace_bytes < need)
+    return fail(MGPT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu bytes < required %zu",
+                workspace_bytes, need);
+  const size_t xbytes = (size_t)num_tokens * h->C * h->act_bytes();
+  if ((const char*)x < (const char*)y + xbytes && (const char*)y < (const char*)x + xbytes)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "y must not overlap x");
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  if (h->act == MGPT_DTYPE_BF16)
+    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, num_tokens, (char*)workspace, st);
+  return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, st);
+}
+
+int mgpt_moe_get_routing(const mgpt_moe* h, int num_tokens, void* workspace,
+                         mgpt_moe_routing* out) {
+  if (!h || !workspace || !out || num_tokens < 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "null argument or negative num_tokens");
+  const Layout L = h->layout(num_tokens);
+  char* ws = (char*)workspace;
+  out->topk_idx = (int32_t*)(ws + L.topk_idx);
+  out->topk_p = (float*)(ws + L.topk_p);
+  out->counts = (int32_t*)(ws + L.counts);
+  out->perm = (int32_t*)(ws + L.perm);
+  out->slot_of = (int32_t*)(ws + L.slot_of);
+  return MGPT_OK;
+}
+
+int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts) {
+  if (!h || !host_counts || num_experts != h->E)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "null argument or num_experts != E");
+  if (!h->done_valid || !h->last_counts)
+    return fail(MGPT_ERR_NOT_READY, "no forward has been run");
+  HIP_TRY(hipEventSynchronize(h->done));
+  HIP_TRY(hipMemcpy(host_counts, h->last_counts, sizeof(int32_t) * h->E, hipMemcpyDeviceToHost));
+  return MGPT_OK;
+}
+
+int mgpt_moe_set_profiling(mgpt_moe* h, int enable) {
+  if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  h->profiling = enable != 0;
+  h->prof_count = 0;
+  return MGPT_OK;
+}
+
+int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n) {
+  if (!h || !ms || n < MGPT_MOE_NUM_STAGES)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "need room for %d stage times", MGPT_MOE_NUM_STAGES);
+  if (h->prof_count == 0) return fail(MGPT_ERR_NOT_READY, "no profiled forward has been run");
+  const int slots = std::min(h->prof_count, mgpt_moe::kProfSlots);
+  const int last = (h->prof_count - 1) % mgpt_moe::kProfSlots;
+  HIP_TRY(hipEventSynchronize(h->ev[last][MGPT_MOE_NUM_STAGES]));
+  for (int i = 0; i < MGPT_MOE_NUM_STAGES; ++i) {
+    double sum = 0.0;
+    for (int s = 0; s < slots; ++s) {
+      float t = 0.0f;
+      HIP_TRY(hipEventElapsedTime(&t, h->ev[s][i], h->ev[s][i + 1]));
+      sum += t;
+    }
+    ms[i] = (float)(sum / slots);
+  }
+  if (n > MGPT_MOE_NUM_STAGES) ms[MGPT_MOE_NUM_STAGES] = (float)slots;
+  return MGPT_OK;
+}
+
+int mgpt_moe_export_fp8(const mgpt_moe* h, int expert, int which, uint8_t* q_host,
+                        float* scale_host) {
+  if (!h || !q_host || !scale_host || expert < 0 || expert >= h->E || which < 0 || which > 2)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "bad arguments");
+  if (h->wdt != MGPT_DTYPE_FP8_E4M3) return fail(MGPT_ERR_INVALID_ARGUMENT, "not an fp8 handle");
+  if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
+  const int C = h->C, H = h->H, Hp = h->Hp, Cp = h->Cp;
+  if (which < 2) {
+    std::vector<uint8_t> q((size_t)2 * Hp * C);
+    std::vector<float> s((size_t)2 * Hp);
+    HIP_TRY(hipMemcpy(q.data(), (const uint8_t*)h->wgu + (size_t)expert * 2 * Hp * C, q.size(),
+                      hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(s.data(), h->sgu + (size_t)expert * 2 * Hp, sizeof(float) * s.size(),
+                      hipMemcpyDeviceToHost));
+    for (int n = 0; n < H; ++n) {
+      const int prow = (n / 32) * 64 + (n % 32) + 32 * which;
+      scale_host[n] = s[prow];
+      for (int c = 0; c < C; ++c) q_host[(size_t)c * H + n] = q[(size_t)prow * C + c];
+    }
+  } else {
+    std::vector<uint8_t> q((size_t)Cp * Hp);
+    std::vector<float> s((size_t)Cp);
+    HIP_TRY(hipMemcpy(q.data(), (const uint8_t*)h->wd + (size_t)expert * Cp * Hp, q.size(),
+                      hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(s.data(), h->sd + (size_t)expert * Cp, sizeof(float) * Cp,
+                      hipMemcpyDeviceToHost));
+    for (int c = 0; c < C; ++c) {
+      scale_host[c] = s[c];
+      for (int n = 0; n < H; ++n) q_host[(size_t)n * C + c] = q[(size_t)c * Hp + n];
+    }
+  }
+  return MGPT_OK;
+}
+
+int mgpt_moe_device_expf(const float* d_in, float* d_out, int n, void* stream) {
+  if (n < 0 || (n > 0 && (!d_in || !d_out)))
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "bad arguments");
+  HIP_TRY(launch_expf_probe(d_in, d_out, n, (hipStream_t)stream));
+  return MGPT_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,118 @@
+// pack.hip -- weight packing: reference layout fp32 -> GEMM layouts.
+//
+// The reference stores a Linear weight as W[in][out] row-major
+// (layers/LinearLayer.cpp:15-21).  The grouped GEMMs want each output
+// channel's K-run contiguous (B[n][k]), so the weights are transposed once
+// at load time through 64x64 LDS tiles (coalesced on both sides), converted
+// to the compute type, and, for gate/up, interleaved in 64-row groups
+// [32 gate rows | 32 up rows] of the same 32 hidden units.  fp8 weights are
+// first packed as fp32 and then quantised row by row: per output channel,
+// scale = amax / 448 (1 for an all-zero channel) and q = e4m3(w / scale),
+// round-to-nearest-even, saturating at +-448, zero encoded as +0.
+#include "common.hpp"
+
+namespace mgpt {
+namespace {
+
+__device__ __forceinline__ void put(float* p, float v) { *p = v; }
+__device__ __forceinline__ void put(bf16_t* p, float v) { *p = f32_to_bf16(v); }
+
+// dst row of source column n: gate/up interleave (mode 1) or identity (0).
+__device__ __forceinline__ int dst_row(int n, int mode, int off) {
+  return mode ? (n / 32) * 64 + (n % 32) + off : n;
+}
+
+// src [Kin][Nout] fp32 (leading dim Nout) -> dst[dst_row(n)][k] (leading dim ldd).
+template <typename DT>
+__global__ __launch_bounds__(256) void pack_transpose_kernel(const float* __restrict__ src, int Kin,
+                                                             int Nout, DT* __restrict__ dst,
+                                                             int ldd, int mode, int off) {
+  __shared__ float tile[64][65];
+  const int k0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  for (int r = ty; r < 64; r += 4) {
+    const int k = k0 + r, n = n0 + tx;
+    tile[r][tx] = (k < Kin && n < Nout) ? src[(size_t)k * Nout + n] : 0.0f;
+  }
+  __syncthreads();
+  for (int r = ty; r < 64; r += 4) {
+    const int n = n0 + r, k = k0 + tx;
+    if (n < Nout && k < Kin) put(dst + (size_t)dst_row(n, mode, off) * ldd + k, tile[tx][r]);
+  }
+}
+
+// OCP E4M3FN encode, nearest-even, saturating to 448.
+__device__ __forceinline__ uint8_t f32_to_e4m3(float v) {
+  const uint32_t sign = (__float_as_uint(v) >> 31) & 1u;
+  const float a = fabsf(v);
+  uint32_t code;
+  if (!(a < 448.0f)) {
+    code = 0x7E;
+  } else if (a < 0x1p-6f) {
+    code = (uint32_t)rintf(a * 512.0f);          // subnormal grid m * 2^-9 (m = 8 is 2^-6)
+  } else {
+    uint32_t b = __float_as_uint(a);
+    uint32_t q = b >> 20;                          // exponent + top 3 mantissa bits
+    const uint32_t rem = b & 0xFFFFFu;
+    q += (rem > 0x80000u) || (rem == 0x80000u && (q & 1u));
+    const int ex = (int)(q >> 3) - 127 + 7;
+    code = ((uint32_t)ex << 3) | (q & 7u);
+    if (code > 0x7E) code = 0x7E;
+  }
+  return (uint8_t)(code | ((sign && code) ? 0x80u : 0u));
+}
+
+// Row-wise quantisation of src [rows][K] fp32 -> q [rows][K] e4m3, scale[rows].
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ src, int K,
+                                                            uint8_t* __restrict__ q,
+                                                            float* __restrict__ scale) {
+  __shared__ float s_red[4];
+  const size_t r = blockIdx.x;
+  const float* row = src + r * K;
+  float m = 0.0f;
+  for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(row[k]));
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) m = fmaxf(m, __shfl_xor(m, d, kWave));
+  if (lane_id() == 0) s_red[threadIdx.x / kWave] = m;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+  const float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+  for (int k = threadIdx.x; k < K; k += 256) q[r * K + k] = f32_to_e4m3(row[k] / s);
+  if (threadIdx.x == 0) scale[r] = s;
+}
+
+// dst[i][0..n) = src[i][0..n), zero elsewhere up to ldd (bias padding).
+__global__ void pad_rows_kernel(const float* __restrict__ src, int n, float* __restrict__ dst,
+                                int ldd) {
+  const int i = threadIdx.x + blockIdx.x * blockDim.x;
+  if (i < ldd) dst[i] = i < n ? src[i] : 0.0f;
+}
+
+}  // namespace
+
+template <typename DT>
+hipError_t launch_pack_transpose(const float* src, int Kin, int Nout, DT* dst, int ldd, int mode,
+                                 int off, hipStream_t stream) {
+  dim3 grid((Nout + 63) / 64, (Kin + 63) / 64);
+  hipLaunchKernelGGL(pack_transpose_kernel<DT>, grid, dim3(256), 0, stream, src, Kin, Nout, dst,
+                     ldd, mode, off);
+  return hipGetLastError();
+}
+template hipError_t launch_pack_transpose<float>(const float*, int, int, float*, int, int, int,
+                                                 hipStream_t);
+template hipError_t launch_pack_transpose<bf16_t>(const float*, int, int, bf16_t*, int, int, int,
+                                                  hipStream_t);
+
+hipError_t launch_quantize_rows(const float* src, int rows, int K, uint8_t* q, float* scale,
+                                hipStream_t stream) {
+  hipLaunchKernelGGL(quantize_rows_kernel, dim3(rows), dim3(256), 0, stream, src, K, q, scale);
+  return hipGetLastError();
+}
+
+hipError_t launch_pad_row(const float* src, int n, float* dst, int ldd, hipStream_t stream) {
+  hipLaunchKernelGGL(pad_rows_kernel, dim3((ldd + 255) / 256), dim3(256), 0, stream, src, n, dst,
+                     ldd);
+  return hipGetLastError();
+}
+
+}  // namespace mgpt

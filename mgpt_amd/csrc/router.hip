@@ -1,0 +1,191 @@
+// router.hip -- fused router GEMM + clamped softmax + top-k + block histogram.
+//
+// Reference path (all bit-exact): router Linear layers/LinearLayer.cpp:23-28
+// -> Tensor::matmul_into utils/Tensor.cpp:1231-1249 -> matmul2d_raw :567-577
+// (each logit is a sequential fp32 sum over c of rounded products, then the
+// bias is added, :1499-1507 / :331-342); softmax utils/Tensor.cpp:850-883;
+// top-k utils/Tensor.cpp:1296-1334; histogram utils/Tensor.cpp:1336-1352.
+//
+// One block of 256 threads owns kRouterTokens = 64 tokens.  Phase 1 computes
+// the 64 x E logits: thread t owns the (token, expert) pairs t, t+256, ... and
+// walks c = 0..C-1 in order over LDS-staged 64-column chunks of x and W_r^T
+// (so every dot product has exactly the reference's rounding sequence; the
+// file is built with -ffp-contract=off, so nothing is fused).  MFMA cannot
+// be used here: its internal accumulation order differs.  Phase 2: per-token
+// max (strict '>' from element 0, as the reference, so NaN handling
+// matches), the E exponentials in parallel with glibc's expf algorithm, then
+// per token the sequential sum, the clamp and the insertion top-k in
+// registers.  Phase 3: block-local expert histogram (LDS atomics on ints;
+// counts are order-free), written expert-major as hist[e][block] for the
+// per-expert scan of dispatch.hip.
+#include "common.hpp"
+#include "glibc_expf.hpp"
+
+namespace mgpt {
+
+__constant__ uint64_t c_exp2_tab[32] = MGPT_EXP2_TABLE_INIT;
+
+namespace {
+
+constexpr int kRT = kRouterTokens;   // tokens per block
+constexpr int kCK = 64;              // columns per LDS chunk
+constexpr int kMaxPairsPerThread = kRT * kMaxExperts / 256;   // 16
+
+// Branch-free insertion of (v, e) into a descending top-K list, identical to
+// the reference's shifting loop: the element at j-1 moves to j exactly when
+// v > list[j-1]; a value not greater than list[K-1] changes nothing.
+template <int K>
+__device__ __forceinline__ void topk_insert(float (&ov)[K], int (&oi)[K], float v, int e) {
+#pragma unroll
+  for (int j = K - 1; j >= 0; --j) {
+    const bool from_prev = (j > 0) && (v > ov[j > 0 ? j - 1 : 0]);
+    const bool take_v = !from_prev && (v > ov[j]);
+    const float nv = from_prev ? ov[j > 0 ? j - 1 : 0] : (take_v ? v : ov[j]);
+    const int ni = from_prev ? oi[j > 0 ? j - 1 : 0] : (take_v ? e : oi[j]);
+    ov[j] = nv;
+    oi[j] = ni;
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void softmax_topk_token(const float* __restrict__ ex, float inv, int E,
+                                                   int32_t* __restrict__ idx_out,
+                                                   float* __restrict__ p_out, int* s_hist) {
+  float ov[K];
+  int oi[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) { ov[j] = -1e9f; oi[j] = -1; }
+  for (int v = 0; v < E; ++v) {
+    const float p = fminf(fmaxf(ex[v] * inv, 1e-7f), 1.0f);
+    topk_insert<K>(ov, oi, p, v);
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    idx_out[j] = oi[j];
+    p_out[j] = ov[j];
+    if (oi[j] >= 0) atomicAdd(&s_hist[oi[j]], 1);
+  }
+}
+
+template <typename ActT>
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr_t,   // [E][C]
+    const float* __restrict__ br, int N, int C, int E, int k,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
+    int32_t* __restrict__ hist, int num_blocks) {
+  __shared__ float s_x[kRT][kCK + 1];
+  __shared__ float s_w[kMaxExperts][kCK + 1];
+  __shared__ float s_l[kRT][kMaxExperts + 1];   // logits, then exponentials
+  __shared__ float s_m[kRT];
+  __shared__ int s_hist[kMaxExperts];
+
+  const int tid = threadIdx.x;
+  const int tok0 = blockIdx.x * kRT;
+  const int pairs = kRT * E;
+  if (tid < kMaxExperts) s_hist[tid] = 0;
+
+  float acc[kMaxPairsPerThread];
+#pragma unroll
+  for (int j = 0; j < kMaxPairsPerThread; ++j) acc[j] = 0.0f;
+
+  for (int c0 = 0; c0 < C; c0 += kCK) {
+    __syncthreads();
+    // Stage x[tok0 .. tok0+63][c0 .. c0+63] (rows past N read as 0) and
+    // W_r^T[0..E-1][c0 .. c0+63].
+    for (int q = tid; q < kRT * kCK; q += 256) {
+      const int r = q / kCK, c = q % kCK;
+      const int t = tok0 + r;
+      s_x[r][c] = (t < N) ? ActTraits<ActT>::load(x + (size_t)t * C + c0 + c) : 0.0f;
+    }
+    for (int q = tid; q < E * kCK; q += 256) {
+      const int e = q / kCK, c = q % kCK;
+      s_w[e][c] = wr_t[(size_t)e * C + c0 + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kMaxPairsPerThread; ++j) {
+      const int p = tid + 256 * j;
+      if (p < pairs) {
+        const int r = p / E, e = p % E;
+        float a = acc[j];
+        for (int c = 0; c < kCK; ++c) a = a + s_x[r][c] * s_w[e][c];
+        acc[j] = a;
+      }
+    }
+  }
+  // Logits = dot + bias (a separate rounded add, as the reference's bias pass).
+#pragma unroll
+  for (int j = 0; j < kMaxPairsPerThread; ++j) {
+    const int p = tid + 256 * j;
+    if (p < pairs) {
+      const int r = p / E, e = p % E;
+      s_l[r][e] = acc[j] + br[e];
+    }
+  }
+  __syncthreads();
+  // Row max with the reference's strict '>' scan starting from element 0.
+  if (tid < kRT) {
+    float m = s_l[tid][0];
+    for (int v = 1; v < E; ++v)
+      if (s_l[tid][v] > m) m = s_l[tid][v];
+    s_m[tid] = m;
+  }
+  __syncthreads();
+  for (int p = tid; p < pairs; p += 256) {
+    const int r = p / E, e = p % E;
+    s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], c_exp2_tab);
+  }
+  __syncthreads();
+  if (tid < kRT && tok0 + tid < N) {
+    const float* ex = s_l[tid];
+    float s = 0.0f;
+    for (int v = 0; v < E; ++v) s = s + ex[v];
+    const float inv = 1.0f / fmaxf(s, 1e-15f);
+    int32_t* io = topk_idx + (size_t)(tok0 + tid) * k;
+    float* po = topk_p + (size_t)(tok0 + tid) * k;
+    switch (k) {
+      case 1: softmax_topk_token<1>(ex, inv, E, io, po, s_hist); break;
+      case 2: softmax_topk_token<2>(ex, inv, E, io, po, s_hist); break;
+      case 3: softmax_topk_token<3>(ex, inv, E, io, po, s_hist); break;
+      case 4: softmax_topk_token<4>(ex, inv, E, io, po, s_hist); break;
+      case 5: softmax_topk_token<5>(ex, inv, E, io, po, s_hist); break;
+      case 6: softmax_topk_token<6>(ex, inv, E, io, po, s_hist); break;
+      case 7: softmax_topk_token<7>(ex, inv, E, io, po, s_hist); break;
+      default: softmax_topk_token<8>(ex, inv, E, io, po, s_hist); break;
+    }
+  }
+  __syncthreads();
+  if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
+}
+
+}  // namespace
+
+template <typename ActT>
+hipError_t launch_router(const ActT* x, const float* wr_t, const float* br, int N, int C,
+                         int E, int k, int32_t* topk_idx, float* topk_p, int32_t* hist,
+                         hipStream_t stream) {
+  const int nb = (N + kRT - 1) / kRT;
+  if (nb == 0) return hipSuccess;
+  hipLaunchKernelGGL(router_topk_kernel<ActT>, dim3(nb), dim3(256), 0, stream, x, wr_t, br, N,
+                     C, E, k, topk_idx, topk_p, hist, nb);
+  return hipGetLastError();
+}
+
+template hipError_t launch_router<float>(const float*, const float*, const float*, int, int, int,
+                                         int, int32_t*, float*, int32_t*, hipStream_t);
+template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*, int, int,
+                                          int, int, int32_t*, float*, int32_t*, hipStream_t);
+
+// Device expf over a buffer (tests compare it with the host's glibc expf).
+__global__ void expf_probe_kernel(const float* __restrict__ in, float* __restrict__ out, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = mgpt_expf::expf_glibc(in[i], c_exp2_tab);
+}
+
+hipError_t launch_expf_probe(const float* in, float* out, int n, hipStream_t stream) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(expf_probe_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, in, out, n);
+  return hipGetLastError();
+}
+
+}  // namespace mgpt

@@ -1,0 +1,143 @@
+// ref_driver.cpp -- drives the reference's own MoELayer CPU forward.
+//
+// TEST INFRASTRUCTURE ONLY.  Linked with the reference's unmodified sources
+// (compiled from /root/reference by oracle/Makefile into oracle/_ref/), it is
+// used to (1) write the golden fixtures that pin oracle/moe_oracle.c and the
+// HIP path (tests/golden/make_golden.py) and (2) time the reference CPU path
+// for bench.py's cpu_baseline leg.  Nothing in the product links it.
+//
+//   ref_driver run  <in.bin> <out.bin>
+//   ref_driver bench <N> <C> <H> <E> <k> <reps>
+//
+// in.bin : "MGPTMOE1", int32 N C H E k, then float32 x[N*C] and the 2+6E
+//          parameters in MoELayer::get_parameters() order
+//          (layers/MoELayer.cpp:225-236): W_r[C*E], b_r[E], then per expert
+//          W_g[C*H], b_g[H], W_u[C*H], b_u[H], W_d[H*C], b_d[C].
+// out.bin: "MGPTOUT1", int32 N C E k, float32 y[N*C], int32 idx[N*k],
+//          float32 topp[N*k], int32 counts[E], int32 offsets[E],
+//          int32 perm[N*k], float32 logits[N*E], float32 probs[N*E].
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <iostream>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+// The routing arrays the reference caches for its backward pass are private
+// members of MoELayer (layers/MoELayer.h:11-35); this driver reads them after
+// forward_into.  Standard headers are included first so only the reference
+// headers see the redefinition.
+#define private public
+#include "MoELayer.h"
+#undef private
+
+namespace {
+
+bool read_exact(FILE* f, void* dst, size_t bytes) {
+  return std::fread(dst, 1, bytes, f) == bytes;
+}
+
+int run(const char* in_path, const char* out_path) {
+  FILE* f = std::fopen(in_path, "rb");
+  if (!f) { std::perror(in_path); return 2; }
+  char magic[8];
+  int32_t dims[5];
+  if (!read_exact(f, magic, 8) || std::memcmp(magic, "MGPTMOE1", 8) != 0 ||
+      !read_exact(f, dims, sizeof(dims))) {
+    std::fprintf(stderr, "bad input header\n");
+    return 2;
+  }
+  const int N = dims[0], C = dims[1], H = dims[2], E = dims[3], k = dims[4];
+  Tensor x({1, N, C}, 0.0f, Device::CPU);
+  if (!read_exact(f, x.data.data(), sizeof(float) * (size_t)N * C)) return 3;
+  MoELayer layer(C, H, E, k);
+  std::vector<Tensor*> params = layer.get_parameters();
+  if ((int)params.size() != 2 + 6 * E) {
+    std::fprintf(stderr, "unexpected parameter count %zu\n", params.size());
+    return 4;
+  }
+  for (Tensor* p : params)
+    if (!read_exact(f, p->data.data(), sizeof(float) * p->size())) return 3;
+  std::fclose(f);
+
+  Tensor y;
+  layer.forward_into(x, y);
+
+  const size_t A = (size_t)N * k;
+  std::vector<int32_t> idx(A), perm(A), counts(E), offsets(E);
+  for (size_t i = 0; i < A; ++i) idx[i] = (int32_t)layer.cached_top_indices.data[i];
+  for (size_t i = 0; i < A; ++i) perm[i] = (int32_t)layer.cached_sorted_token_ids.data[i];
+  for (int e = 0; e < E; ++e) counts[e] = (int32_t)layer.cached_cpu_counts[e];
+  for (int e = 0; e < E; ++e) offsets[e] = (int32_t)layer.cached_cpu_offsets[e];
+
+  FILE* o = std::fopen(out_path, "wb");
+  if (!o) { std::perror(out_path); return 2; }
+  int32_t odims[4] = {N, C, E, k};
+  std::fwrite("MGPTOUT1", 1, 8, o);
+  std::fwrite(odims, sizeof(int32_t), 4, o);
+  std::fwrite(y.data.data(), sizeof(float), (size_t)N * C, o);
+  std::fwrite(idx.data(), sizeof(int32_t), A, o);
+  std::fwrite(layer.cached_top_probs.data.data(), sizeof(float), A, o);
+  std::fwrite(counts.data(), sizeof(int32_t), E, o);
+  std::fwrite(offsets.data(), sizeof(int32_t), E, o);
+  std::fwrite(perm.data(), sizeof(int32_t), A, o);
+  std::fwrite(layer.cached_router_logits.data.data(), sizeof(float), (size_t)N * E, o);
+  std::fwrite(layer.cached_router_probs.data.data(), sizeof(float), (size_t)N * E, o);
+  std::fclose(o);
+  return 0;
+}
+
+// Times MoELayer::forward_into on one fresh layer (its CPU caches are sized
+// on first use and never resized, layers/MoELayer.cpp:42-50): 1 warmup, then
+// `reps` timed runs; prints one JSON line with every run and the median.
+int bench(int N, int C, int H, int E, int k, int reps) {
+  std::mt19937 gen(20261201u);
+  std::normal_distribution<float> nd(0.0f, 1.0f);
+  Tensor x({1, N, C}, 0.0f, Device::CPU);
+  for (auto& v : x.data) v = nd(gen);
+  for (int i = 0; i < N; ++i) {  // RMSNorm-like scaling to unit RMS
+    double ss = 0;
+    for (int c = 0; c < C; ++c) ss += (double)x.data[(size_t)i * C + c] * x.data[(size_t)i * C + c];
+    float r = (float)(1.0 / std::sqrt(ss / C + 1e-5));
+    for (int c = 0; c < C; ++c) x.data[(size_t)i * C + c] *= r;
+  }
+  MoELayer layer(C, H, E, k);
+  for (Tensor* p : layer.get_parameters())
+    for (auto& v : p->data) v = 0.02f * nd(gen);
+  Tensor y;
+  layer.forward_into(x, y);  // warmup
+  std::vector<double> t;
+  for (int r = 0; r < reps; ++r) {
+    auto t0 = std::chrono::steady_clock::now();
+    layer.forward_into(x, y);
+    auto t1 = std::chrono::steady_clock::now();
+    t.push_back(std::chrono::duration<double>(t1 - t0).count());
+  }
+  std::vector<double> s = t;
+  std::sort(s.begin(), s.end());
+  double med = s[s.size() / 2];
+  std::printf("{\"N\": %d, \"C\": %d, \"H\": %d, \"E\": %d, \"k\": %d, \"reps\": %d, "
+              "\"median_s\": %.6f, \"runs_s\": [", N, C, H, E, k, reps, med);
+  for (size_t i = 0; i < t.size(); ++i) std::printf("%s%.6f", i ? ", " : "", t[i]);
+  std::printf("], \"tokens_per_s\": %.3f, \"threads\": 1}\n", N / med);
+  return 0;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
+  if (argc == 8 && std::string(argv[1]) == "bench")
+    return bench(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]),
+                 std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]));
+  std::fprintf(stderr, "usage: ref_driver run <in> <out> | bench N C H E k reps\n");
+  return 1;
+}

@@ -1,0 +1,92 @@
+"""Input cases shared by the golden-fixture generator and the tests.
+
+Each case is rebuilt from (config, seed, tweaks) with the seeded generator in
+mgpt_amd.workload, so a committed fixture holds only the reference's
+outputs.  The unit cases cover the edge cases of the routing rules in
+/root/reference/src/main/utils/Tensor.cpp: exact ties (:1296-1334, lower
+expert id first), clamped probabilities (:879), NaN/Inf inputs (F16: every
+p = 1e-7 so experts 0..k-1 win), ragged token counts, k = 1 and k = E, one
+expert, and nonzero biases everywhere (the benchmark configurations use zero
+expert biases, which would hide a dropped bias term).
+"""
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+
+from mgpt_amd import workload as wl
+
+SEED = 20261201
+
+
+@dataclasses.dataclass(frozen=True)
+class Case:
+    name: str
+    cfg: wl.MoEConfig
+    bias_std: float = 0.0
+    tweak: str = ""           # "ones", "tie_router", "nan_rows", "wide_router"
+    gpu: bool = True          # shape supported by the HIP path (C % 64 == 0)
+    full_arrays: bool = True  # store full routing arrays (small cases)
+
+
+def _c(name, N, C, E, k, H, act="f32", weights=None, rb="zero"):
+    return wl.MoEConfig(name, N, C, E, k, H, act, weights or act, rb)
+
+
+UNIT_CASES = [
+    # the shape of the reference's own MoE test (tests/networkTest/moeTests.cpp:6-19):
+    # B=2, T=4, C=16, E=4, k=2, hidden 4C, input all ones -> every token ties
+    Case("moetests_shape", _c("moetests_shape", 8, 16, 4, 2, 64), 0.0, "ones", gpu=False),
+    Case("ties_ones", _c("ties_ones", 16, 64, 4, 2, 64), 0.1, "tie_router"),
+    Case("small_f32", _c("small_f32", 64, 64, 4, 2, 96, rb="normal"), 0.1),
+    Case("ragged_k3", _c("ragged_k3", 37, 64, 6, 3, 80, rb="normal"), 0.05),
+    Case("k8_bf16", _c("k8_bf16", 50, 128, 16, 8, 64, "bf16", rb="zipf"), 0.02),
+    Case("nan_rows", _c("nan_rows", 16, 64, 8, 2, 64), 0.05, "nan_rows"),
+    Case("clamp_ties", _c("clamp_ties", 32, 64, 8, 3, 64), 0.05, "wide_router"),
+    Case("single_expert", _c("single_expert", 20, 64, 1, 1, 64), 0.05),
+    Case("k_equals_e", _c("k_equals_e", 24, 64, 4, 4, 64, rb="normal"), 0.05),
+    Case("bf16_e64_k6", _c("bf16_e64_k6", 96, 128, 64, 6, 128, "bf16", rb="zipf"), 0.02),
+    Case("fp8_small", _c("fp8_small", 48, 128, 8, 4, 192, "bf16", "fp8", rb="normal"), 0.02),
+]
+
+CONFIG_CASES = [
+    Case("cfg1", wl.CONFIGS["cfg1"], full_arrays=True),
+    Case("cfg2", wl.CONFIGS["cfg2"], full_arrays=False),
+    Case("cfg3", wl.CONFIGS["cfg3"], full_arrays=False),
+    Case("cfg4", wl.CONFIGS["cfg4"], full_arrays=False),
+    Case("cfg5", wl.CONFIGS["cfg5"], full_arrays=True),
+]
+
+ALL_CASES = {c.name: c for c in UNIT_CASES + CONFIG_CASES}
+
+
+def build_inputs(case: Case) -> wl.MoEInputs:
+    inp = wl.make_inputs(case.cfg, SEED, bias_std=case.bias_std)
+    if case.tweak == "ones":
+        inp.x[:] = 1.0
+    elif case.tweak == "tie_router":
+        # identical router columns: every logit of a token ties exactly
+        inp.Wr[:] = inp.Wr[:, :1]
+        inp.br[:] = 0.0
+    elif case.tweak == "nan_rows":
+        inp.x[3, :] = np.nan
+        inp.x[5, 2] = np.nan
+        inp.x[9, 0] = np.inf
+        inp.x[11, 7] = -np.inf
+    elif case.tweak == "wide_router":
+        # large logit gaps: most probabilities clamp to exactly 1e-7 (and the
+        # winner to 1), so lower-index tie-breaks among the losers decide
+        # the second and third choices
+        inp.Wr[:] = inp.Wr * np.float32(100.0)
+    if case.cfg.act == "bf16":
+        inp.x[:] = wl.bf16_round(inp.x)
+        inp.Wr[:] = wl.bf16_round(inp.Wr)
+    return inp
+
+
+def sample_rows(N: int, n: int = 32) -> np.ndarray:
+    """Deterministic sample of token rows whose outputs fixtures store."""
+    if N <= n:
+        return np.arange(N, dtype=np.int32)
+    return np.unique(np.linspace(0, N - 1, n).round().astype(np.int32))

@@ -1,0 +1,135 @@
+"""ctypes binding of the CPU oracle (oracle/libmoe_oracle.so).
+
+Test infrastructure: the checker the HIP path is compared with.  Only
+tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+LIB_PATH = os.path.join(ORACLE_DIR, "libmoe_oracle.so")
+REF_DRIVER = os.path.join(ORACLE_DIR, "_ref", "ref_driver")
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            subprocess.run(["make", "-C", ORACLE_DIR, "libmoe_oracle.so"], check=True,
+                           capture_output=True)
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        L.oracle_expf.argtypes = [ctypes.c_float]
+        L.oracle_expf.restype = ctypes.c_float
+        L.oracle_expf_array.argtypes = [vp, vp, ctypes.c_int64]
+        L.oracle_router_logits.argtypes = [i, i, i, vp, vp, vp, vp]
+        L.oracle_softmax.argtypes = [i, i, vp, vp]
+        L.oracle_topk.argtypes = [i, i, i, vp, vp, vp]
+        L.oracle_dispatch.argtypes = [i, i, i, vp, vp, vp, vp]
+        L.oracle_moe_forward.argtypes = [i] * 5 + [vp] * 17
+        L.oracle_moe_forward.restype = i
+        L.oracle_moe_tokens.argtypes = [i] * 5 + [vp] * 11
+        L.oracle_moe_tokens.restype = i
+        L.oracle_rmsnorm.argtypes = [i, i, ctypes.c_float, vp, vp]
+        _LIB = L
+    return _LIB
+
+
+def _p(a):
+    return a.ctypes.data if a is not None else None
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def expf(x: np.ndarray) -> np.ndarray:
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().oracle_expf_array(x.ctypes.data, out.ctypes.data, x.size)
+    return out
+
+
+def router_logits(x, Wr, br):
+    x, Wr, br = _f32(x), _f32(Wr), _f32(br)
+    N, C = x.shape
+    E = Wr.shape[1]
+    out = np.empty((N, E), np.float32)
+    lib().oracle_router_logits(N, C, E, _p(x), _p(Wr), _p(br), _p(out))
+    return out
+
+
+def softmax(logits):
+    logits = _f32(logits)
+    out = np.empty_like(logits)
+    lib().oracle_softmax(logits.shape[0], logits.shape[1], _p(logits), _p(out))
+    return out
+
+
+def topk(probs, k):
+    probs = _f32(probs)
+    N, E = probs.shape
+    idx = np.empty((N, k), np.int32)
+    p = np.empty((N, k), np.float32)
+    lib().oracle_topk(N, E, k, _p(probs), _p(idx), _p(p))
+    return idx, p
+
+
+def dispatch(idx, E):
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    N, k = idx.shape
+    counts = np.empty(E, np.int32)
+    offsets = np.empty(E, np.int32)
+    perm = np.empty(N * k, np.int32)
+    lib().oracle_dispatch(N, E, k, _p(idx), _p(counts), _p(offsets), _p(perm))
+    return counts, offsets, perm
+
+
+def forward(inp, with_y: bool = True) -> dict:
+    """Full reference-order forward of a workload.MoEInputs."""
+    cfg = inp.cfg
+    N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
+    arrs = [_f32(a) for a in (inp.x, inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu,
+                              inp.Wd, inp.bd)]
+    out = {
+        "y": np.empty((N, C), np.float32) if with_y else None,
+        "logits": np.empty((N, E), np.float32), "probs": np.empty((N, E), np.float32),
+        "idx": np.empty((N, k), np.int32), "topp": np.empty((N, k), np.float32),
+        "counts": np.empty(E, np.int32), "offsets": np.empty(E, np.int32),
+        "perm": np.empty(N * k, np.int32),
+    }
+    rc = lib().oracle_moe_forward(N, C, H, E, k, *[_p(a) for a in arrs],
+                                  _p(out["y"]), _p(out["logits"]), _p(out["probs"]),
+                                  _p(out["idx"]), _p(out["topp"]), _p(out["counts"]),
+                                  _p(out["offsets"]), _p(out["perm"]))
+    assert rc == 0
+    return out
+
+
+def tokens(inp, idx, topp, rows) -> np.ndarray:
+    """Output rows of the given tokens under the given routing."""
+    cfg = inp.cfg
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    idx = np.ascontiguousarray(idx, dtype=np.int32)
+    topp = _f32(topp)
+    arrs = [_f32(a) for a in (inp.x, inp.Wg, inp.bg, inp.Wu, inp.bu, inp.Wd, inp.bd)]
+    y = np.empty((rows.size, cfg.C), np.float32)
+    rc = lib().oracle_moe_tokens(cfg.C, cfg.H, cfg.E, cfg.k, rows.size, _p(rows), _p(arrs[0]),
+                                 _p(idx), _p(topp), *[_p(a) for a in arrs[1:]], _p(y))
+    assert rc == 0
+    return y
+
+
+def rmsnorm(x, eps=1e-5):
+    x = _f32(x)
+    out = np.empty_like(x)
+    lib().oracle_rmsnorm(x.shape[0], x.shape[1], eps, _p(x), _p(out))
+    return out
