@@ -127,7 +127,7 @@ def test_device_expf_matches_host_expf():
     # every 61st float in [-104, -0] plus the edges of the special-case paths
     lo = np.float32(-104.0).view(np.uint32)
     u = np.arange(np.uint32(0x80000000), lo + np.uint32(1), 61, dtype=np.uint64).astype(np.uint32)
-    special = np.array([0.0, -0.0, -1e-45, -0x1.9fe368p6, -0x1.9fe36ap6, -88.0, -87.99,
+    special = np.array([0.0, -0.0, -1e-45, -float.fromhex("0x1.9fe368p6"), -float.fromhex("0x1.9fe36ap6"), -88.0, -87.99,
                         -103.97, -104.0, -150.0, -1e30, -np.inf, np.nan], np.float32)
     x = np.concatenate([u.view(np.float32), special])
     xd = torch.from_numpy(x).cuda()
