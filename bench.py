@@ -67,6 +67,9 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=1024)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed run, copy this many MiB device-to-device 3 times "
+                         "(a known-size kernel for calibrating FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
@@ -163,6 +166,14 @@ def main() -> int:
         },
         "wall_s_timed": round(wall, 3),
     }
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):                  # an elementwise kernel, not a DMA-engine copy
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        result["calib_copy_mib"] = args.calib_copy_mib
     if not args.no_cpu_baseline:
         print("cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_tokens, N), args.cpu_reps)

@@ -19,8 +19,8 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "lib")
 OBJ = os.path.join(HERE, "_build")
 
-HIP_SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "combine.hip", "pack.hip",
-               "moe_capi.hip"]
+HIP_SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_dma.hip", "combine.hip",
+               "pack.hip", "moe_capi.hip"]
 ARCH = os.environ.get("MGPT_OFFLOAD_ARCH", "gfx950")
 
 # -ffp-contract=off: the router must round every product and sum separately

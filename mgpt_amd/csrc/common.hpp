@@ -18,11 +18,23 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
+constexpr int kNumXcd = 8;        // MI355X: 8 accelerator complex dies, one L2 each
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
-// Tokens per router / permute block: one block owns the flat assignment
-// range [b*kRouterTokens*k, (b+1)*kRouterTokens*k).
+// Tokens per router / permute block (at most kRouterTokens): block b owns
+// tokens [b*TB, (b+1)*TB) and so the flat assignment ids
+// [b*TB*k, (b+1)*TB*k).  The router's register tiling fixes TB per E.
 constexpr int kRouterTokens = 64;
+__host__ __device__ inline int router_tokens_per_block(int E) {
+  switch (E) {
+    case 64: return 16;   // 2 tokens x 2 experts per thread
+    case 32: return 32;   // 2 x 2
+    case 16: return 32;   // 2 x 1
+    case 8: return 64;    // 2 x 1
+    case 4: return 64;    // 1 x 1
+    default: return kRouterTokens;   // generic kernel
+  }
+}
 
 // Grouped-GEMM epilogues (gemm.hip).
 enum Epilogue { kEpiGateUp = 0, kEpiDown = 1 };

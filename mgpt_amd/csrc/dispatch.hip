@@ -52,7 +52,7 @@ struct alignas(16) V16 {
   uint32_t w[4];
 };
 
-// One block per router block (kRouterTokens tokens = kRouterTokens*k flat ids).
+// One block per router block (TB tokens = TB*k flat ids).
 template <typename ActT>
 __global__ __launch_bounds__(256) void permute_kernel(
     const ActT* __restrict__ x, const int32_t* __restrict__ topk_idx,
@@ -64,8 +64,9 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int s_slot[kRouterTokens * kMaxTopK];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
-  const int tok0 = b * kRouterTokens;
-  const int ntok = min(kRouterTokens, N - tok0);
+  const int TB = router_tokens_per_block(E);
+  const int tok0 = b * TB;
+  const int ntok = min(TB, N - tok0);
   const int nflat = ntok * k;
   const size_t flat0 = (size_t)tok0 * k;
 
@@ -140,7 +141,8 @@ template <typename ActT>
 hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t* counts,
                           const int32_t* base, int N, int C, int E, int k, int32_t* perm,
                           int32_t* slot_of, ActT* xg, hipStream_t stream) {
-  const int nb = (N + kRouterTokens - 1) / kRouterTokens;
+  const int TB = router_tokens_per_block(E);
+  const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
   hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb), dim3(256), 0, stream, x, topk_idx, counts,
                      base, nb, N, C, E, k, perm, slot_of, xg);

@@ -73,10 +73,20 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
   __shared__ __attribute__((aligned(16))) AT sA[2][BM][LDK];
   __shared__ __attribute__((aligned(16))) AT sB[2][BN][LDK];
 
+  // XCD-aware order: the hardware deals consecutive workgroups round-robin
+  // to the 8 XCDs (each with its own L2); remap so each XCD receives a
+  // contiguous run of tiles, n fastest, so concurrently resident blocks on
+  // one XCD share their A (activation) tile and neighbouring B tiles.
+  const int nbx = gridDim.x;
+  const int total = nbx * gridDim.y;
+  int bid = blockIdx.y * nbx + blockIdx.x;
+  const int per = total / kNumXcd;
+  if (bid < per * kNumXcd) bid = (bid % kNumXcd) * per + bid / kNumXcd;
+  const int mtile = bid / nbx;
   TileInfo ti;
-  if (!find_tile<BM>(counts, E, blockIdx.y, &ti)) return;
+  if (!find_tile<BM>(counts, E, mtile, &ti)) return;
   const int e = ti.expert;
-  const int n0 = blockIdx.x * BN;
+  const int n0 = (bid % nbx) * BN;
   const int tid = threadIdx.x;
   const int w = tid / kWave, lane = lane_id();
   const int wm = w / WN, wn = w % WN;
@@ -147,22 +157,30 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
     const int cur = kt & 1;
     if (kt + 1 < KT) gload(kt + 1);
     if constexpr (!kF32) {
-#pragma unroll
-      for (int ks = 0; ks < BK / 16; ++ks) {
-        bf16x8 af[TM], bfr[TN];
+      // Fragments of k-step ks+1 are read from LDS while the MFMAs of
+      // k-step ks run.
+      constexpr int KS = BK / 16;
+      bf16x8 af[2][TM], bfr[2][TN];
+      auto lds_frags = [&](int ks, bf16x8 (&a)[TM], bf16x8 (&b)[TN]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < TM; ++i)
-          af[i] = *reinterpret_cast<const bf16x8*>(
+          a[i] = *reinterpret_cast<const bf16x8*>(
               &sA[cur][wm * WTM + i * 32 + lrow][ks * 16 + lhalf * 8]);
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          bfr[j] = *reinterpret_cast<const bf16x8*>(
+          b[j] = *reinterpret_cast<const bf16x8*>(
               &sB[cur][wn * WTN + j * 32 + lrow][ks * 16 + lhalf * 8]);
+      };
+      lds_frags(0, af[0], bfr[0]);
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + 1 < KS) lds_frags(ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
           for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][i], bfr[ks & 1][j],
+                                                                acc[i][j], 0, 0, 0);
       }
     } else {
 #pragma unroll

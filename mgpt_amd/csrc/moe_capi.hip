@@ -13,6 +13,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -42,6 +43,10 @@ template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
+template <int EPI>
+hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
+                           const int32_t*, int, int, int, int, int, bf16_t*, int, int,
+                           hipStream_t);
 }  // namespace mgpt
 
 using namespace mgpt;
@@ -69,7 +74,7 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr size_t kAlign = 256;
-constexpr int kRowPad = 128;   // rows of slack after activation buffers (GEMM tile overrun)
+constexpr int kRowPad = 256;   // rows of slack after activation buffers (GEMM tile overrun)
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
@@ -84,6 +89,7 @@ struct mgpt_moe {
   int C, H, E, k, Hp, Cp;
   int act, wdt;
   int device;
+  int gemm_tile = 256;     // block tile of the large-M bf16 GEMMs (256 or 128)
   float* wr_t = nullptr;   // [E][C]
   float* br = nullptr;     // [E]
   void* wgu = nullptr;     // [E][2Hp][C] of bf16 / fp8 / f32
@@ -110,7 +116,8 @@ struct mgpt_moe {
   Layout layout(int N) const {
     Layout L{};
     const size_t A = (size_t)N * k;
-    const size_t nb = ((size_t)N + kRouterTokens - 1) / kRouterTokens;
+    const size_t TB = router_tokens_per_block(E);
+    const size_t nb = ((size_t)N + TB - 1) / TB;
     size_t off = 0;
     auto take = [&](size_t bytes) {
       size_t o = off;
@@ -191,6 +198,8 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
   h->wdt = cfg->weight_dtype;
   h->Hp = round_up(h->H, 128);
   h->Cp = round_up(h->C, 256);
+  // Tuning override for the large-M tile (default 256x256).
+  if (const char* t = std::getenv("MGPT_MOE_GEMM_TILE")) h->gemm_tile = std::atoi(t) == 128 ? 128 : 256;
   hipError_t e = hipGetDevice(&h->device);
   if (e == hipSuccess) {
     for (auto& slot : h->ev)
@@ -352,7 +361,7 @@ template <typename ActT>
 int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream_t st) {
   const Layout L = h->layout(N);
   const int C = h->C, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
-  const int nb = (N + kRouterTokens - 1) / kRouterTokens;
+  const int nb = (N + router_tokens_per_block(E) - 1) / router_tokens_per_block(E);
   const size_t A = (size_t)N * k;
   int32_t* idx = (int32_t*)(ws + L.topk_idx);
   float* topp = (float*)(ws + L.topk_p);
@@ -405,6 +414,14 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
             mt, st)));
       }
+    } else if (h->gemm_tile == 256 && !fp8) {
+      // bf16 weights, prefill-shaped segments: 256x256 direct-to-LDS kernel.
+      const int mt = (int)((A + 255) / 256) + E;
+      HIP_TRY(launch_gemm_dma<kEpiGateUp>(xg, (const bf16_t*)h->wgu, h->bg, h->bu, counts, E, C,
+                                          2 * Hp, 2 * Hp, Hp, hb, Hp, mt, st));
+      HIP_TRY(mark(4));
+      HIP_TRY(launch_gemm_dma<kEpiDown>(hb, (const bf16_t*)h->wd, h->bd, nullptr, counts, E, Hp,
+                                        Cp, C, Cp, ob, C, mt, st));
     } else {
       const int mt = (int)((A + 127) / 128) + E;
       if (fp8) {

@@ -158,16 +158,143 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
 }
 
+// Register-tiled variant for E in {4, 8, 16, 32, 64}: thread (tg, eg) owns
+// RT tokens x RE experts (experts fastest across lanes, so the lanes of a
+// wave that share a token read the same LDS address), walks c in order and
+// reads 4 consecutive c of x and W_r^T as one float4 per operand.  Blocks
+// hold TB = 256 / (E / RE) * RT tokens (16..64), so the grid has enough
+// workgroups to occupy every CU.  Same rounding sequence per logit as the
+// generic kernel.
+template <typename ActT, int RT, int RE>
+__global__ __launch_bounds__(256) void router_topk_tiled_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr_t, const float* __restrict__ br,
+    int N, int C, int E, int k, int TB, int32_t* __restrict__ topk_idx,
+    float* __restrict__ topk_p, int32_t* __restrict__ hist, int num_blocks) {
+  constexpr int LD = kCK + 4;          // float4-aligned rows
+  __shared__ __attribute__((aligned(16))) float s_x[kRT][LD];
+  __shared__ __attribute__((aligned(16))) float s_w[kMaxExperts][LD];
+  __shared__ float s_l[kRT][kMaxExperts + 1];
+  __shared__ float s_m[kRT];
+  __shared__ int s_hist[kMaxExperts];
+
+  const int tid = threadIdx.x;
+  const int tok0 = blockIdx.x * TB;
+  const int EG = E / RE;               // expert groups
+  const int eg = tid % EG, tg = tid / EG;
+  if (tid < kMaxExperts) s_hist[tid] = 0;
+
+  float acc[RT][RE];
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < RE; ++j) acc[i][j] = 0.0f;
+
+  for (int c0 = 0; c0 < C; c0 += kCK) {
+    __syncthreads();
+    for (int q = tid; q < TB * kCK; q += 256) {
+      const int r = q / kCK, c = q % kCK;
+      const int t = tok0 + r;
+      s_x[r][c] = (t < N) ? ActTraits<ActT>::load(x + (size_t)t * C + c0 + c) : 0.0f;
+    }
+    for (int q = tid; q < E * kCK; q += 256) {
+      const int e = q / kCK, c = q % kCK;
+      s_w[e][c] = wr_t[(size_t)e * C + c0 + c];
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int c = 0; c < kCK; c += 4) {
+      float4 xv[RT], wv[RE];
+#pragma unroll
+      for (int i = 0; i < RT; ++i) xv[i] = *reinterpret_cast<const float4*>(&s_x[tg * RT + i][c]);
+#pragma unroll
+      for (int j = 0; j < RE; ++j) wv[j] = *reinterpret_cast<const float4*>(&s_w[eg * RE + j][c]);
+#pragma unroll
+      for (int i = 0; i < RT; ++i)
+#pragma unroll
+        for (int j = 0; j < RE; ++j) {
+          float a = acc[i][j];
+          a = a + xv[i].x * wv[j].x;
+          a = a + xv[i].y * wv[j].y;
+          a = a + xv[i].z * wv[j].z;
+          a = a + xv[i].w * wv[j].w;
+          acc[i][j] = a;
+        }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RT; ++i)
+#pragma unroll
+    for (int j = 0; j < RE; ++j) {
+      const int e = eg * RE + j;
+      s_l[tg * RT + i][e] = acc[i][j] + br[e];
+    }
+  __syncthreads();
+  if (tid < TB) {
+    float m = s_l[tid][0];
+    for (int v = 1; v < E; ++v)
+      if (s_l[tid][v] > m) m = s_l[tid][v];
+    s_m[tid] = m;
+  }
+  __syncthreads();
+  for (int p = tid; p < TB * E; p += 256) {
+    const int r = p / E, e = p % E;
+    s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], c_exp2_tab);
+  }
+  __syncthreads();
+  if (tid < TB && tok0 + tid < N) {
+    const float* ex = s_l[tid];
+    float sum = 0.0f;
+    for (int v = 0; v < E; ++v) sum = sum + ex[v];
+    const float inv = 1.0f / fmaxf(sum, 1e-15f);
+    int32_t* io = topk_idx + (size_t)(tok0 + tid) * k;
+    float* po = topk_p + (size_t)(tok0 + tid) * k;
+    switch (k) {
+      case 1: softmax_topk_token<1>(ex, inv, E, io, po, s_hist); break;
+      case 2: softmax_topk_token<2>(ex, inv, E, io, po, s_hist); break;
+      case 3: softmax_topk_token<3>(ex, inv, E, io, po, s_hist); break;
+      case 4: softmax_topk_token<4>(ex, inv, E, io, po, s_hist); break;
+      case 5: softmax_topk_token<5>(ex, inv, E, io, po, s_hist); break;
+      case 6: softmax_topk_token<6>(ex, inv, E, io, po, s_hist); break;
+      case 7: softmax_topk_token<7>(ex, inv, E, io, po, s_hist); break;
+      default: softmax_topk_token<8>(ex, inv, E, io, po, s_hist); break;
+    }
+  }
+  __syncthreads();
+  if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
+}
+
 }  // namespace
 
 template <typename ActT>
 hipError_t launch_router(const ActT* x, const float* wr_t, const float* br, int N, int C,
                          int E, int k, int32_t* topk_idx, float* topk_p, int32_t* hist,
                          hipStream_t stream) {
-  const int nb = (N + kRT - 1) / kRT;
+  const int TB = router_tokens_per_block(E);
+  const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
-  hipLaunchKernelGGL(router_topk_kernel<ActT>, dim3(nb), dim3(256), 0, stream, x, wr_t, br, N,
-                     C, E, k, topk_idx, topk_p, hist, nb);
+  const dim3 g(nb), b(256);
+  switch (E) {
+    case 64:
+      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 2, 2>), g, b, 0, stream, x, wr_t, br, N,
+                         C, E, k, TB, topk_idx, topk_p, hist, nb);
+      break;
+    case 32:
+      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 2, 2>), g, b, 0, stream, x, wr_t, br, N,
+                         C, E, k, TB, topk_idx, topk_p, hist, nb);
+      break;
+    case 16:
+    case 8:
+      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 2, 1>), g, b, 0, stream, x, wr_t, br, N,
+                         C, E, k, TB, topk_idx, topk_p, hist, nb);
+      break;
+    case 4:
+      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 1, 1>), g, b, 0, stream, x, wr_t, br, N,
+                         C, E, k, TB, topk_idx, topk_p, hist, nb);
+      break;
+    default:
+      hipLaunchKernelGGL(router_topk_kernel<ActT>, g, b, 0, stream, x, wr_t, br, N, C, E, k,
+                         topk_idx, topk_p, hist, nb);
+  }
   return hipGetLastError();
 }
 

@@ -48,6 +48,10 @@ UNIT_CASES = [
     Case("k_equals_e", _c("k_equals_e", 24, 64, 4, 4, 64, rb="normal"), 0.05),
     Case("bf16_e64_k6", _c("bf16_e64_k6", 96, 128, 64, 6, 128, "bf16", rb="zipf"), 0.02),
     Case("fp8_small", _c("fp8_small", 48, 128, 8, 4, 192, "bf16", "fp8", rb="normal"), 0.02),
+    # enough rows per expert for the large-M (256/128-row tile) GEMM path,
+    # with a ragged last tile in every expert
+    Case("bf16_large_m", _c("bf16_large_m", 1100, 192, 4, 2, 320, "bf16", rb="zipf"), 0.02),
+    Case("fp8_large_m", _c("fp8_large_m", 900, 256, 4, 2, 256, "bf16", "fp8", rb="normal"), 0.02),
 ]
 
 CONFIG_CASES = [

@@ -114,6 +114,20 @@ def test_parity_full_size(name):
     check_close(y[rows], fx["y_rows"], TOL[case.cfg.weights], name)
 
 
+@pytest.mark.parametrize("tile", ["128", "256"])
+@pytest.mark.parametrize("name", ["bf16_large_m", "fp8_large_m"])
+def test_large_m_tiles(name, tile, monkeypatch):
+    """Both block tiles of the large-M grouped GEMM (the tile is chosen when
+    the handle is created)."""
+    monkeypatch.setenv("MGPT_MOE_GEMM_TILE", tile)
+    case = C.ALL_CASES[name]
+    fx = fixture(name)
+    inp = C.build_inputs(case)
+    layer, y, r, _, _ = run_gpu(inp)
+    check_routing(r, fx, full=True)
+    check_close(y, O.forward(inp)["y"], TOL[case.cfg.weights], f"{name}/tile{tile}")
+
+
 def test_deterministic_and_repeatable():
     case = C.ALL_CASES["bf16_e64_k6"]
     inp = C.build_inputs(case)
