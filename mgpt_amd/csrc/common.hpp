@@ -92,7 +92,8 @@ __device__ __forceinline__ int wave_sum(int v) {
 // over an upper bound of m-tiles; each block derives its expert, the
 // segment's first row and its end row from the per-expert counts (E <= 64),
 // so no host round-trip is needed.  Returns false for blocks past the last
-// tile.  Must be called by every thread of the block (uses shared memory).
+// tile.  Must be called by every thread of the block (uses shared memory);
+// it may be called repeatedly (persistent kernels).
 struct TileInfo {
   int expert;
   int row0;     // first row of this m-tile (global slot index)
@@ -103,6 +104,7 @@ template <int BM>
 __device__ __forceinline__ bool find_tile(const int32_t* __restrict__ counts, int E,
                                           int mtile, TileInfo* out) {
   __shared__ int s_info[4];
+  __syncthreads();   // every wave has read the previous call's result
   if (threadIdx.x < kWave) {
     const int l = lane_id();
     int cnt = (l < E) ? counts[l] : 0;

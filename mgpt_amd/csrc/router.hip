@@ -160,19 +160,40 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 
 // Register-tiled variant for E in {4, 8, 16, 32, 64}: thread (tg, eg) owns
 // RT tokens x RE experts (experts fastest across lanes, so the lanes of a
-// wave that share a token read the same LDS address), walks c in order and
-// reads 4 consecutive c of x and W_r^T as one float4 per operand.  Blocks
-// hold TB = 256 / (E / RE) * RT tokens (16..64), so the grid has enough
-// workgroups to occupy every CU.  Same rounding sequence per logit as the
-// generic kernel.
+// wave that share a token load the same address) and streams its x rows and
+// W_r^T rows straight from global memory, 8 consecutive c per 16-byte load,
+// with no LDS staging and no barriers in the dot-product loop; x is read
+// from HBM once per block (the other lanes hit in the cache) and W_r^T
+// (E*C*4 bytes) stays cache-resident.  Each logit still accumulates c = 0,
+// 1, 2, ... in order with a rounded product and a rounded add per term.
+// Blocks hold TB = 256 / (E / RE) * RT tokens (16..64) so the grid fills
+// the GPU.
+template <typename ActT> struct Load8;
+template <> struct Load8<bf16_t> {
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+template <> struct Load8<float> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+};
+
 template <typename ActT, int RT, int RE>
 __global__ __launch_bounds__(256) void router_topk_tiled_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr_t, const float* __restrict__ br,
     int N, int C, int E, int k, int TB, int32_t* __restrict__ topk_idx,
     float* __restrict__ topk_p, int32_t* __restrict__ hist, int num_blocks) {
-  constexpr int LD = kCK + 4;          // float4-aligned rows
-  __shared__ __attribute__((aligned(16))) float s_x[kRT][LD];
-  __shared__ __attribute__((aligned(16))) float s_w[kMaxExperts][LD];
   __shared__ float s_l[kRT][kMaxExperts + 1];
   __shared__ float s_m[kRT];
   __shared__ int s_hist[kMaxExperts];
@@ -183,43 +204,35 @@ __global__ __launch_bounds__(256) void router_topk_tiled_kernel(
   const int eg = tid % EG, tg = tid / EG;
   if (tid < kMaxExperts) s_hist[tid] = 0;
 
+  const ActT* xr[RT];
+  const float* wr[RE];
+#pragma unroll
+  for (int i = 0; i < RT; ++i) {
+    const int t = min(tok0 + tg * RT + i, N - 1);   // rows past N: compute, never store
+    xr[i] = x + (size_t)t * C;
+  }
+#pragma unroll
+  for (int j = 0; j < RE; ++j) wr[j] = wr_t + (size_t)(eg * RE + j) * C;
+
   float acc[RT][RE];
 #pragma unroll
   for (int i = 0; i < RT; ++i)
 #pragma unroll
     for (int j = 0; j < RE; ++j) acc[i][j] = 0.0f;
 
-  for (int c0 = 0; c0 < C; c0 += kCK) {
-    __syncthreads();
-    for (int q = tid; q < TB * kCK; q += 256) {
-      const int r = q / kCK, c = q % kCK;
-      const int t = tok0 + r;
-      s_x[r][c] = (t < N) ? ActTraits<ActT>::load(x + (size_t)t * C + c0 + c) : 0.0f;
-    }
-    for (int q = tid; q < E * kCK; q += 256) {
-      const int e = q / kCK, c = q % kCK;
-      s_w[e][c] = wr_t[(size_t)e * C + c0 + c];
-    }
-    __syncthreads();
-#pragma unroll 4
-    for (int c = 0; c < kCK; c += 4) {
-      float4 xv[RT], wv[RE];
+#pragma unroll 2
+  for (int c = 0; c < C; c += 8) {
+    float xv[RT][8], wv[RE][8];
 #pragma unroll
-      for (int i = 0; i < RT; ++i) xv[i] = *reinterpret_cast<const float4*>(&s_x[tg * RT + i][c]);
+    for (int i = 0; i < RT; ++i) Load8<ActT>::load(xr[i] + c, xv[i]);
 #pragma unroll
-      for (int j = 0; j < RE; ++j) wv[j] = *reinterpret_cast<const float4*>(&s_w[eg * RE + j][c]);
+    for (int j = 0; j < RE; ++j) Load8<float>::load(wr[j] + c, wv[j]);
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
 #pragma unroll
       for (int i = 0; i < RT; ++i)
 #pragma unroll
-        for (int j = 0; j < RE; ++j) {
-          float a = acc[i][j];
-          a = a + xv[i].x * wv[j].x;
-          a = a + xv[i].y * wv[j].y;
-          a = a + xv[i].z * wv[j].z;
-          a = a + xv[i].w * wv[j].w;
-          acc[i][j] = a;
-        }
-    }
+        for (int j = 0; j < RE; ++j) acc[i][j] = acc[i][j] + xv[i][cc] * wv[j][cc];
   }
 #pragma unroll
   for (int i = 0; i < RT; ++i)
