@@ -21,19 +21,15 @@ constexpr int kWave = 64;
 constexpr int kNumXcd = 8;        // MI355X: 8 accelerator complex dies, one L2 each
 constexpr int kMaxExperts = 64;
 constexpr int kMaxTopK = 8;
-// Tokens per router / permute block (at most kRouterTokens): block b owns
-// tokens [b*TB, (b+1)*TB) and so the flat assignment ids
-// [b*TB*k, (b+1)*TB*k).  The router's register tiling fixes TB per E.
+// Tokens per router / permute block: block b owns tokens [b*64, (b+1)*64)
+// and so the flat assignment ids [b*64*k, (b+1)*64*k).
 constexpr int kRouterTokens = 64;
-__host__ __device__ inline int router_tokens_per_block(int E) {
-  switch (E) {
-    case 64: return 16;   // 2 tokens x 2 experts per thread
-    case 32: return 32;   // 2 x 2
-    case 16: return 32;   // 2 x 1
-    case 8: return 64;    // 2 x 1
-    case 4: return 64;    // 1 x 1
-    default: return kRouterTokens;   // generic kernel
-  }
+__host__ __device__ inline int router_tokens_per_block(int /*E*/) { return kRouterTokens; }
+
+// Router experts per wave (the router block has ceil(E / RE) <= 16 waves);
+// router weights are packed [ceil(E/RE)][C][RE], zero-padded.
+__host__ __device__ inline int router_experts_per_wave(int E) {
+  return E <= 16 ? 1 : (E <= 32 ? 2 : 4);
 }
 
 // Grouped-GEMM epilogues (gemm.hip).

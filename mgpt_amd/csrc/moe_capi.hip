@@ -43,6 +43,7 @@ template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
+hipError_t launch_pack_router(const float*, int, int, float*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
                            const int32_t*, int, int, int, int, int, bf16_t*, int, int,
@@ -90,7 +91,7 @@ struct mgpt_moe {
   int act, wdt;
   int device;
   int gemm_tile = 256;     // block tile of the large-M bf16 GEMMs (256 or 128)
-  float* wr_t = nullptr;   // [E][C]
+  float* wr_g = nullptr;   // router weights [G][C][RE] (router_experts_per_wave)
   float* br = nullptr;     // [E]
   void* wgu = nullptr;     // [E][2Hp][C] of bf16 / fp8 / f32
   void* wd = nullptr;      // [E][Cp][Hp]
@@ -165,10 +166,10 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_t, h->br, h->wgu, h->wd, h->sgu, h->sd, h->bg, h->bu, h->bd};
+  void* ptrs[] = {h->wr_g, h->br, h->wgu, h->wd, h->sgu, h->sd, h->bg, h->bu, h->bd};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  h->wr_t = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
+  h->wr_g = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
   h->wgu = h->wd = nullptr;
   h->loaded = false;
 }
@@ -241,7 +242,8 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   const size_t wb = h->w_bytes();
   const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
   const bool bf = h->wdt == MGPT_DTYPE_BF16;
-  HIP_TRY(hipMalloc(&h->wr_t, sizeof(float) * E * C));
+  const int RE = router_experts_per_wave(E);
+  HIP_TRY(hipMalloc(&h->wr_g, sizeof(float) * ((E + RE - 1) / RE) * RE * C));
   HIP_TRY(hipMalloc(&h->br, sizeof(float) * E));
   HIP_TRY(hipMalloc(&h->wgu, wb * E * 2 * Hp * C));
   HIP_TRY(hipMalloc(&h->wd, wb * E * Cp * Hp));
@@ -290,7 +292,7 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   do {
     const float* s = src(0, (size_t)C * E);
     if (!s) break;
-    if (launch_pack_transpose<float>(s, C, E, h->wr_t, C, 0, 0, st) != hipSuccess) {
+    if (launch_pack_router(s, C, E, h->wr_g, st) != hipSuccess) {
       rc = fail(MGPT_ERR_HIP, "router pack failed");
       break;
     }
@@ -378,7 +380,7 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
   HIP_TRY(mark(0));
-  HIP_TRY(launch_router<ActT>(x, h->wr_t, h->br, N, C, E, k, idx, topp, hist, st));
+  HIP_TRY(launch_router<ActT>(x, h->wr_g, h->br, N, C, E, k, idx, topp, hist, st));
   HIP_TRY(mark(1));
   HIP_TRY(launch_expert_scan(hist, nb, E, base, counts, st));
   HIP_TRY(mark(2));

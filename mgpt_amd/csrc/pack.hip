@@ -88,7 +88,25 @@ __global__ void pad_rows_kernel(const float* __restrict__ src, int n, float* __r
   if (i < ldd) dst[i] = i < n ? src[i] : 0.0f;
 }
 
+// Router weights W_r [C][E] -> [G][C][RE] (G = ceil(E/RE)), zero-padded.
+__global__ void pack_router_kernel(const float* __restrict__ wr, int C, int E, int RE,
+                                   float* __restrict__ out, int total) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int j = i % RE, c = (i / RE) % C, g = i / (RE * C);
+  const int e = g * RE + j;
+  out[i] = e < E ? wr[(size_t)c * E + e] : 0.0f;
+}
+
 }  // namespace
+
+hipError_t launch_pack_router(const float* wr, int C, int E, float* out, hipStream_t stream) {
+  const int RE = router_experts_per_wave(E);
+  const int total = ((E + RE - 1) / RE) * C * RE;
+  hipLaunchKernelGGL(pack_router_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, wr, C,
+                     E, RE, out, total);
+  return hipGetLastError();
+}
 
 template <typename DT>
 hipError_t launch_pack_transpose(const float* src, int Kin, int Nout, DT* dst, int ldd, int mode,

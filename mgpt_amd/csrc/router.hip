@@ -6,18 +6,18 @@
 // bias is added, :1499-1507 / :331-342); softmax utils/Tensor.cpp:850-883;
 // top-k utils/Tensor.cpp:1296-1334; histogram utils/Tensor.cpp:1336-1352.
 //
-// One block of 256 threads owns kRouterTokens = 64 tokens.  Phase 1 computes
-// the 64 x E logits: thread t owns the (token, expert) pairs t, t+256, ... and
-// walks c = 0..C-1 in order over LDS-staged 64-column chunks of x and W_r^T
-// (so every dot product has exactly the reference's rounding sequence; the
-// file is built with -ffp-contract=off, so nothing is fused).  MFMA cannot
-// be used here: its internal accumulation order differs.  Phase 2: per-token
-// max (strict '>' from element 0, as the reference, so NaN handling
-// matches), the E exponentials in parallel with glibc's expf algorithm, then
-// per token the sequential sum, the clamp and the insertion top-k in
-// registers.  Phase 3: block-local expert histogram (LDS atomics on ints;
-// counts are order-free), written expert-major as hist[e][block] for the
-// per-expert scan of dispatch.hip.
+// One block owns 64 tokens (one per lane) and E/RE waves.  Phase 1: wave g
+// computes the logits of experts [g*RE, g*RE+RE) for the 64 tokens, walking
+// c = 0..C-1 in order with one rounded product and one rounded add per term
+// (the file is built with -ffp-contract=off), so every logit has exactly the
+// reference's rounding sequence; MFMA cannot be used here, its internal
+// accumulation order differs.  The weights of a wave are wave-uniform and
+// come through the scalar cache.  Phase 2: per-token max (strict '>' from
+// element 0, as the reference, so NaN handling matches), the exponentials
+// in parallel with glibc's expf algorithm, then per token the sequential
+// sum, the clamp and the insertion top-k in registers.  Phase 3: block-local
+// expert histogram (LDS atomics on ints; counts are order-free), written
+// expert-major as hist[e][block] for the per-expert scan of dispatch.hip.
 #include "common.hpp"
 #include "glibc_expf.hpp"
 
@@ -27,9 +27,7 @@ __constant__ uint64_t c_exp2_tab[32] = MGPT_EXP2_TABLE_INIT;
 
 namespace {
 
-constexpr int kRT = kRouterTokens;   // tokens per block
-constexpr int kCK = 64;              // columns per LDS chunk
-constexpr int kMaxPairsPerThread = kRT * kMaxExperts / 256;   // 16
+constexpr int kRT = kRouterTokens;   // tokens per block (one per lane)
 
 // Branch-free insertion of (v, e) into a descending top-K list, identical to
 // the reference's shifting loop: the element at j-1 moves to j exactly when
@@ -67,107 +65,6 @@ __device__ __forceinline__ void softmax_topk_token(const float* __restrict__ ex,
   }
 }
 
-template <typename ActT>
-__global__ __launch_bounds__(256) void router_topk_kernel(
-    const ActT* __restrict__ x, const float* __restrict__ wr_t,   // [E][C]
-    const float* __restrict__ br, int N, int C, int E, int k,
-    int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
-    int32_t* __restrict__ hist, int num_blocks) {
-  __shared__ float s_x[kRT][kCK + 1];
-  __shared__ float s_w[kMaxExperts][kCK + 1];
-  __shared__ float s_l[kRT][kMaxExperts + 1];   // logits, then exponentials
-  __shared__ float s_m[kRT];
-  __shared__ int s_hist[kMaxExperts];
-
-  const int tid = threadIdx.x;
-  const int tok0 = blockIdx.x * kRT;
-  const int pairs = kRT * E;
-  if (tid < kMaxExperts) s_hist[tid] = 0;
-
-  float acc[kMaxPairsPerThread];
-#pragma unroll
-  for (int j = 0; j < kMaxPairsPerThread; ++j) acc[j] = 0.0f;
-
-  for (int c0 = 0; c0 < C; c0 += kCK) {
-    __syncthreads();
-    // Stage x[tok0 .. tok0+63][c0 .. c0+63] (rows past N read as 0) and
-    // W_r^T[0..E-1][c0 .. c0+63].
-    for (int q = tid; q < kRT * kCK; q += 256) {
-      const int r = q / kCK, c = q % kCK;
-      const int t = tok0 + r;
-      s_x[r][c] = (t < N) ? ActTraits<ActT>::load(x + (size_t)t * C + c0 + c) : 0.0f;
-    }
-    for (int q = tid; q < E * kCK; q += 256) {
-      const int e = q / kCK, c = q % kCK;
-      s_w[e][c] = wr_t[(size_t)e * C + c0 + c];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < kMaxPairsPerThread; ++j) {
-      const int p = tid + 256 * j;
-      if (p < pairs) {
-        const int r = p / E, e = p % E;
-        float a = acc[j];
-        for (int c = 0; c < kCK; ++c) a = a + s_x[r][c] * s_w[e][c];
-        acc[j] = a;
-      }
-    }
-  }
-  // Logits = dot + bias (a separate rounded add, as the reference's bias pass).
-#pragma unroll
-  for (int j = 0; j < kMaxPairsPerThread; ++j) {
-    const int p = tid + 256 * j;
-    if (p < pairs) {
-      const int r = p / E, e = p % E;
-      s_l[r][e] = acc[j] + br[e];
-    }
-  }
-  __syncthreads();
-  // Row max with the reference's strict '>' scan starting from element 0.
-  if (tid < kRT) {
-    float m = s_l[tid][0];
-    for (int v = 1; v < E; ++v)
-      if (s_l[tid][v] > m) m = s_l[tid][v];
-    s_m[tid] = m;
-  }
-  __syncthreads();
-  for (int p = tid; p < pairs; p += 256) {
-    const int r = p / E, e = p % E;
-    s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], c_exp2_tab);
-  }
-  __syncthreads();
-  if (tid < kRT && tok0 + tid < N) {
-    const float* ex = s_l[tid];
-    float s = 0.0f;
-    for (int v = 0; v < E; ++v) s = s + ex[v];
-    const float inv = 1.0f / fmaxf(s, 1e-15f);
-    int32_t* io = topk_idx + (size_t)(tok0 + tid) * k;
-    float* po = topk_p + (size_t)(tok0 + tid) * k;
-    switch (k) {
-      case 1: softmax_topk_token<1>(ex, inv, E, io, po, s_hist); break;
-      case 2: softmax_topk_token<2>(ex, inv, E, io, po, s_hist); break;
-      case 3: softmax_topk_token<3>(ex, inv, E, io, po, s_hist); break;
-      case 4: softmax_topk_token<4>(ex, inv, E, io, po, s_hist); break;
-      case 5: softmax_topk_token<5>(ex, inv, E, io, po, s_hist); break;
-      case 6: softmax_topk_token<6>(ex, inv, E, io, po, s_hist); break;
-      case 7: softmax_topk_token<7>(ex, inv, E, io, po, s_hist); break;
-      default: softmax_topk_token<8>(ex, inv, E, io, po, s_hist); break;
-    }
-  }
-  __syncthreads();
-  if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
-}
-
-// Register-tiled variant for E in {4, 8, 16, 32, 64}: thread (tg, eg) owns
-// RT tokens x RE experts (experts fastest across lanes, so the lanes of a
-// wave that share a token load the same address) and streams its x rows and
-// W_r^T rows straight from global memory, 8 consecutive c per 16-byte load,
-// with no LDS staging and no barriers in the dot-product loop; x is read
-// from HBM once per block (the other lanes hit in the cache) and W_r^T
-// (E*C*4 bytes) stays cache-resident.  Each logit still accumulates c = 0,
-// 1, 2, ... in order with a rounded product and a rounded add per term.
-// Blocks hold TB = 256 / (E / RE) * RT tokens (16..64) so the grid fills
-// the GPU.
 template <typename ActT> struct Load8;
 template <> struct Load8<bf16_t> {
   static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
@@ -189,72 +86,64 @@ template <> struct Load8<float> {
   }
 };
 
-template <typename ActT, int RT, int RE>
-__global__ __launch_bounds__(256) void router_topk_tiled_kernel(
-    const ActT* __restrict__ x, const float* __restrict__ wr_t, const float* __restrict__ br,
-    int N, int C, int E, int k, int TB, int32_t* __restrict__ topk_idx,
-    float* __restrict__ topk_p, int32_t* __restrict__ hist, int num_blocks) {
+// Wave-uniform router weights.  A block owns 64 tokens (one per lane) and
+// E/RE waves; wave g computes experts [g*RE, g*RE + RE) for all 64 tokens.
+// Its slice of W_r is the same for every lane, so it is read with scalar
+// loads into SGPRs (packed as [G][C][RE], 8*RE consecutive floats per 8 c),
+// and each lane streams only its own token's row of x with 16-byte loads:
+// no per-lane copies of the weights, no LDS and no barrier in the loop.
+// Each logit accumulates c = 0, 1, ... in order, one rounded product and one
+// rounded add per term (built with -ffp-contract=off), then the bias.
+template <typename ActT, int RE>
+__global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
+    int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
+    int32_t* __restrict__ hist, int num_blocks) {
   __shared__ float s_l[kRT][kMaxExperts + 1];
   __shared__ float s_m[kRT];
   __shared__ int s_hist[kMaxExperts];
 
   const int tid = threadIdx.x;
-  const int tok0 = blockIdx.x * TB;
-  const int EG = E / RE;               // expert groups
-  const int eg = tid % EG, tg = tid / EG;
+  const int lane = lane_id();
+  const int g = __builtin_amdgcn_readfirstlane(tid / kWave);   // expert group of this wave
+  const int tok0 = blockIdx.x * kRT;
   if (tid < kMaxExperts) s_hist[tid] = 0;
 
-  const ActT* xr[RT];
-  const float* wr[RE];
-#pragma unroll
-  for (int i = 0; i < RT; ++i) {
-    const int t = min(tok0 + tg * RT + i, N - 1);   // rows past N: compute, never store
-    xr[i] = x + (size_t)t * C;
-  }
-#pragma unroll
-  for (int j = 0; j < RE; ++j) wr[j] = wr_t + (size_t)(eg * RE + j) * C;
+  const ActT* xrow = x + (size_t)min(tok0 + lane, N - 1) * C;   // rows past N: never stored
+  const float* wg = wr_g + (size_t)g * C * RE;
 
-  float acc[RT][RE];
+  float acc[RE];
 #pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int j = 0; j < RE; ++j) acc[i][j] = 0.0f;
-
+  for (int j = 0; j < RE; ++j) acc[j] = 0.0f;
 #pragma unroll 2
   for (int c = 0; c < C; c += 8) {
-    float xv[RT][8], wv[RE][8];
-#pragma unroll
-    for (int i = 0; i < RT; ++i) Load8<ActT>::load(xr[i] + c, xv[i]);
-#pragma unroll
-    for (int j = 0; j < RE; ++j) Load8<float>::load(wr[j] + c, wv[j]);
+    float xv[8];
+    Load8<ActT>::load(xrow + c, xv);
+    const float* wc = wg + (size_t)c * RE;
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc)
 #pragma unroll
-      for (int i = 0; i < RT; ++i)
-#pragma unroll
-        for (int j = 0; j < RE; ++j) acc[i][j] = acc[i][j] + xv[i][cc] * wv[j][cc];
+      for (int j = 0; j < RE; ++j) acc[j] = acc[j] + xv[cc] * wc[cc * RE + j];
   }
 #pragma unroll
-  for (int i = 0; i < RT; ++i)
-#pragma unroll
-    for (int j = 0; j < RE; ++j) {
-      const int e = eg * RE + j;
-      s_l[tg * RT + i][e] = acc[i][j] + br[e];
-    }
+  for (int j = 0; j < RE; ++j) {
+    const int e = g * RE + j;
+    if (e < E) s_l[lane][e] = acc[j] + br[e];
+  }
   __syncthreads();
-  if (tid < TB) {
+  if (tid < kRT) {
     float m = s_l[tid][0];
     for (int v = 1; v < E; ++v)
       if (s_l[tid][v] > m) m = s_l[tid][v];
     s_m[tid] = m;
   }
   __syncthreads();
-  for (int p = tid; p < TB * E; p += 256) {
+  for (int p = tid; p < kRT * E; p += blockDim.x) {
     const int r = p / E, e = p % E;
     s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], c_exp2_tab);
   }
   __syncthreads();
-  if (tid < TB && tok0 + tid < N) {
+  if (tid < kRT && tok0 + tid < N) {
     const float* ex = s_l[tid];
     float sum = 0.0f;
     for (int v = 0; v < E; ++v) sum = sum + ex[v];
@@ -279,34 +168,26 @@ __global__ __launch_bounds__(256) void router_topk_tiled_kernel(
 }  // namespace
 
 template <typename ActT>
-hipError_t launch_router(const ActT* x, const float* wr_t, const float* br, int N, int C,
-                         int E, int k, int32_t* topk_idx, float* topk_p, int32_t* hist,
+hipError_t launch_router(const ActT* x, const float* wr_g, const float* br, int N, int C, int E,
+                         int k, int32_t* topk_idx, float* topk_p, int32_t* hist,
                          hipStream_t stream) {
-  const int TB = router_tokens_per_block(E);
-  const int nb = (N + TB - 1) / TB;
+  const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
-  const dim3 g(nb), b(256);
-  switch (E) {
-    case 64:
-      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 2, 2>), g, b, 0, stream, x, wr_t, br, N,
-                         C, E, k, TB, topk_idx, topk_p, hist, nb);
+  const int RE = router_experts_per_wave(E);
+  const int waves = (E + RE - 1) / RE;
+  const dim3 g(nb), b(waves * kWave);
+  switch (RE) {
+    case 1:
+      hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 1>), g, b, 0, stream, x, wr_g, br, N,
+                         C, E, k, topk_idx, topk_p, hist, nb);
       break;
-    case 32:
-      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 2, 2>), g, b, 0, stream, x, wr_t, br, N,
-                         C, E, k, TB, topk_idx, topk_p, hist, nb);
-      break;
-    case 16:
-    case 8:
-      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 2, 1>), g, b, 0, stream, x, wr_t, br, N,
-                         C, E, k, TB, topk_idx, topk_p, hist, nb);
-      break;
-    case 4:
-      hipLaunchKernelGGL((router_topk_tiled_kernel<ActT, 1, 1>), g, b, 0, stream, x, wr_t, br, N,
-                         C, E, k, TB, topk_idx, topk_p, hist, nb);
+    case 2:
+      hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 2>), g, b, 0, stream, x, wr_g, br, N,
+                         C, E, k, topk_idx, topk_p, hist, nb);
       break;
     default:
-      hipLaunchKernelGGL(router_topk_kernel<ActT>, g, b, 0, stream, x, wr_t, br, N, C, E, k,
-                         topk_idx, topk_p, hist, nb);
+      hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 4>), g, b, 0, stream, x, wr_g, br, N,
+                         C, E, k, topk_idx, topk_p, hist, nb);
   }
   return hipGetLastError();
 }
