@@ -17,6 +17,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import subprocess
 import sys
 import time
@@ -27,6 +28,68 @@ sys.path.insert(0, ROOT)
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
+CALIB_MIB = 512               # known-size elementwise copy for counter calibration
+
+
+def stage_of(kernel_name: str):
+    """Forward stage of a kernel in a rocprofv3 trace (None: not a forward kernel)."""
+    short = kernel_name.replace("(anonymous namespace)", "").split("(")[0]
+    if "router_topk" in short:
+        return "router_topk"
+    if "expert_scan" in short:
+        return "expert_scan"
+    if "permute_kernel" in short:
+        return "permute"
+    if "combine_kernel" in short:
+        return "combine"
+    m = re.search(r"gemm_dma_kernel<(\d)>", short)
+    if m:
+        return ("gemm_gateup", "gemm_down")[int(m.group(1))]
+    m = re.search(r"grouped_gemm_kernel<([^>]*)>", short)
+    if m:
+        epi = int(m.group(1).split(",")[6])
+        return ("gemm_gateup", "gemm_down")[epi]
+    if "MulFunctor" in kernel_name:
+        return "calib_copy"
+    return None
+
+
+def _counter_means(d: str, counter: str):
+    """Mean counter value per dispatch, by stage, from a rocprofv3 --pmc csv."""
+    import csv
+    vals = {}
+    with open(os.path.join(d, "run_counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            if r["Counter_Name"] != counter:
+                continue
+            st = stage_of(r["Kernel_Name"])
+            if st:
+                vals.setdefault(st, []).append(float(r["Counter_Value"]))
+    if "calib_copy" in vals:      # the 512 MiB copies only, not torch's small multiplies
+        big = max(vals["calib_copy"])
+        vals["calib_copy"] = [v for v in vals["calib_copy"] if v > 0.5 * big]
+    return {k: sum(v) / len(v) for k, v in vals.items()}
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str, workload: str, commands) -> dict:
+    """HBM bytes per launch of each forward kernel from two rocprofv3 --pmc
+    runs (FETCH_SIZE, WRITE_SIZE; KiB per dispatch), each scaled by the factor
+    that makes the same counter read exactly the known size of the
+    calibration copy (CALIB_MIB read and CALIB_MIB written)."""
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    known = CALIB_MIB * 1024.0
+    ff = known / fetch["calib_copy"]
+    fw = known / write["calib_copy"]
+    kern = {st: {"fetch_bytes": round(fetch[st] * 1024 * ff), "write_bytes": round(write[st] * 1024 * fw)}
+            for st in fetch if st != "calib_copy" and st in write}
+    for v in kern.values():
+        v["hbm_bytes"] = v["fetch_bytes"] + v["write_bytes"]
+    return {"workload": workload, "calib_copy_mib": CALIB_MIB,
+            "calib_fetch_kib_read": round(fetch["calib_copy"], 1),
+            "calib_write_kib_read": round(write["calib_copy"], 1),
+            "fetch_factor": round(ff, 4), "write_factor": round(fw, 4),
+            "kernels": kern, "commands": commands}
 
 
 def cpu_baseline(cfg, sample_tokens: int, reps: int):
@@ -58,19 +121,92 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int):
     }
 
 
+def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
+    """Markdown table of a rocprofv3 kernel-statistics csv next to the HIP-event
+    stage means that bench.py measured in the same run."""
+    import csv
+    with open(bench_json) as f:
+        b = json.loads(f.read().strip().splitlines()[-1])
+    rows = list(csv.DictReader(open(stats_csv)))
+    cmd = (f"rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python bench.py "
+           f"--config {config} --steps {b['steps']} --warmup {b['warmup']} --no-cpu-baseline")
+    out = [f"# {config} MoE forward: rocprofv3 kernel statistics (MI355X)", "",
+           "Command (repository root, on the GPU box), then "
+           "`python bench.py --config %s --summarize-stats <dir>/run_kernel_stats.csv <json line>`:"
+           % config, "", "```", cmd, "```", "",
+           f"Workload: {b['config']['workload']}.  {b['warmup'] + b['steps']} forwards "
+           f"({b['warmup']} warmup + {b['steps']} timed); pack/pad/quantise/copy kernels are the "
+           "one-time parameter load.", "",
+           "| Kernel | Stage | Calls | Average (us) | Share of GPU time |", "|---|---|---|---|---|"]
+    for r in rows:
+        name = r["Name"].replace("unsigned short", "bf16").replace("mgpt::(anonymous namespace)::", "")
+        if len(name) > 110:
+            name = name[:107] + "..."
+        out.append(f"| `{name}` | {stage_of(r['Name']) or '-'} | {r['Calls']} | "
+                   f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['Percentage']):.2f}% |")
+    out += ["", "HIP-event stage means measured by bench.py in the same run (ms):", "",
+            "| Stage | ms |", "|---|---|"]
+    out += [f"| {k} | {v} |" for k, v in b["stage_ms"].items()]
+    rf = b["roofline"]
+    out += ["", f"bench.py: {b['value']:.0f} tokens/s, {b['ms_per_step']} ms/step; gate/up GEMM "
+            f"{rf['achieved']} TFLOP/s = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s dense bf16; "
+            f"both expert GEMMs {b['expert_gemm_tflops']} TFLOP/s."]
+    return "\n".join(out)
+
+
+def workload_name(cfg) -> str:
+    return (f"{cfg.name}: MoE block forward N={cfg.N} (B={cfg.B},T={cfg.T}) C={cfg.C} E={cfg.E} "
+            f"k={cfg.k} H={cfg.H} act={cfg.act} weights={cfg.weights} "
+            f"router_bias={cfg.router_bias}")
+
+
+def traffic_path(cfg) -> str:
+    return os.path.join(ROOT, "profiles", f"{cfg.name}_hbm_traffic.json")
+
+
+def load_traffic(cfg):
+    """Committed per-kernel HBM traffic of this workload (summarize_traffic's
+    output), if it was measured for exactly this workload."""
+    try:
+        with open(traffic_path(cfg)) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    return t if t.get("workload") == workload_name(cfg) else None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg3")
-    ap.add_argument("--cpu-tokens", type=int, default=1024)
+    ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="after the timed run, copy this many MiB device-to-device 3 times "
-                         "(a known-size kernel for calibrating FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help=f"after the timed run, copy {CALIB_MIB} MiB with an elementwise kernel 3 "
+                         "times (known-size traffic for calibrating FETCH_SIZE/WRITE_SIZE)")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU run: turn two rocprofv3 --pmc outputs (FETCH_SIZE, WRITE_SIZE) "
+                         "of 'bench.py --calib-copy' into the per-kernel HBM traffic JSON")
+    ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_CSV", "BENCH_JSON"),
+                    help="no GPU run: markdown summary of a rocprofv3 --kernel-trace --stats run "
+                         "of this script and of the JSON line that run printed")
     args = ap.parse_args()
+    if args.summarize_stats:
+        print(summarize_stats(*args.summarize_stats, args.config))
+        return 0
+    if args.summarize_traffic:
+        from mgpt_amd import workload as wl
+        cfg = wl.CONFIGS[args.config]
+        cmd = ("rocprofv3 --pmc {c} --output-format csv -d {d} -o run -- python bench.py "
+               f"--config {args.config} --steps 3 --warmup 1 --no-cpu-baseline --calib-copy")
+        out = summarize_traffic(*args.summarize_traffic, workload_name(cfg),
+                                [cmd.format(c="FETCH_SIZE", d=args.summarize_traffic[0]),
+                                 cmd.format(c="WRITE_SIZE", d=args.summarize_traffic[1])])
+        print(json.dumps(out, indent=1))
+        return 0
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
               "expert-parallel multi-GPU path is a design note, not implemented", file=sys.stderr)
@@ -146,9 +282,7 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16" if cfg.act == "bf16" else "f32",
         "data": "synthetic (seeded; mgpt_amd.workload)",
-        "config": {"workload": f"{cfg.name}: MoE block forward N={N} (B={cfg.B},T={cfg.T}) "
-                               f"C={C} E={E} k={k} H={H} act={cfg.act} weights={cfg.weights} "
-                               f"router_bias={cfg.router_bias}",
+        "config": {"workload": workload_name(cfg),
                    "N": N, "C": C, "E": E, "k": k, "H": H, "global_batch": cfg.B,
                    "seq_len": cfg.T, "parallelism": "single GPU"},
         "layer_tflops": round(total_flops / (ms_per_step * 1e-3) / 1e12, 2),
@@ -166,14 +300,23 @@ def main() -> int:
         },
         "wall_s_timed": round(wall, 3),
     }
-    if args.calib_copy_mib:
-        n = args.calib_copy_mib * (1 << 20) // 4
+    traffic = load_traffic(cfg)
+    if traffic:
+        gu = traffic["kernels"].get("gemm_gateup")
+        result["roofline"]["traffic"] = gu["hbm_bytes"] if gu else None
+        result["roofline"]["traffic_source"] = (
+            "rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE bytes per launch, calibrated on a "
+            f"{CALIB_MIB} MiB copy (factors {traffic['fetch_factor']}, {traffic['write_factor']}); "
+            "profiles/" + os.path.basename(traffic_path(cfg)))
+        result["hbm_bytes_per_launch"] = {st: v["hbm_bytes"] for st, v in traffic["kernels"].items()}
+    if args.calib_copy:
+        n = CALIB_MIB * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):                  # an elementwise kernel, not a DMA-engine copy
             torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
-        result["calib_copy_mib"] = args.calib_copy_mib
+        result["calib_copy_mib"] = CALIB_MIB
     if not args.no_cpu_baseline:
         print("cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_tokens, N), args.cpu_reps)
