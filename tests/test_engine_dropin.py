@@ -1,0 +1,88 @@
+"""The C++ drop-in (mgpt_amd/host/MoELayer.{h,cpp}) inside the engine.
+
+CPU: the drop-in compiles against the engine's own headers (Layer.h,
+Tensor.h, LinearLayer.h, SwiGLU.h under /root/reference) and keeps the
+engine's public MoELayer interface (layers/MoELayer.h:36-51).
+GPU: tests/engine/_build/dropin_main -- the engine's unmodified Tensor,
+LinearLayer and SwiGLU sources with the drop-in in place of MoELayer.cpp --
+runs the engine's MoE shape test and full forwards whose outputs are
+compared with the oracle (fp32: 1e-5) and whose expert counts must equal the
+reference fixture's.
+"""
+import os
+import re
+import subprocess
+import tempfile
+
+import numpy as np
+import pytest
+
+import cases as C
+import oracle_lib as O
+from make_golden import write_input
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+ENGINE = "/root/reference/src/main"
+BIN = os.path.join(HERE, "engine", "_build", "dropin_main")
+HOST = os.path.join(ROOT, "mgpt_amd", "host")
+
+
+def public_methods(header_text):
+    body = header_text.split("public:", 1)[1]
+    return set(re.findall(r"\b(\w+)\s*\(", body))
+
+
+@pytest.mark.skipif(not os.path.isdir(ENGINE), reason="engine sources not present")
+def test_dropin_compiles_against_engine_headers():
+    cmd = ["g++", "-std=c++20", "-fsyntax-only", "-include", "cstring",
+           f"-I{HOST}", f"-I{ROOT}/include", f"-I{ENGINE}/utils",
+           f"-I{ENGINE}/neuralnetwork/layers", "-I/opt/rocm/include", "-D__HIP_PLATFORM_AMD__",
+           os.path.join(HOST, "MoELayer.cpp")]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+
+
+@pytest.mark.skipif(not os.path.isdir(ENGINE), reason="engine sources not present")
+def test_dropin_keeps_engine_interface():
+    ref = public_methods(open(os.path.join(ENGINE, "neuralnetwork/layers/MoELayer.h")).read())
+    ours = public_methods(open(os.path.join(HOST, "MoELayer.h")).read())
+    missing = ref - ours
+    assert not missing, f"drop-in lacks {missing}"
+
+
+def _run(args):
+    print("dropin_main", *args, flush=True)
+    return subprocess.run([BIN, *args], capture_output=True, text=True, timeout=300)
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.exists(BIN), reason="engine test binary not built")
+def test_engine_moe_shapes():
+    r = _run(["shapes"])
+    assert r.returncode == 0, r.stdout + r.stderr
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.exists(BIN), reason="engine test binary not built")
+@pytest.mark.parametrize("name", ["small_f32", "ragged_k3", "cfg1"])
+def test_engine_forward_matches_reference(name):
+    case = C.ALL_CASES[name]
+    inp = C.build_inputs(case)
+    fx = np.load(os.path.join(HERE, "golden", name + ".npz"))
+    with tempfile.TemporaryDirectory() as d:
+        ip, op = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
+        write_input(ip, inp)
+        r = _run(["run", ip, op])
+        assert r.returncode == 0, r.stdout + r.stderr
+        raw = open(op, "rb").read()
+    assert raw[:8] == b"MGPTDRP1"
+    N, Cc, E = np.frombuffer(raw, np.int32, 3, 8)
+    y = np.frombuffer(raw, np.float32, N * Cc, 20).reshape(N, Cc)
+    counts = np.frombuffer(raw, np.float32, E, 20 + 4 * N * Cc)
+    assert np.array_equal(counts, fx["counts"].astype(np.float32))
+    ref = O.forward(inp)["y"]
+    rel = np.linalg.norm(y - ref) / np.linalg.norm(ref)
+    mx = np.abs(y - ref).max() / np.abs(ref).max()
+    print(f"{name}: normwise {rel:.3e} max/max {mx:.3e}")
+    assert rel <= 1e-5 and mx <= 1e-5
