@@ -8,20 +8,24 @@
 //
 // CDNA4 design (choices measured on MI355X):
 //  * Persistent: one 512-thread block per CU walks the 256 x 256 output
-//    tiles t = blockIdx.x, +gridDim.x, ...; the first K-slab of the next
-//    tile is requested while the last slab of the current one is multiplied,
-//    so the DMA stream never drains between tiles.
+//    tiles; the blocks of one XCD take consecutive tiles of an order that
+//    groups 4 token blocks x all feature blocks, so they share operand
+//    panels in their XCD's L2.  Tile lookup is a per-wave register scan of
+//    the expert counts (no LDS, no barrier).
 //  * 8 waves (2 per SIMD) each own 64 output features x 128 tokens: 2 x 4
 //    tiles of v_mfma_f32_32x32x16_bf16.  Issue is in order within a wave, so
 //    one wave's MFMAs cover the other's LDS and barrier waits.
 //  * The MFMA computes D = W . X^T (weights as the row operand), so each
 //    lane holds 4 consecutive output features of one token: the epilogue
 //    writes 8-byte vectors.
-//  * Operands move HBM -> LDS with global_load_lds_dwordx4 (one 1 KB row
-//    block per wave instruction; no staging registers, no ds_write) into a
-//    2-stage ring.  The slab barrier is a bare s_barrier after an explicit
-//    vmcnt wait for the wave's own DMA; __syncthreads() would also drain the
-//    prefetch in flight.
+//  * Operands move HBM -> LDS with global_load_lds_dwordx4 (1 KB per wave
+//    instruction; no staging registers, no ds_write) into a ring of five
+//    32 KB units (activations or weights of a 64-column slab) that runs
+//    across tile boundaries.  The loads are inline asm the compiler does not
+//    track, with explicit vmcnt waits: for the builtin it inserts vmcnt(0)
+//    before LDS reads, which serialises the ring.
+//  * Fragments are read one k-step ahead of the MFMAs, interleaved with
+//    them (sched_group_barrier), across slab boundaries.
 //  * LDS rows are 128 B (64 bf16); K-chunk c of row r sits at slot
 //    c ^ ((r >> 1) & 7): gfx950's LDS has 64 banks, so the 16 lanes served
 //    together (16 rows of one logical chunk) hit 16 distinct bank groups.
@@ -32,29 +36,18 @@
 namespace mgpt {
 namespace {
 
-constexpr int kThreads = 512;
-constexpr int kWaves = kThreads / kWave;                  // 8
 constexpr int kBM = 256, kBN = 256;                       // tokens x features per tile
-constexpr int kWTN = 64, kWTM = 128;                      // wave tile: features x tokens
-constexpr int kTN = kWTN / 32, kTM = kWTM / 32;           // 2 x 4 MFMA tiles
-constexpr int kLdsBytes = 128 * 1024;                     // the operand ring
 
-// K-slab geometry.  A slab is BK columns of the 256 activation rows and the
-// 256 weight rows; the ring holds STAGES slabs (BK * STAGES = 128).
-template <int BK>
-struct Slab {
-  static constexpr int kRowBytes = BK * 2;                   // LDS row
-  static constexpr int kChunks = kRowBytes / 16;             // 16-byte chunks per row
-  static constexpr int kRowsPerDma = 1024 / kRowBytes;       // rows per 1 KB DMA
-  static constexpr int kStageBytes = (kBM + kBN) * kRowBytes;
-  static constexpr int kDmaPerWave = kStageBytes / 1024 / kWaves;
-  static constexpr int kSteps = BK / 16;                     // MFMA k-steps per slab
-  // LDS bank swizzle: chunk c of row r sits in slot c ^ swz(r).  gfx950 LDS
-  // serves 16 lanes of a 16-byte read per pass over 64 banks (256 bytes):
-  // the 16 rows of one fragment column must land on 16 distinct 16-byte bank
-  // groups, i.e. rows that share (r * kChunks) mod 16 need distinct slots.
-  static constexpr int kSwzDiv = 16 / kChunks;
-  static __device__ __forceinline__ int swz(int r) { return (r / kSwzDiv) & (kChunks - 1); }
+// Wave layout of a block: NW waves as WN (features) x WM (tokens); each wave
+// owns a WTN x WTM tile of TN x TM 32x32 MFMA tiles.
+template <int NW>
+struct Waves {
+  static constexpr int kWaves = NW;
+  static constexpr int kThreads = NW * kWave;
+  static constexpr int WN = NW == 8 ? 4 : 2, WM = 2;
+  static constexpr int WTN = kBN / WN, WTM = kBM / WM;
+  static constexpr int TN = WTN / 32, TM = WTM / 32;
+  static_assert(WN * WM == NW, "wave layout");
 };
 
 typedef __attribute__((address_space(3))) char lds_char;
@@ -145,22 +138,25 @@ __device__ __forceinline__ bool locate_tile(const SegScan& sc, int E, int nbx, i
   return true;
 }
 
-// Epilogue straight from the accumulators of a wave's 64-feature x
-// 128-token tile.  Register v of a 32x32 tile holds feature row
+// Epilogue straight from the accumulators of a wave's WTN-feature x
+// WTM-token tile.  Register v of a 32x32 tile holds feature row
 // 8*(v/4) + 4*(lane/32) + v%4 (four consecutive features per group v/4) and
 // token column lane%32.  Biases are read at wave-uniform addresses (scalar
 // loads): a vector load here would make the compiler wait for the DMA loads
 // it does not track as well.
-template <int EPI>
-__device__ __forceinline__ void store_tile(const f32x16 (&acc)[kTN][kTM], const Tile& cur, int wn,
-                                           int wm, int lrow, int lhalf,
+template <int EPI, int NW>
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Waves<NW>::TM],
+                                           const Tile& cur, int wn, int wm, int lrow, int lhalf,
                                            const float* __restrict__ bias0,
                                            const float* __restrict__ bias1, int n_store,
                                            int bias_ld, bf16_t* __restrict__ out, int ldo) {
-    const int tok_base = cur.row0 + wm * kWTM + lrow;
-    if constexpr (EPI == kEpiGateUp) {
-      // the wave's 64 packed rows are one [32 gate | 32 up] group
-      const int hb = (cur.n0 + wn * kWTN) / 2;
+  using W = Waves<NW>;
+  const int tok_base = cur.row0 + wm * W::WTM + lrow;
+  if constexpr (EPI == kEpiGateUp) {
+    // each 64 packed rows of the wave are one [32 gate | 32 up] group
+#pragma unroll
+    for (int gi = 0; gi < W::TN / 2; ++gi) {
+      const int hb = (cur.n0 + wn * W::WTN) / 2 + 32 * gi;
       const float* bgp = bias0 + (size_t)cur.expert * bias_ld + hb;
       const float* bup = bias1 + (size_t)cur.expert * bias_ld + hb;
       float bg[16], bu[16];
@@ -174,12 +170,12 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[kTN][kTM], const 
           bu[4 * g + q] = lhalf ? u1 : u0;
         }
 #pragma unroll
-      for (int i = 0; i < kTM; ++i) {
+      for (int i = 0; i < W::TM; ++i) {
         const int row = tok_base + i * 32;
         if (row < cur.row_end) {
           bf16_t* orow = out + (size_t)row * ldo + hb + 4 * lhalf;
-          const f32x16& ga = acc[0][i];
-          const f32x16& ua = acc[1][i];
+          const f32x16& ga = acc[2 * gi][i];
+          const f32x16& ua = acc[2 * gi + 1][i];
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int v = 4 * g;
@@ -191,56 +187,61 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[kTN][kTM], const 
           }
         }
       }
-    } else {
+    }
+  } else {
 #pragma unroll
-      for (int j = 0; j < kTN; ++j) {
-        const int cb = cur.n0 + wn * kWTN + j * 32;
-        if (cb >= n_store) continue;   // n_store is a multiple of 64
-        const float* bdp = bias0 + (size_t)cur.expert * bias_ld + cb;
-        float b[16];
+    for (int j = 0; j < W::TN; ++j) {
+      const int cb = cur.n0 + wn * W::WTN + j * 32;
+      if (cb >= n_store) continue;   // n_store is a multiple of 64
+      const float* bdp = bias0 + (size_t)cur.expert * bias_ld + cb;
+      float b[16];
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float b0 = uniform_load(bdp + 8 * g + q), b1 = uniform_load(bdp + 8 * g + 4 + q);
-            b[4 * g + q] = lhalf ? b1 : b0;
-          }
+        for (int q = 0; q < 4; ++q) {
+          const float b0 = uniform_load(bdp + 8 * g + q), b1 = uniform_load(bdp + 8 * g + 4 + q);
+          b[4 * g + q] = lhalf ? b1 : b0;
+        }
 #pragma unroll
-        for (int i = 0; i < kTM; ++i) {
-          const int row = tok_base + i * 32;
-          if (row < cur.row_end) {
-            bf16_t* orow = out + (size_t)row * ldo + cb + 4 * lhalf;
-            const f32x16& a = acc[j][i];
+      for (int i = 0; i < W::TM; ++i) {
+        const int row = tok_base + i * 32;
+        if (row < cur.row_end) {
+          bf16_t* orow = out + (size_t)row * ldo + cb + 4 * lhalf;
+          const f32x16& a = acc[j][i];
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-              *reinterpret_cast<uint2*>(orow + 8 * g) =
-                  pack4_bf16(a[4 * g + 0] + b[4 * g + 0], a[4 * g + 1] + b[4 * g + 1],
-                             a[4 * g + 2] + b[4 * g + 2], a[4 * g + 3] + b[4 * g + 3]);
-          }
+          for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<uint2*>(orow + 8 * g) =
+                pack4_bf16(a[4 * g + 0] + b[4 * g + 0], a[4 * g + 1] + b[4 * g + 1],
+                           a[4 * g + 2] + b[4 * g + 2], a[4 * g + 3] + b[4 * g + 3]);
         }
       }
     }
+  }
 }
 
-// The operand stream is a sequence of slabs (tile, kt) over the tiles this
-// block owns.  A DMA cursor runs STAGES-1 slabs ahead of the MFMA consumer,
-// crossing tile boundaries, so the ring never drains between tiles.  Needs
-// K / BK >= STAGES - 1 (the cursor is then at most one tile ahead) and an
-// even number of 16-wide k-steps per slab.
-template <int EPI, int BK, int STAGES>
-__global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
+// ---------------------------------------------------------------------------
+// Split ring.  LDS holds 5 units of 32 KB, a unit being the 256 activation
+// rows or the 256 weight rows of one 64-column slab (128-byte rows, as in
+// the whole design).  Units are loaded in the order A0 B0 A1 B1 ...; slab s
+// reads units 2s and 2s+1, and barrier B_s frees the two units of slab s-1
+// and refills them with units 2s+3 (weights of slab s+1) and 2s+4
+// (activations of slab s+2): the activations are requested two slabs ahead
+// and the weights one (a 2-stage ring of 64 KB slabs manages one for both).
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
     int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo) {
-  using S = Slab<BK>;
-  static_assert(STAGES * S::kStageBytes == kLdsBytes, "ring size");
-  static_assert(S::kDmaPerWave * S::kRowsPerDma * 4 == kBM, "four waves per operand");
-  __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+  using W = Waves<8>;
+  constexpr int kTN = W::TN, kTM = W::TM;
+  constexpr int kUnits = 5;
+  constexpr int kRowBytes = 128;
+  constexpr int kUnit = 256 * kRowBytes;          // 32 KB
+  constexpr int kDmaPerWave = kUnit / 1024 / 8;   // 4
+  __shared__ __attribute__((aligned(1024))) char smem[kUnits * kUnit];
 
   const int nbx = Npad / kBN;
   const int G = gridDim.x;
-  // Blocks are dispatched round-robin over the 8 XCDs; give the blocks of
-  // one XCD consecutive tile indices in every round.
   int t = (G % kNumXcd == 0) ? (blockIdx.x % kNumXcd) * (G / kNumXcd) + blockIdx.x / kNumXcd
                              : blockIdx.x;
   SegScan sc;
@@ -250,92 +251,97 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave), lane = lane_id();
-  const int wn = w & 3, wm = w >> 2;                      // 4 (features) x 2 (tokens)
+  const int wn = w % W::WN, wm = w / W::WN;
   const int lrow = lane & 31, lhalf = lane >> 5;
   const size_t row_bytes_g = (size_t)K * 2;
-  const int KT = K / BK;
+  const int KT = K / 64;
 
-  // DMA: waves 0-3 fill the activation rows 0..255 of a stage, waves 4-7 the
-  // weight rows 256..511, 64 rows per wave in kDmaPerWave 1 KB blocks.  Lane
-  // l of block i covers row r = 64*(w&3) + i*kRowsPerDma + l/kChunks, slot
-  // l%kChunks, and so loads logical chunk slot ^ swz(r) of that row.
-  uint32_t lane_off[S::kDmaPerWave];
+  // DMA of a unit: wave w fills its rows 32w .. 32w+31 in 4 blocks of 8
+  // rows; lane l covers row r = 8i + l/8, slot l%8 = chunk ^ ((r >> 1) & 7).
+  uint32_t lane_off[2];
 #pragma unroll
-  for (int i = 0; i < S::kDmaPerWave; ++i) {
-    const int r = i * S::kRowsPerDma + lane / S::kChunks;   // within the wave's 64 rows
-    const int c = (lane % S::kChunks) ^ S::swz(r);          // 64*(w&3) keeps swz(r)
-    lane_off[i] = (uint32_t)r * (uint32_t)row_bytes_g + (uint32_t)(c * 16);
+  for (int i = 0; i < 2; ++i) {
+    const int r = i * 8 + lane / 8;
+    lane_off[i] = (uint32_t)(lane / 8) * (uint32_t)row_bytes_g +
+                  (uint32_t)((((lane % 8) ^ ((r >> 1) & 7))) * 16);
   }
-  auto dma_base = [&](const Tile& tl) -> const char* {
-    const char* p = (w < 4) ? reinterpret_cast<const char*>(A + (size_t)tl.row0 * K)
-                            : reinterpret_cast<const char*>(B + ((size_t)tl.expert * Npad + tl.n0) * K);
-    return p + (size_t)((w & 3) * 64) * row_bytes_g;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)smem + (uint32_t)(w * kDmaPerWave * 1024);
+  auto abase = [&](const Tile& tl) -> const char* {
+    return reinterpret_cast<const char*>(A + ((size_t)tl.row0 + 32 * w) * K);
   };
-  const uint32_t lds_base =
-      (uint32_t)(uintptr_t)(lds_char*)smem + (uint32_t)(w * S::kDmaPerWave * 1024);
-  auto dma = [&](const char* gbase, int kt, int stage) __attribute__((always_inline)) {
-    const uint32_t dst = lds_base + (uint32_t)(stage * S::kStageBytes);
-    const char* g = gbase + (size_t)kt * S::kRowBytes;
-#pragma unroll
-    for (int i = 0; i < S::kDmaPerWave; ++i) dma16(g + lane_off[i], dst + i * 1024);
+  auto bbase = [&](const Tile& tl) -> const char* {
+    return reinterpret_cast<const char*>(B + ((size_t)tl.expert * Npad + tl.n0 + 32 * w) * K);
   };
 
-  // Fragment rows start at multiples of 32, so swz(row) = swz(lrow).
-  int x_off[kTM], w_off[kTN];
-#pragma unroll
-  for (int i = 0; i < kTM; ++i) x_off[i] = (wm * kWTM + i * 32 + lrow) * S::kRowBytes;
-#pragma unroll
-  for (int j = 0; j < kTN; ++j) w_off[j] = (kBM + wn * kWTN + j * 32 + lrow) * S::kRowBytes;
-  const int swz = S::swz(lrow);
-
-  // DMA cursor: the next slab to load (tile dtile, column block dkt) and
-  // its ring stage.
+  // Cursor over units: (tile dtile, slab dkt, operand dop), ring slot dslot.
   Tile dtile = cur;
-  int dt = t, dkt = 0, dstage = 0;
+  int dt = t, dkt = 0, dop = 0, dslot = 0;
   bool dvalid = true;
-  const char* dg = dma_base(cur);
-  int ahead = 0;   // slabs issued after the newest slab known to have landed
+  const char* dga = abase(cur);
+  const char* dgb = bbase(cur);
+  int ahead = 0;   // units issued and not yet waited for
   auto advance = [&]() __attribute__((always_inline)) {
     if (dvalid) {
-      dma(dg, dkt, dstage);
+      const char* g = (dop ? dgb : dga) + (size_t)dkt * kRowBytes;
+      const uint32_t dst = lds_base + (uint32_t)(dslot * kUnit);
+#pragma unroll
+      for (int i = 0; i < kDmaPerWave; ++i)
+        dma16(g + (size_t)(i * 8) * row_bytes_g + lane_off[i & 1], dst + i * 1024);
       ++ahead;
     }
-    dstage = dstage + 1 == STAGES ? 0 : dstage + 1;
-    if (++dkt == KT) {
-      dkt = 0;
-      dt += G;
-      if (dvalid) dvalid = locate_tile(sc, E, nbx, dt, &dtile);
-      if (dvalid) dg = dma_base(dtile);
+    dslot = dslot + 1 == kUnits ? 0 : dslot + 1;
+    if (dop == 0) {
+      dop = 1;
+    } else {
+      dop = 0;
+      if (++dkt == KT) {
+        dkt = 0;
+        dt += G;
+        if (dvalid) dvalid = locate_tile(sc, E, nbx, dt, &dtile);
+        if (dvalid) {
+          dga = abase(dtile);
+          dgb = bbase(dtile);
+        }
+      }
     }
   };
-  // Barrier B_c before the first fragment read of slab c: slab c has landed
-  // (the slabs issued after it may still be in flight: `ahead` of them), and
-  // every wave has finished reading slab c-1, whose stage the DMA issued
-  // right after the barrier refills.
+  // B_s: units 2s and 2s+1 landed with unit 2s+2 possibly in flight; all
+  // waves done with slab s-1, whose two units are then refilled.
   auto next_slab_barrier = [&]() __attribute__((always_inline)) {
-    --ahead;
-    if (ahead == STAGES - 2) slab_barrier<(STAGES - 2) * S::kDmaPerWave>();
+    ahead -= 2;
+    if (ahead >= 1) slab_barrier<kDmaPerWave>();
     else slab_barrier<0>();
+    advance();
     advance();
   };
 
+  const int x_row = (wm * W::WTM + lrow) * kRowBytes;
+  const int w_row = (wn * W::WTN + lrow) * kRowBytes;
+  const int swz = (lrow >> 1) & 7;
   bf16x8 xf[2][kTM], wf[2][kTN];
-  auto frags = [&](int stage, int ks, bf16x8 (&xs)[kTM], bf16x8 (&ws)[kTN])
+  // k-step ks of the slab whose activation unit is in ring slot `aslot`
+  // (its weight unit follows in the next slot)
+  auto frags = [&](int aslot, int ks, bf16x8 (&xs)[kTM], bf16x8 (&ws)[kTN])
       __attribute__((always_inline)) {
-    const char* st = smem + stage * S::kStageBytes;
+    const int bslot = aslot + 1 == kUnits ? 0 : aslot + 1;
+    const char* sa = smem + aslot * kUnit + x_row;
+    const char* sb = smem + bslot * kUnit + w_row;
     const int cofs = (((ks * 2 + lhalf) ^ swz) << 4);
 #pragma unroll
-    for (int i = 0; i < kTM; ++i) xs[i] = *reinterpret_cast<const bf16x8*>(st + x_off[i] + cofs);
+    for (int i = 0; i < kTM; ++i)
+      xs[i] = *reinterpret_cast<const bf16x8*>(sa + i * 32 * kRowBytes + cofs);
 #pragma unroll
-    for (int j = 0; j < kTN; ++j) ws[j] = *reinterpret_cast<const bf16x8*>(st + w_off[j] + cofs);
+    for (int j = 0; j < kTN; ++j)
+      ws[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRowBytes + cofs);
   };
 
-#pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s) advance();
-  ++ahead;   // B_0 consumes slab 0
+  // Prologue: units 0, 1, 2 (A0 B0 A1).
+  advance();
+  advance();
+  advance();
   next_slab_barrier();
   frags(0, 0, xf[0], wf[0]);
-  int cstage = 0;
+  int aslot = 0;
 
   for (;;) {
     Tile nxt;
@@ -348,21 +354,19 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][i][v] = 0.0f;
 
-    // Fragments run one k-step ahead of the MFMAs, across slab (and tile)
-    // boundaries: the reads of slab c+1's first k-step overlap the MFMAs of
-    // slab c's last one.  S::kSteps is even, so k-step s uses buffer s & 1.
     for (int kt = 0; kt < KT; ++kt) {
 #pragma unroll
-      for (int ks = 0; ks < S::kSteps; ++ks) {
-        if (ks + 1 < S::kSteps) {
-          frags(cstage, ks + 1, xf[(ks + 1) & 1], wf[(ks + 1) & 1]);
+      for (int ks = 0; ks < 4; ++ks) {
+        if (ks + 1 < 4) {
+          frags(aslot, ks + 1, xf[(ks + 1) & 1], wf[(ks + 1) & 1]);
         } else {
-          // Next slab (after the block's last one this reads a stale stage
-          // whose values are never used: one code path keeps the compiler's
-          // LDS wait counting exact).
-          cstage = cstage + 1 == STAGES ? 0 : cstage + 1;
+          // next slab; after the block's last slab this reads stale units
+          // whose values are never used (one code path keeps the compiler's
+          // LDS wait counting exact)
+          aslot += 2;
+          if (aslot >= kUnits) aslot -= kUnits;
           next_slab_barrier();
-          frags(cstage, 0, xf[0], wf[0]);
+          frags(aslot, 0, xf[0], wf[0]);
         }
 #pragma unroll
         for (int j = 0; j < kTN; ++j)
@@ -370,10 +374,6 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
           for (int i = 0; i < kTM; ++i)
             acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][j], xf[ks & 1][i],
                                                                 acc[j][i], 0, 0, 0);
-        // Issue order: the next k-step's six fragment reads one per MFMA
-        // from the start, so their latency hides under this k-step's MFMAs
-        // (left alone, the scheduler sinks them to the end to reuse
-        // registers).
 #pragma unroll
         for (int q = 0; q < kTM + kTN; ++q) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
@@ -382,22 +382,21 @@ __global__ __launch_bounds__(kThreads) void gemm_dma_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, kTM * kTN - (kTM + kTN), 0);
       }
     }
-
-    store_tile<EPI>(acc, cur, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out, ldo);
+    store_tile<EPI, 8>(acc, cur, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out, ldo);
     if (!have_next) break;
     t += G;
     cur = nxt;
   }
 }
 
-
 }  // namespace
 
 // Persistent launch: one block per CU (the kernel walks the tiles itself).
-// max_mtiles bounds sum_e ceil(count_e / 256); it only caps the grid.  The
-// ring is 2 slabs of 64 columns: measured on MI355X, halving the barriers
-// beats a deeper ring of 32-column slabs (4 x 32: 898 TFLOP/s, 2 x 64: 1036
-// TFLOP/s on the cfg3 gate/up shape).
+// max_mtiles bounds sum_e ceil(count_e / 256); it only caps the grid.
+// Measured on MI355X (cfg3 shapes, skewed counts): the split 5-unit ring
+// (gate/up 1035, down 871 TFLOP/s) beats a 2-slab ring of 64 KB slabs
+// (1034, 827) and 32-column slabs (4 x 32: 938, 724; 5 x 32 with 2 per
+// barrier: 970, 786), whose 64-byte row segments double the DMA cost.
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                            const float* bias1, const int32_t* counts, int E, int K, int Npad,
@@ -414,8 +413,8 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
   }
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
-  hipLaunchKernelGGL((gemm_dma_kernel<EPI, 64, 2>), dim3(grid), dim3(kThreads), 0, stream, A, B,
-                     bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo);
+  hipLaunchKernelGGL((gemm_ring5_kernel<EPI>), dim3(grid), dim3(8 * kWave), 0, stream, A, B, bias0,
+                     bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo);
   return hipGetLastError();
 }
 
