@@ -52,7 +52,11 @@ struct alignas(16) V16 {
   uint32_t w[4];
 };
 
-// One block per router block (TB tokens = TB*k flat ids).
+// One block per (router block of TB tokens = TB*k flat ids, column slice):
+// every slice ranks the block's ids (cheap), slice 0 writes perm/slot_of,
+// and each slice copies its share of the row bytes.  Slices only matter for
+// few tokens (decode shapes), where one block per 64 tokens would leave the
+// GPU idle.
 template <typename ActT>
 __global__ __launch_bounds__(256) void permute_kernel(
     const ActT* __restrict__ x, const int32_t* __restrict__ topk_idx,
@@ -64,6 +68,7 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __shared__ int s_slot[kRouterTokens * kMaxTopK];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
+  const bool writer = blockIdx.y == 0;
   const int TB = router_tokens_per_block(E);
   const int tok0 = b * TB;
   const int ntok = min(TB, N - tok0);
@@ -103,27 +108,42 @@ __global__ __launch_bounds__(256) void permute_kernel(
         const int rank = run + __popcll(match & lt);
         const int slot = s_base[e] + rank;
         s_slot[f] = slot;
-        perm[slot] = (int32_t)(flat0 + f);
-        slot_of[flat0 + f] = slot;
+        if (writer) {
+          perm[slot] = (int32_t)(flat0 + f);
+          slot_of[flat0 + f] = slot;
+        }
         // The highest lane of each expert group advances the running count.
         if ((match >> l) == 1ull) s_run[e] = run + __popcll(match);
       }
     }
   }
   __syncthreads();
-  // Row copy: wave w handles tokens w, w+4, ...; 16-byte chunks across lanes.
+  // Row copy of this slice's 16-byte chunks [q0, q1): wave w handles tokens
+  // w, w+4, ..., four tokens per step so that four loads are in flight
+  // before their k stores each.
   const int w = tid / kWave;
   const int l = lane_id();
   const int chunks = C * (int)sizeof(ActT) / 16;
-  for (int r = w; r < ntok; r += 4) {
-    const V16* src = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C);
-    for (int q = l; q < chunks; q += kWave) {
-      const V16 v = src[q];
-      for (int j = 0; j < k; ++j) {
-        const int slot = s_slot[r * k + j];
-        if (slot < 0) continue;
-        V16* dst = reinterpret_cast<V16*>(xg + (size_t)slot * C);
-        dst[q] = v;
+  const int q0 = (int)((long)blockIdx.y * chunks / gridDim.y);
+  const int q1 = (int)((long)(blockIdx.y + 1) * chunks / gridDim.y);
+  constexpr int U = 4;
+  for (int r0 = w; r0 < ntok; r0 += 4 * U) {
+    for (int q = q0 + l; q < q1; q += kWave) {
+      V16 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = min(r0 + 4 * u, ntok - 1);
+        v[u] = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C)[q];
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int r = r0 + 4 * u;
+        if (r >= ntok) break;
+        for (int j = 0; j < k; ++j) {
+          const int slot = s_slot[r * k + j];
+          if (slot < 0) continue;
+          reinterpret_cast<V16*>(xg + (size_t)slot * C)[q] = v[u];
+        }
       }
     }
   }
@@ -144,8 +164,11 @@ hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t*
   const int TB = router_tokens_per_block(E);
   const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
-  hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb), dim3(256), 0, stream, x, topk_idx, counts,
-                     base, nb, N, C, E, k, perm, slot_of, xg);
+  // Column slices: enough blocks for ~512 in all, each slice >= 64 chunks.
+  const int chunks = C * (int)sizeof(ActT) / 16;
+  const int slices = max(1, min(chunks / 64, (512 + nb - 1) / nb));
+  hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb, slices), dim3(256), 0, stream, x, topk_idx,
+                     counts, base, nb, N, C, E, k, perm, slot_of, xg);
   return hipGetLastError();
 }
 

@@ -25,8 +25,8 @@
 namespace mgpt {
 // kernels (router.hip, dispatch.hip, gemm.hip, combine.hip, pack.hip)
 template <typename ActT>
-hipError_t launch_router(const ActT*, const float*, const float*, int, int, int, int, int32_t*,
-                         float*, int32_t*, hipStream_t);
+hipError_t launch_router(const ActT*, const float*, const float*, const float*, int, int, int,
+                         int, int32_t*, float*, int32_t*, float*, hipStream_t);
 hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
 hipError_t launch_expert_scan(const int32_t*, int, int, int32_t*, int32_t*, hipStream_t);
 template <typename ActT>
@@ -43,7 +43,7 @@ template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
-hipError_t launch_pack_router(const float*, int, int, float*, hipStream_t);
+hipError_t launch_pack_router(const float*, int, int, int, float*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
                            const int32_t*, int, int, int, int, int, bf16_t*, int, int,
@@ -81,7 +81,7 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 struct Layout {
-  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, xg, hbuf, obuf, total;
+  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, total;
 };
 
 }  // namespace
@@ -92,6 +92,7 @@ struct mgpt_moe {
   int device;
   int gemm_tile = 256;     // block tile of the large-M bf16 GEMMs (256 or 128)
   float* wr_g = nullptr;   // router weights [G][C][RE] (router_experts_per_wave)
+  float* wr1 = nullptr;    // router weights [E][C] (split decode router, E > 16)
   float* br = nullptr;     // [E]
   void* wgu = nullptr;     // [E][2Hp][C] of bf16 / fp8 / f32
   void* wd = nullptr;      // [E][Cp][Hp]
@@ -112,6 +113,9 @@ struct mgpt_moe {
   const int32_t* last_counts = nullptr;
 
   size_t act_bytes() const { return act == MGPT_DTYPE_BF16 ? 2 : 4; }
+  // Few tokens and many experts: the router's logits are spread over more
+  // blocks (one expert per wave) instead of one block per 64 tokens.
+  bool router_split(int N) const { return E > 16 && N < 4096; }
   size_t w_bytes() const { return wdt == MGPT_DTYPE_FP8_E4M3 ? 1 : (wdt == MGPT_DTYPE_BF16 ? 2 : 4); }
   // h (SwiGLU output) is kept in the activation dtype.
   Layout layout(int N) const {
@@ -132,6 +136,7 @@ struct mgpt_moe {
     L.hist = take(nb * E * 4);
     L.base = take(nb * E * 4);
     L.counts = take((size_t)E * 4);
+    L.logits = take(router_split(N) ? (size_t)N * E * 4 : 0);
     L.xg = take((A + kRowPad) * C * act_bytes());
     L.hbuf = take((A + kRowPad) * Hp * act_bytes());
     L.obuf = take((A + kRowPad) * C * act_bytes());
@@ -166,10 +171,10 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_g, h->br, h->wgu, h->wd, h->sgu, h->sd, h->bg, h->bu, h->bd};
+  void* ptrs[] = {h->wr_g, h->wr1, h->br, h->wgu, h->wd, h->sgu, h->sd, h->bg, h->bu, h->bd};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  h->wr_g = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
+  h->wr_g = h->wr1 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
   h->wgu = h->wd = nullptr;
   h->loaded = false;
 }
@@ -244,6 +249,7 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   const bool bf = h->wdt == MGPT_DTYPE_BF16;
   const int RE = router_experts_per_wave(E);
   HIP_TRY(hipMalloc(&h->wr_g, sizeof(float) * ((E + RE - 1) / RE) * RE * C));
+  if (E > 16) HIP_TRY(hipMalloc(&h->wr1, sizeof(float) * E * C));
   HIP_TRY(hipMalloc(&h->br, sizeof(float) * E));
   HIP_TRY(hipMalloc(&h->wgu, wb * E * 2 * Hp * C));
   HIP_TRY(hipMalloc(&h->wd, wb * E * Cp * Hp));
@@ -292,7 +298,8 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   do {
     const float* s = src(0, (size_t)C * E);
     if (!s) break;
-    if (launch_pack_router(s, C, E, h->wr_g, st) != hipSuccess) {
+    if (launch_pack_router(s, C, E, RE, h->wr_g, st) != hipSuccess ||
+        (h->wr1 && launch_pack_router(s, C, E, 1, h->wr1, st) != hipSuccess)) {
       rc = fail(MGPT_ERR_HIP, "router pack failed");
       break;
     }
@@ -380,7 +387,8 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
   HIP_TRY(mark(0));
-  HIP_TRY(launch_router<ActT>(x, h->wr_g, h->br, N, C, E, k, idx, topp, hist, st));
+  float* logits = h->router_split(N) ? (float*)(ws + L.logits) : nullptr;
+  HIP_TRY(launch_router<ActT>(x, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits, st));
   HIP_TRY(mark(1));
   HIP_TRY(launch_expert_scan(hist, nb, E, base, counts, st));
   HIP_TRY(mark(2));

@@ -100,8 +100,10 @@ __global__ void pack_router_kernel(const float* __restrict__ wr, int C, int E, i
 
 }  // namespace
 
-hipError_t launch_pack_router(const float* wr, int C, int E, float* out, hipStream_t stream) {
-  const int RE = router_experts_per_wave(E);
+// RE experts per wave group; the fused router uses router_experts_per_wave(E),
+// the split decode path RE = 1 (W_r transposed).
+hipError_t launch_pack_router(const float* wr, int C, int E, int RE, float* out,
+                              hipStream_t stream) {
   const int total = ((E + RE - 1) / RE) * C * RE;
   hipLaunchKernelGGL(pack_router_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, wr, C,
                      E, RE, out, total);

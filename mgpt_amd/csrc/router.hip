@@ -11,13 +11,15 @@
 // c = 0..C-1 in order with one rounded product and one rounded add per term
 // (the file is built with -ffp-contract=off), so every logit has exactly the
 // reference's rounding sequence; MFMA cannot be used here, its internal
-// accumulation order differs.  The weights of a wave are wave-uniform and
-// come through the scalar cache.  Phase 2: per-token max (strict '>' from
+// accumulation order differs.  The weights of a wave are wave-uniform
+// (broadcast loads).  Phase 2: per-token max (strict '>' from
 // element 0, as the reference, so NaN handling matches), the exponentials
 // in parallel with glibc's expf algorithm, then per token the sequential
 // sum, the clamp and the insertion top-k in registers.  Phase 3: block-local
 // expert histogram (LDS atomics on ints; counts are order-free), written
 // expert-major as hist[e][block] for the per-expert scan of dispatch.hip.
+// Decode shapes (few tokens, E > 16) split phase 1 over more blocks, one
+// expert per wave, through a logits buffer.
 #include "common.hpp"
 #include "glibc_expf.hpp"
 
@@ -65,72 +67,168 @@ __device__ __forceinline__ void softmax_topk_token(const float* __restrict__ ex,
   }
 }
 
-template <typename ActT> struct Load8;
-template <> struct Load8<bf16_t> {
-  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-    }
-  }
-};
-template <> struct Load8<float> {
-  static __device__ __forceinline__ void load(const float* p, float (&v)[8]) {
-    const float4 a = *reinterpret_cast<const float4*>(p);
-    const float4 b = *reinterpret_cast<const float4*>(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-  }
-};
+// Element i of a 16-byte row unit, widened to fp32 (bf16: a shift or a
+// mask; fp32: as is).
+template <typename ActT>
+__device__ __forceinline__ float widen(const uint4& q, int i);
+template <>
+__device__ __forceinline__ float widen<bf16_t>(const uint4& q, int i) {
+  const uint32_t w = (i < 2) ? q.x : (i < 4) ? q.y : (i < 6) ? q.z : q.w;
+  return __uint_as_float((i & 1) ? (w & 0xFFFF0000u) : (w << 16));
+}
+template <>
+__device__ __forceinline__ float widen<float>(const uint4& q, int i) {
+  return __uint_as_float((i == 0) ? q.x : (i == 1) ? q.y : (i == 2) ? q.z : q.w);
+}
 
-// Wave-uniform router weights.  A block owns 64 tokens (one per lane) and
-// E/RE waves; wave g computes experts [g*RE, g*RE + RE) for all 64 tokens.
-// Its slice of W_r is the same for every lane, so it is read with scalar
-// loads into SGPRs (packed as [G][C][RE], 8*RE consecutive floats per 8 c),
-// and each lane streams only its own token's row of x with 16-byte loads:
-// no per-lane copies of the weights, no LDS and no barrier in the loop.
-// Each logit accumulates c = 0, 1, ... in order, one rounded product and one
-// rounded add per term (built with -ffp-contract=off), then the bias.
+typedef __attribute__((address_space(3))) char lds_char;
+
+// One 1 KB direct-to-LDS load (lane l's 16 bytes at g land at lds + 16*l),
+// as inline asm the compiler does not track; the caller waits for it.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
+
+// All of this wave's loads landed and its LDS accesses completed, then the
+// workgroup barrier.
+__device__ __forceinline__ void drain_barrier() {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// LDS budget of the logit stage: two buffers of (x chunk + weight chunk).
+constexpr int kRouterLds = 96 * 1024;
+
+// LDS bytes of one group's weight chunk: whole 1 KB DMA blocks.
+__device__ __forceinline__ int wgroup_bytes(int CB, int RE) { return max(CB * RE * 4, 1024); }
+
+// Columns per chunk: the largest power of two >= 64 whose two stages fit.
+template <typename ActT>
+__device__ __forceinline__ int chunk_cols(int nw, int RE) {
+  auto stage = [&](int cb) { return kRT * cb * (int)sizeof(ActT) + nw * wgroup_bytes(cb, RE); };
+  int CB = 64;
+  while (2 * stage(2 * CB) <= kRouterLds) CB *= 2;
+  return CB;
+}
+
+// The logits of experts [g*RE, g*RE + RE) for the block's 64 tokens (one
+// per lane), computed by the nw waves of a block (all threads call this;
+// the weights of groups past g_valid are not loaded and those waves'
+// results are garbage).  xblk is the block's first token row (rows past
+// the last token, n_rows, re-read the last one); wsrc is packed [G][C][RE]
+// from the block's first group on.
+//
+// Both operands are staged through LDS in column chunks, double-buffered
+// and requested one chunk ahead with direct-to-LDS loads: every lane reads
+// its own token row, so reading x straight from memory would touch 64
+// cache lines per load instruction in every wave of the block (the load
+// pipeline, not the VALU, bound that design); staged, each row is fetched
+// once per block with whole-line loads.  Row units are swizzled (unit u of
+// row r at slot u ^ (r & 15)) so the 16 rows read together hit 16 bank
+// groups; the weights are the same for every lane of a wave (broadcast
+// reads).  Each logit accumulates c = 0, 1, ... in order, one rounded
+// product and one rounded add per term (built with -ffp-contract=off); the
+// caller adds the bias.
 template <typename ActT, int RE>
-__global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
-    const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
-    int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
-    int32_t* __restrict__ hist, int num_blocks) {
-  __shared__ float s_l[kRT][kMaxExperts + 1];
-  __shared__ float s_m[kRT];
-  __shared__ int s_hist[kMaxExperts];
-
-  const int tid = threadIdx.x;
+__device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int n_rows,
+                                             const float* __restrict__ wsrc, int g_valid, int nw,
+                                             int g, int C, char* smem, float (&acc)[RE]) {
+  constexpr int kPer = 16 / (int)sizeof(ActT);   // columns per 16-byte unit
+  const int CB = chunk_cols<ActT>(nw, RE);
+  const int xrow_bytes = CB * (int)sizeof(ActT);   // LDS bytes per token row
+  const int x_bytes = kRT * xrow_bytes;
+  const int wgb = wgroup_bytes(CB, RE);
+  const int w_bytes = nw * wgb;
+  const int stage_bytes = x_bytes + w_bytes;
   const int lane = lane_id();
-  const int g = __builtin_amdgcn_readfirstlane(tid / kWave);   // expert group of this wave
-  const int tok0 = blockIdx.x * kRT;
-  if (tid < kMaxExperts) s_hist[tid] = 0;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)smem;
+  const size_t xrow_g = (size_t)C * sizeof(ActT);
 
-  const ActT* xrow = x + (size_t)min(tok0 + lane, N - 1) * C;   // rows past N: never stored
-  const float* wg = wr_g + (size_t)g * C * RE;
+  // One chunk [c0, c0 + cnum) into stage b.  x: 1 KB blocks of whole rows
+  // segments (xrow_bytes is a multiple of 128), lane l -> row
+  // (blk*1024 + 16l) / xrow_bytes, slot s -> logical unit s ^ (row & 15).
+  // Weights: group gg's cnum*RE floats in 1 KB blocks at a 1 KB-aligned
+  // group stride; lanes past a partial block re-read the group's first
+  // bytes (in bounds, never used).
+  auto chunk_dma = [&](int c0, int cnum, int b) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (uint32_t)(b * stage_bytes);
+    const int units_row = cnum * (int)sizeof(ActT) / 16;   // valid units per row
+    const int x_blocks = x_bytes / 1024;
+    for (int q = g; q < x_blocks; q += nw) {
+      const int byte = q * 1024 + lane * 16;
+      const int row = byte / xrow_bytes, slot = (byte % xrow_bytes) / 16;
+      int unit = slot ^ (row & 15);
+      if (unit >= units_row) unit = 0;
+      const char* src = reinterpret_cast<const char*>(xblk) +
+                        (size_t)min(row, n_rows - 1) * xrow_g + (size_t)c0 * sizeof(ActT) +
+                        unit * 16;
+      dma16(src, st + (uint32_t)(q * 1024));
+    }
+    const int gbytes = cnum * RE * 4;
+    const int gblocks = (gbytes + 1023) / 1024;
+    for (int q = g; q < g_valid * gblocks; q += nw) {
+      const int gg = q / gblocks, bk = q - gg * gblocks;
+      const char* src = reinterpret_cast<const char*>(wsrc + ((size_t)gg * C + c0) * RE);
+      const int off = bk * 1024 + lane * 16;
+      dma16(src + (off < gbytes ? off : 0), st + (uint32_t)(x_bytes + gg * wgb + bk * 1024));
+    }
+  };
 
-  float acc[RE];
 #pragma unroll
   for (int j = 0; j < RE; ++j) acc[j] = 0.0f;
-#pragma unroll 2
-  for (int c = 0; c < C; c += 8) {
-    float xv[8];
-    Load8<ActT>::load(xrow + c, xv);
-    const float* wc = wg + (size_t)c * RE;
+  constexpr int kWU = kPer * RE / 4;   // float4 of weights per unit
+  int b = 0;
+  chunk_dma(0, min(CB, C), 0);
+  for (int c0 = 0; c0 < C; c0 += CB) {
+    const int cnum = min(CB, C - c0);
+    drain_barrier();   // chunk c0 landed; every wave done with the other stage
+    if (c0 + CB < C) chunk_dma(c0 + CB, min(CB, C - c0 - CB), b ^ 1);
+    const char* st = smem + b * stage_bytes;
+    const char* xr = st + lane * xrow_bytes;
+    const float* wq = reinterpret_cast<const float*>(st + x_bytes + g * wgb);
+    const int units = cnum / kPer;
+    // operands of unit u+1 are read while unit u is multiplied
+    uint4 x0, x1;
+    float4 w0[kWU], w1[kWU];
+    auto rd = [&](int u, uint4& xv, float4 (&wv)[kWU]) __attribute__((always_inline)) {
+      xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc)
+      for (int v = 0; v < kWU; ++v) wv[v] = reinterpret_cast<const float4*>(wq + u * kPer * RE)[v];
+    };
+    auto mul_add = [&](const uint4& xv, const float4 (&wv)[kWU]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int j = 0; j < RE; ++j) acc[j] = acc[j] + xv[cc] * wc[cc * RE + j];
+      for (int v = 0; v < kWU; ++v) {
+        const float w4[4] = {wv[v].x, wv[v].y, wv[v].z, wv[v].w};
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int idx = 4 * v + e4;   // = column * RE + expert
+          acc[idx % RE] = acc[idx % RE] + widen<ActT>(xv, idx / RE) * w4[e4];
+        }
+      }
+    };
+    rd(0, x0, w0);
+    for (int u = 0; u < units; u += 2) {   // units is even (cnum % 64 == 0)
+      rd(u + 1, x1, w1);
+      mul_add(x0, w0);
+      if (u + 2 < units) rd(u + 2, x0, w0);
+      mul_add(x1, w1);
+    }
+    b ^= 1;
   }
-#pragma unroll
-  for (int j = 0; j < RE; ++j) {
-    const int e = g * RE + j;
-    if (e < E) s_l[lane][e] = acc[j] + br[e];
-  }
-  __syncthreads();
+  drain_barrier();   // the block may reuse the LDS after this
+}
+
+// Softmax, top-k and the block histogram of kRT tokens whose logits are in
+// s_l (all threads of the block call it).  Per token: max with strict '>'
+// from element 0 (as the reference, so NaN handling matches), the
+// exponentials in parallel with glibc's expf algorithm, then the sequential
+// sum, the clamp and the insertion top-k.  The histogram counts are written
+// expert-major as hist[e][block].
+__device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1], float* s_m,
+                                                   int* s_hist, int tok0, int N, int E, int k,
+                                                   int32_t* __restrict__ topk_idx,
+                                                   float* __restrict__ topk_p,
+                                                   int32_t* __restrict__ hist, int num_blocks) {
+  const int tid = threadIdx.x;
   if (tid < kRT) {
     float m = s_l[tid][0];
     for (int v = 1; v < E; ++v)
@@ -165,14 +263,96 @@ __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
   if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
 }
 
+// Fused router: a block owns kRT tokens (one per lane) and ceil(E/RE) waves;
+// wave g computes experts [g*RE, g*RE + RE) into LDS, then the block runs
+// softmax, top-k and its histogram.
+template <typename ActT, int RE>
+__global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
+    int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
+    int32_t* __restrict__ hist, int num_blocks) {
+  __shared__ float s_l[kRT][kMaxExperts + 1];
+  __shared__ float s_m[kRT];
+  __shared__ int s_hist[kMaxExperts];
+  __shared__ __attribute__((aligned(1024))) char smem[kRouterLds];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int g = __builtin_amdgcn_readfirstlane(tid / kWave);   // expert group of this wave
+  const int nw = blockDim.x / kWave;
+  const int tok0 = blockIdx.x * kRT;
+  if (tid < kMaxExperts) s_hist[tid] = 0;
+  float acc[RE];
+  logit_chains<ActT, RE>(x + (size_t)tok0 * C, N - tok0, wr_g, nw, nw, g, C, smem, acc);
+#pragma unroll
+  for (int j = 0; j < RE; ++j) {
+    const int e = g * RE + j;
+    if (e < E) s_l[lane][e] = acc[j] + br[e];
+  }
+  __syncthreads();
+  softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks);
+}
+
+// Few tokens, many experts (decode shapes): the fused kernel would run a
+// handful of blocks whose waves each walk RE experts.  Here a block of
+// kSplitExperts waves computes that many experts' logits (one each; wr1 =
+// W_r transposed, [E][C]) for 64 tokens, written to global memory, and
+// router_softmax_kernel finishes: the chains are as long as before, but
+// spread over more CUs.
+constexpr int kSplitExperts = 4;
+template <typename ActT>
+__global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr1, const float* __restrict__ br,
+    int N, int C, int E, float* __restrict__ logits) {
+  __shared__ __attribute__((aligned(1024))) char smem[kRouterLds];
+  const int lane = lane_id();
+  const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int e0 = blockIdx.y * kSplitExperts;
+  const int tok0 = blockIdx.x * kRT;
+  float acc[1];
+  logit_chains<ActT, 1>(x + (size_t)tok0 * C, N - tok0, wr1 + (size_t)e0 * C,
+                        min(kSplitExperts, E - e0), kSplitExperts, g, C, smem, acc);
+  const int e = e0 + g;
+  if (e < E && tok0 + lane < N) logits[(size_t)(tok0 + lane) * E + e] = acc[0] + br[e];
+}
+
+__global__ __launch_bounds__(256) void router_softmax_kernel(const float* __restrict__ logits,
+                                                             int N, int E, int k,
+                                                             int32_t* __restrict__ topk_idx,
+                                                             float* __restrict__ topk_p,
+                                                             int32_t* __restrict__ hist,
+                                                             int num_blocks) {
+  __shared__ float s_l[kRT][kMaxExperts + 1];
+  __shared__ float s_m[kRT];
+  __shared__ int s_hist[kMaxExperts];
+  const int tid = threadIdx.x;
+  const int tok0 = blockIdx.x * kRT;
+  if (tid < kMaxExperts) s_hist[tid] = 0;
+  for (int p = tid; p < kRT * E; p += blockDim.x) {
+    const int r = p / E, e = p % E;
+    s_l[r][e] = tok0 + r < N ? logits[(size_t)(tok0 + r) * E + e] : 0.0f;
+  }
+  __syncthreads();
+  softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks);
+}
+
 }  // namespace
 
+// logits == nullptr: the fused kernel.  Otherwise (E > 16, few tokens) the
+// split path through logits [N][E] (wr1 = W_r as [E][C]).
 template <typename ActT>
-hipError_t launch_router(const ActT* x, const float* wr_g, const float* br, int N, int C, int E,
-                         int k, int32_t* topk_idx, float* topk_p, int32_t* hist,
-                         hipStream_t stream) {
+hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, const float* br,
+                         int N, int C, int E, int k, int32_t* topk_idx, float* topk_p,
+                         int32_t* hist, float* logits, hipStream_t stream) {
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
+  if (logits) {
+    hipLaunchKernelGGL(router_logits_kernel<ActT>,
+                       dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
+                       dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits);
+    hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(256), 0, stream, logits, N, E, k,
+                       topk_idx, topk_p, hist, nb);
+    return hipGetLastError();
+  }
   const int RE = router_experts_per_wave(E);
   const int waves = (E + RE - 1) / RE;
   const dim3 g(nb), b(waves * kWave);
@@ -192,10 +372,12 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* br, int 
   return hipGetLastError();
 }
 
-template hipError_t launch_router<float>(const float*, const float*, const float*, int, int, int,
-                                         int, int32_t*, float*, int32_t*, hipStream_t);
-template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*, int, int,
-                                          int, int, int32_t*, float*, int32_t*, hipStream_t);
+template hipError_t launch_router<float>(const float*, const float*, const float*, const float*,
+                                         int, int, int, int, int32_t*, float*, int32_t*, float*,
+                                         hipStream_t);
+template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*,
+                                          const float*, int, int, int, int, int32_t*, float*,
+                                          int32_t*, float*, hipStream_t);
 
 // Device expf over a buffer (tests compare it with the host's glibc expf).
 __global__ void expf_probe_kernel(const float* __restrict__ in, float* __restrict__ out, int n) {
