@@ -42,7 +42,7 @@ def stage_of(kernel_name: str):
         return "permute"
     if "combine_kernel" in short:
         return "combine"
-    m = re.search(r"gemm_dma_kernel<(\d)[,>]", short)
+    m = re.search(r"gemm_(?:dma|ring5)_kernel<(\d)[,>]", short)
     if m:
         return ("gemm_gateup", "gemm_down")[int(m.group(1))]
     m = re.search(r"grouped_gemm_kernel<([^>]*)>", short)
