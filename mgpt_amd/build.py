@@ -19,7 +19,7 @@ CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "lib")
 OBJ = os.path.join(HERE, "_build")
 
-HIP_SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_dma.hip", "combine.hip",
+HIP_SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_dma.hip", "gemm_decode.hip", "combine.hip",
                "pack.hip", "moe_capi.hip"]
 ARCH = os.environ.get("MGPT_OFFLOAD_ARCH", "gfx950")
 

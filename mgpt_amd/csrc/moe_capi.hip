@@ -48,6 +48,10 @@ template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
                            const int32_t*, int, int, int, int, int, bf16_t*, int, int,
                            hipStream_t);
+template <int EPI>
+hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
+                              const float*, const int32_t*, int, int, int, int, int, bf16_t*, int,
+                              int, hipStream_t);
 }  // namespace mgpt
 
 using namespace mgpt;
@@ -407,7 +411,14 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
     const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
     if (small_m(h, N)) {
       const int mt = (int)((A + 31) / 32) + E;
-      if (fp8) {
+      if (fp8 && C % 128 == 0 && (2 * Hp) % 256 == 0) {
+        // weight streaming: the persistent direct-to-LDS decode kernel
+        HIP_TRY(launch_gemm_decode<kEpiGateUp>(xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu,
+                                               counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt, st));
+        HIP_TRY(mark(4));
+        HIP_TRY(launch_gemm_decode<kEpiDown>(hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr,
+                                             counts, E, Hp, Cp, C, Cp, ob, C, mt, st));
+      } else if (fp8) {
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
             xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
             Hp, mt, st)));
