@@ -219,6 +219,57 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
   }
 }
 
+// Work items of a persistent launch over T tiles with G blocks: the
+// ceil(T/G)-th round would leave most blocks idle when T % G is small, so
+// the tiles of that last round are split along K into s parts (s <= 8,
+// G/(T % G) of them), each a work item of its own whose fp32 partial sums
+// go to a workspace; gemm_split_reduce_kernel adds the parts in order and
+// runs the epilogue.  All tiles of the full rounds are whole items.
+struct SplitPlan {
+  int full, rem, s, items;
+  __device__ __forceinline__ void init(int T, int G, int KT, bool enable) {
+    full = (T / G) * G;
+    rem = T - full;
+    s = 1;
+    if (enable && rem > 0) {
+      s = min(min(G / rem, 8), KT);
+      if (s < 2) s = 1;
+    }
+    items = s > 1 ? full + rem * s : T;
+  }
+};
+
+struct Work {
+  Tile tile;
+  int k0, k1;   // slab range
+  int sidx;     // partial-sum slot, or -1 for a whole tile
+};
+
+__device__ __forceinline__ bool locate_work(const SegScan& sc, const SplitPlan& pl, int E,
+                                            int nbx, int KT, int v, Work* wk) {
+  if (v >= pl.items) return false;
+  int tv;
+  if (pl.s == 1 || v < pl.full) {
+    tv = v;
+    wk->k0 = 0;
+    wk->k1 = KT;
+    wk->sidx = -1;
+  } else {
+    const int u = v - pl.full;
+    const int part = u % pl.s;
+    tv = pl.full + u / pl.s;
+    wk->k0 = part * KT / pl.s;
+    wk->k1 = (part + 1) * KT / pl.s;
+    wk->sidx = u;
+  }
+  return locate_tile(sc, E, nbx, tv, &wk->tile);
+}
+
+// Partial sums of one work item: 512 threads x 128 floats, stored as
+// [32 float4 slots q][512 threads] so that every store and load is a
+// coalesced 8 KB row.  q = (j * kTM + i) * 4 + v4 holds acc[j][i][4v4 ..].
+constexpr int kPartialFloats = 512 * 128;
+
 // ---------------------------------------------------------------------------
 // Split ring.  LDS holds 5 units of 32 KB, a unit being the 256 activation
 // rows or the 256 weight rows of one 64-column slab (128-byte rows, as in
@@ -231,7 +282,7 @@ template <int EPI>
 __global__ __launch_bounds__(512) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
-    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo) {
+    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, float* __restrict__ partials) {
   using W = Waves<8>;
   constexpr int kTN = W::TN, kTM = W::TM;
   constexpr int kUnits = 5;
@@ -244,17 +295,19 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
   const int G = gridDim.x;
   int t = (G % kNumXcd == 0) ? (blockIdx.x % kNumXcd) * (G / kNumXcd) + blockIdx.x / kNumXcd
                              : blockIdx.x;
+  const int KT = K / 64;
   SegScan sc;
   sc.init(counts, E);
-  Tile cur;
-  if (!locate_tile(sc, E, nbx, t, &cur)) return;
+  SplitPlan plan;
+  plan.init(sc.tm * nbx, G, KT, partials != nullptr);
+  Work cur;
+  if (!locate_work(sc, plan, E, nbx, KT, t, &cur)) return;
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid / kWave), lane = lane_id();
   const int wn = w % W::WN, wm = w / W::WN;
   const int lrow = lane & 31, lhalf = lane >> 5;
   const size_t row_bytes_g = (size_t)K * 2;
-  const int KT = K / 64;
 
   // DMA of a unit: wave w fills its rows 32w .. 32w+31 in 4 blocks of 8
   // rows; lane l covers row r = 8i + l/8, slot l%8 = chunk ^ ((r >> 1) & 7).
@@ -273,12 +326,13 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
     return reinterpret_cast<const char*>(B + ((size_t)tl.expert * Npad + tl.n0 + 32 * w) * K);
   };
 
-  // Cursor over units: (tile dtile, slab dkt, operand dop), ring slot dslot.
-  Tile dtile = cur;
-  int dt = t, dkt = 0, dop = 0, dslot = 0;
+  // Cursor over units: (work item dwk, slab dkt, operand dop), ring slot
+  // dslot.
+  Work dwk = cur;
+  int dt = t, dkt = cur.k0, dop = 0, dslot = 0;
   bool dvalid = true;
-  const char* dga = abase(cur);
-  const char* dgb = bbase(cur);
+  const char* dga = abase(cur.tile);
+  const char* dgb = bbase(cur.tile);
   int ahead = 0;   // units issued and not yet waited for
   auto advance = [&]() __attribute__((always_inline)) {
     if (dvalid) {
@@ -294,13 +348,13 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
       dop = 1;
     } else {
       dop = 0;
-      if (++dkt == KT) {
-        dkt = 0;
+      if (++dkt == dwk.k1) {
         dt += G;
-        if (dvalid) dvalid = locate_tile(sc, E, nbx, dt, &dtile);
+        if (dvalid) dvalid = locate_work(sc, plan, E, nbx, KT, dt, &dwk);
         if (dvalid) {
-          dga = abase(dtile);
-          dgb = bbase(dtile);
+          dkt = dwk.k0;
+          dga = abase(dwk.tile);
+          dgb = bbase(dwk.tile);
         }
       }
     }
@@ -344,8 +398,8 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
   int aslot = 0;
 
   for (;;) {
-    Tile nxt;
-    const bool have_next = locate_tile(sc, E, nbx, t + G, &nxt);
+    Work nxt;
+    const bool have_next = locate_work(sc, plan, E, nbx, KT, t + G, &nxt);
     f32x16 acc[kTN][kTM];
 #pragma unroll
     for (int j = 0; j < kTN; ++j)
@@ -354,7 +408,7 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][i][v] = 0.0f;
 
-    for (int kt = 0; kt < KT; ++kt) {
+    for (int kt = cur.k0; kt < cur.k1; ++kt) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         if (ks + 1 < 4) {
@@ -382,47 +436,136 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, kTM * kTN - (kTM + kTN), 0);
       }
     }
-    store_tile<EPI, 8>(acc, cur, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out, ldo);
+    if (cur.sidx < 0) {
+      store_tile<EPI, 8>(acc, cur.tile, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out,
+                         ldo);
+    } else {
+      float4* P = reinterpret_cast<float4*>(partials + (size_t)cur.sidx * kPartialFloats) + tid;
+#pragma unroll
+      for (int j = 0; j < kTN; ++j)
+#pragma unroll
+        for (int i = 0; i < kTM; ++i)
+#pragma unroll
+          for (int v4 = 0; v4 < 4; ++v4)
+            P[((j * kTM + i) * 4 + v4) * 512] =
+                make_float4(acc[j][i][4 * v4], acc[j][i][4 * v4 + 1], acc[j][i][4 * v4 + 2],
+                            acc[j][i][4 * v4 + 3]);
+    }
     if (!have_next) break;
     t += G;
     cur = nxt;
   }
 }
 
+
+// Sums the s partial tiles of each split tile in order and applies the
+// epilogue, one output quad (4 features of one token) per thread and
+// iteration: the s float4 loads of a quad are independent, so each thread
+// keeps them all in flight, and the quads of all split tiles are spread over
+// the whole grid.  The (thread, slot) -> (token, feature) mapping is the one
+// store_tile applies to the GEMM's accumulators.
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
+    const float* __restrict__ partials, const float* __restrict__ bias0,
+    const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
+    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, int G) {
+  using W = Waves<8>;
+  constexpr int kTM = W::TM;
+  constexpr bool kGU = EPI == kEpiGateUp;
+  // quads per tile: gate/up pairs two slots (gate j, up j+1) into one quad
+  constexpr int kQuads = 512 * W::TN * kTM * 4 / (kGU ? 2 : 1);
+  const int nbx = Npad / kBN;
+  const int KT = K / 64;
+  SegScan sc;
+  sc.init(counts, E);
+  SplitPlan plan;
+  plan.init(sc.tm * nbx, G, KT, true);
+  if (plan.s == 1) return;
+  const int total = plan.rem * kQuads;
+  for (int u = blockIdx.x * 256 + threadIdx.x; u < total; u += gridDim.x * 256) {
+    const int r = u / kQuads, uq = u % kQuads;
+    Tile tile;
+    if (!locate_tile(sc, E, nbx, plan.full + r, &tile)) return;
+    const int tid = uq % 512, qq = uq / 512;
+    const int w = tid / kWave, lane = tid % kWave;
+    const int wn = w % W::WN, wm = w / W::WN, lrow = lane & 31, lhalf = lane >> 5;
+    const int g = qq % 4, i = (qq / 4) % kTM, j = qq / (4 * kTM);   // j: column group (pair)
+    const int row = tile.row0 + wm * W::WTM + lrow + i * 32;
+    if (row >= tile.row_end) continue;
+    const float4* P = reinterpret_cast<const float4*>(partials + (size_t)r * plan.s * kPartialFloats) + tid;
+    if constexpr (kGU) {
+      const int qg = ((2 * j) * kTM + i) * 4 + g, qu = ((2 * j + 1) * kTM + i) * 4 + g;
+      float4 ga = make_float4(0.f, 0.f, 0.f, 0.f), ua = ga;
+      for (int p = 0; p < plan.s; ++p) {
+        const float4 x = P[(size_t)p * (kPartialFloats / 4) + qg * 512];
+        const float4 y = P[(size_t)p * (kPartialFloats / 4) + qu * 512];
+        ga.x += x.x; ga.y += x.y; ga.z += x.z; ga.w += x.w;
+        ua.x += y.x; ua.y += y.y; ua.z += y.z; ua.w += y.w;
+      }
+      const int hb = (tile.n0 + wn * W::WTN) / 2 + 32 * j;
+      const int f = hb + 8 * g + 4 * lhalf;
+      const float* bg = bias0 + (size_t)tile.expert * bias_ld + f;
+      const float* bu = bias1 + (size_t)tile.expert * bias_ld + f;
+      *reinterpret_cast<uint2*>(out + (size_t)row * ldo + f) =
+          pack4_bf16(silu_mul_fast(ga.x + bg[0], ua.x + bu[0]),
+                     silu_mul_fast(ga.y + bg[1], ua.y + bu[1]),
+                     silu_mul_fast(ga.z + bg[2], ua.z + bu[2]),
+                     silu_mul_fast(ga.w + bg[3], ua.w + bu[3]));
+    } else {
+      const int cb = tile.n0 + wn * W::WTN + j * 32;
+      if (cb >= n_store) continue;
+      const int q = (j * kTM + i) * 4 + g;
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int p = 0; p < plan.s; ++p) {
+        const float4 x = P[(size_t)p * (kPartialFloats / 4) + q * 512];
+        a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
+      }
+      const int f = cb + 8 * g + 4 * lhalf;
+      const float* b = bias0 + (size_t)tile.expert * bias_ld + f;
+      *reinterpret_cast<uint2*>(out + (size_t)row * ldo + f) =
+          pack4_bf16(a.x + b[0], a.y + b[1], a.z + b[2], a.w + b[3]);
+    }
+  }
+}
+
+
 }  // namespace
 
 // Persistent launch: one block per CU (the kernel walks the tiles itself).
 // max_mtiles bounds sum_e ceil(count_e / 256); it only caps the grid.
-// Measured on MI355X (cfg3 shapes, skewed counts): the split 5-unit ring
-// (gate/up 1035, down 871 TFLOP/s) beats a 2-slab ring of 64 KB slabs
-// (1034, 827) and 32-column slabs (4 x 32: 938, 724; 5 x 32 with 2 per
-// barrier: 970, 786), whose 64-byte row segments double the DMA cost.
+// partials (num_cus * kPartialFloats floats, or null to disable) holds the
+// split last round; the reduce kernel that follows exits at once when the
+// counts leave nothing to split.  Measured on MI355X (cfg3 shapes, skewed
+// counts): the split 5-unit ring (gate/up 1035, down 871 TFLOP/s) beats a
+// 2-slab ring of 64 KB slabs (1034, 827) and 32-column slabs (4 x 32: 938,
+// 724; 5 x 32 with 2 per barrier: 970, 786), whose 64-byte row segments
+// double the DMA cost; a ping-pong schedule of the two waves of a SIMD
+// (934) and weights loaded straight into registers in fragment order (990)
+// did not help either.
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                            const float* bias1, const int32_t* counts, int E, int K, int Npad,
                            int n_store, int bias_ld, bf16_t* out, int ldo, int max_mtiles,
-                           hipStream_t stream) {
+                           float* partials, int num_cus, hipStream_t stream) {
   if (max_mtiles <= 0) return hipSuccess;
-  if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0) return hipErrorInvalidValue;
-  static int num_cus = 0;
-  if (num_cus == 0) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e != hipSuccess || num_cus <= 0) num_cus = 256;
-  }
+  if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0 || num_cus <= 0)
+    return hipErrorInvalidValue;
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
   hipLaunchKernelGGL((gemm_ring5_kernel<EPI>), dim3(grid), dim3(8 * kWave), 0, stream, A, B, bias0,
-                     bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo);
+                     bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo, partials);
+  if (partials)
+    hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI>), dim3(8 * grid), dim3(256), 0, stream,
+                       partials, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
+                       grid);
   return hipGetLastError();
 }
 
 template hipError_t launch_gemm_dma<kEpiGateUp>(const bf16_t*, const bf16_t*, const float*,
                                                 const float*, const int32_t*, int, int, int, int,
-                                                int, bf16_t*, int, int, hipStream_t);
+                                                int, bf16_t*, int, int, float*, int, hipStream_t);
 template hipError_t launch_gemm_dma<kEpiDown>(const bf16_t*, const bf16_t*, const float*,
                                               const float*, const int32_t*, int, int, int, int,
-                                              int, bf16_t*, int, int, hipStream_t);
+                                              int, bf16_t*, int, int, float*, int, hipStream_t);
 
 }  // namespace mgpt

@@ -46,7 +46,7 @@ hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
 hipError_t launch_pack_router(const float*, int, int, int, float*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
-                           const int32_t*, int, int, int, int, int, bf16_t*, int, int,
+                           const int32_t*, int, int, int, int, int, bf16_t*, int, int, float*, int,
                            hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
@@ -79,13 +79,15 @@ int fail(int code, const char* fmt, ...) {
   } while (0)
 
 constexpr size_t kAlign = 256;
+constexpr size_t kGemmPartialBytes = 512 * 128 * 4;   // one 256x256 fp32 tile
 constexpr int kRowPad = 256;   // rows of slack after activation buffers (GEMM tile overrun)
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 struct Layout {
-  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, total;
+  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, partials,
+      total;
 };
 
 }  // namespace
@@ -94,6 +96,7 @@ struct mgpt_moe {
   int C, H, E, k, Hp, Cp;
   int act, wdt;
   int device;
+  int num_cus = 0;         // compute units of the device (persistent grids)
   int gemm_tile = 256;     // block tile of the large-M bf16 GEMMs (256 or 128)
   float* wr_g = nullptr;   // router weights [G][C][RE] (router_experts_per_wave)
   float* wr1 = nullptr;    // router weights [E][C] (split decode router, E > 16)
@@ -120,6 +123,11 @@ struct mgpt_moe {
   // Few tokens and many experts: the router's logits are spread over more
   // blocks (one expert per wave) instead of one block per 64 tokens.
   bool router_split(int N) const { return E > 16 && N < 4096; }
+  // The bf16 large-M path (gemm_dma.hip), which may split its last round.
+  bool uses_gemm_dma(int N) const {
+    return act == MGPT_DTYPE_BF16 && wdt == MGPT_DTYPE_BF16 && gemm_tile == 256 &&
+           (size_t)N * k >= (size_t)64 * E;
+  }
   size_t w_bytes() const { return wdt == MGPT_DTYPE_FP8_E4M3 ? 1 : (wdt == MGPT_DTYPE_BF16 ? 2 : 4); }
   // h (SwiGLU output) is kept in the activation dtype.
   Layout layout(int N) const {
@@ -144,6 +152,8 @@ struct mgpt_moe {
     L.xg = take((A + kRowPad) * C * act_bytes());
     L.hbuf = take((A + kRowPad) * Hp * act_bytes());
     L.obuf = take((A + kRowPad) * C * act_bytes());
+    // fp32 partial tiles of the large-M GEMMs' split last round (one per CU)
+    L.partials = take(uses_gemm_dma(N) ? (size_t)num_cus * kGemmPartialBytes : 0);
     L.total = off;
     return L;
   }
@@ -211,6 +221,9 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
   // Tuning override for the large-M tile (default 256x256).
   if (const char* t = std::getenv("MGPT_MOE_GEMM_TILE")) h->gemm_tile = std::atoi(t) == 128 ? 128 : 256;
   hipError_t e = hipGetDevice(&h->device);
+  if (e == hipSuccess)
+    e = hipDeviceGetAttribute(&h->num_cus, hipDeviceAttributeMultiprocessorCount, h->device);
+  if (e == hipSuccess && h->num_cus <= 0) e = hipErrorInvalidDevice;
   if (e == hipSuccess) {
     for (auto& slot : h->ev)
       for (auto& ev : slot)
@@ -438,11 +451,15 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
     } else if (h->gemm_tile == 256 && !fp8) {
       // bf16 weights, prefill-shaped segments: 256x256 direct-to-LDS kernel.
       const int mt = (int)((A + 255) / 256) + E;
+      float* part = (float*)(ws + L.partials);
+      // The gate/up GEMM has ~12x more tiles than CUs at prefill shapes, so a
+      // partial last round costs little; only the down GEMM splits it.
       HIP_TRY(launch_gemm_dma<kEpiGateUp>(xg, (const bf16_t*)h->wgu, h->bg, h->bu, counts, E, C,
-                                          2 * Hp, 2 * Hp, Hp, hb, Hp, mt, st));
+                                          2 * Hp, 2 * Hp, Hp, hb, Hp, mt, nullptr, h->num_cus,
+                                          st));
       HIP_TRY(mark(4));
       HIP_TRY(launch_gemm_dma<kEpiDown>(hb, (const bf16_t*)h->wd, h->bd, nullptr, counts, E, Hp,
-                                        Cp, C, Cp, ob, C, mt, st));
+                                        Cp, C, Cp, ob, C, mt, part, h->num_cus, st));
     } else {
       const int mt = (int)((A + 127) / 128) + E;
       if (fp8) {
