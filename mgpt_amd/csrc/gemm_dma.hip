@@ -138,6 +138,58 @@ __device__ __forceinline__ bool locate_tile(const SegScan& sc, int E, int nbx, i
   return true;
 }
 
+// The accumulators of one 32 x 32 tile as VGPR values.  With 4 waves per
+// block (256 accumulators per lane) the accumulators live in AGPRs; reading
+// them through v_accvgpr_read one tile at a time stops the compiler from
+// copying all 256 into VGPRs at the loop exit (which spills).  The caller
+// has waited out the MFMA result latency (mfma_drain).
+template <int NW>
+__device__ __forceinline__ f32x16 acc_fetch(const f32x16& a) {
+  if constexpr (NW == 8) {
+    return a;
+  } else {
+    f32x16 r;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      float x;
+      asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(x) : "a"(a[v]));
+      r[v] = x;
+    }
+    return r;
+  }
+}
+
+template <int NW>
+__device__ __forceinline__ void mfma_drain() {
+  if constexpr (NW != 8) asm volatile("s_nop 15\n\ts_nop 15\n\ts_nop 15\n\ts_nop 15" ::: "memory");
+}
+
+// Stores the 32 outputs (features base .. base+31) of one token that a lane
+// pair (l, l+32) holds as quads: q[g] of lane l are features 8g..8g+3, of lane
+// l+32 features 8g+4..8g+7 (bf16 pairs).  Swapping two quads across the pair
+// leaves lane l with the whole 8-feature groups 0 and 2 and lane l+32 with 1
+// and 3, so each lane writes 16-byte vectors and a store covers 32 bytes of
+// each of the 32 token rows (instead of 16).  Every lane of the pair must
+// run this (it exchanges registers); `store` gates the memory writes.
+__device__ __forceinline__ void store_group32(bf16_t* base, const uint2 (&q)[4], int lhalf,
+                                              bool store) {
+  const uint2 s0 = lhalf ? q[0] : q[1];
+  const uint2 s1 = lhalf ? q[2] : q[3];
+  uint2 r0, r1;
+  r0.x = __shfl_xor(s0.x, 32);
+  r0.y = __shfl_xor(s0.y, 32);
+  r1.x = __shfl_xor(s1.x, 32);
+  r1.y = __shfl_xor(s1.y, 32);
+  const uint4 w0 = lhalf ? make_uint4(r0.x, r0.y, q[1].x, q[1].y)
+                         : make_uint4(q[0].x, q[0].y, r0.x, r0.y);
+  const uint4 w1 = lhalf ? make_uint4(r1.x, r1.y, q[3].x, q[3].y)
+                         : make_uint4(q[2].x, q[2].y, r1.x, r1.y);
+  if (store) {
+    *reinterpret_cast<uint4*>(base + 8 * lhalf) = w0;
+    *reinterpret_cast<uint4*>(base + 16 + 8 * lhalf) = w1;
+  }
+}
+
 // Epilogue straight from the accumulators of a wave's WTN-feature x
 // WTM-token tile.  Register v of a 32x32 tile holds feature row
 // 8*(v/4) + 4*(lane/32) + v%4 (four consecutive features per group v/4) and
@@ -172,21 +224,22 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
 #pragma unroll
       for (int i = 0; i < W::TM; ++i) {
         const int row = tok_base + i * 32;
-        if (row < cur.row_end) {
-          bf16_t* orow = out + (size_t)row * ldo + hb + 4 * lhalf;
-          const f32x16& ga = acc[2 * gi][i];
-          const f32x16& ua = acc[2 * gi + 1][i];
+        const f32x16 ga = acc_fetch<NW>(acc[2 * gi][i]);
+        const f32x16 ua = acc_fetch<NW>(acc[2 * gi + 1][i]);
+        uint2 q[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int v = 4 * g;
-            *reinterpret_cast<uint2*>(orow + 8 * g) =
-                pack4_bf16(silu_mul_fast(ga[v + 0] + bg[v + 0], ua[v + 0] + bu[v + 0]),
-                           silu_mul_fast(ga[v + 1] + bg[v + 1], ua[v + 1] + bu[v + 1]),
-                           silu_mul_fast(ga[v + 2] + bg[v + 2], ua[v + 2] + bu[v + 2]),
-                           silu_mul_fast(ga[v + 3] + bg[v + 3], ua[v + 3] + bu[v + 3]));
-          }
+        for (int g = 0; g < 4; ++g) {
+          const int v = 4 * g;
+          q[g] = pack4_bf16(silu_mul_fast(ga[v + 0] + bg[v + 0], ua[v + 0] + bu[v + 0]),
+                            silu_mul_fast(ga[v + 1] + bg[v + 1], ua[v + 1] + bu[v + 1]),
+                            silu_mul_fast(ga[v + 2] + bg[v + 2], ua[v + 2] + bu[v + 2]),
+                            silu_mul_fast(ga[v + 3] + bg[v + 3], ua[v + 3] + bu[v + 3]));
         }
+        store_group32(out + (size_t)row * ldo + hb, q, lhalf, row < cur.row_end);
       }
+      // one column group at a time: keeps the scheduler from hoisting every
+      // accumulator read (TN * TM * 16 values) ahead of the stores
+      __builtin_amdgcn_sched_barrier(0);
     }
   } else {
 #pragma unroll
@@ -205,16 +258,15 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
 #pragma unroll
       for (int i = 0; i < W::TM; ++i) {
         const int row = tok_base + i * 32;
-        if (row < cur.row_end) {
-          bf16_t* orow = out + (size_t)row * ldo + cb + 4 * lhalf;
-          const f32x16& a = acc[j][i];
+        const f32x16 a = acc_fetch<NW>(acc[j][i]);
+        uint2 q[4];
 #pragma unroll
-          for (int g = 0; g < 4; ++g)
-            *reinterpret_cast<uint2*>(orow + 8 * g) =
-                pack4_bf16(a[4 * g + 0] + b[4 * g + 0], a[4 * g + 1] + b[4 * g + 1],
-                           a[4 * g + 2] + b[4 * g + 2], a[4 * g + 3] + b[4 * g + 3]);
-        }
+        for (int g = 0; g < 4; ++g)
+          q[g] = pack4_bf16(a[4 * g + 0] + b[4 * g + 0], a[4 * g + 1] + b[4 * g + 1],
+                            a[4 * g + 2] + b[4 * g + 2], a[4 * g + 3] + b[4 * g + 3]);
+        store_group32(out + (size_t)row * ldo + cb, q, lhalf, row < cur.row_end);
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 }
@@ -265,10 +317,10 @@ __device__ __forceinline__ bool locate_work(const SegScan& sc, const SplitPlan& 
   return locate_tile(sc, E, nbx, tv, &wk->tile);
 }
 
-// Partial sums of one work item: 512 threads x 128 floats, stored as
-// [32 float4 slots q][512 threads] so that every store and load is a
-// coalesced 8 KB row.  q = (j * kTM + i) * 4 + v4 holds acc[j][i][4v4 ..].
-constexpr int kPartialFloats = 512 * 128;
+// Partial sums of one work item, a whole 256 x 256 fp32 tile, stored as
+// [TN*TM*4 float4 slots q][threads] so that every store and load is a
+// coalesced row.  q = (j * kTM + i) * 4 + v4 holds acc[j][i][4v4 ..].
+constexpr int kPartialFloats = 256 * 256;
 
 // ---------------------------------------------------------------------------
 // Split ring.  LDS holds 5 units of 32 KB, a unit being the 256 activation
@@ -278,17 +330,18 @@ constexpr int kPartialFloats = 512 * 128;
 // and refills them with units 2s+3 (weights of slab s+1) and 2s+4
 // (activations of slab s+2): the activations are requested two slabs ahead
 // and the weights one (a 2-stage ring of 64 KB slabs manages one for both).
-template <int EPI>
-__global__ __launch_bounds__(512) void gemm_ring5_kernel(
+template <int EPI, int NW>
+__global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
     int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, float* __restrict__ partials) {
-  using W = Waves<8>;
+  using W = Waves<NW>;
   constexpr int kTN = W::TN, kTM = W::TM;
   constexpr int kUnits = 5;
   constexpr int kRowBytes = 128;
-  constexpr int kUnit = 256 * kRowBytes;          // 32 KB
-  constexpr int kDmaPerWave = kUnit / 1024 / 8;   // 4
+  constexpr int kUnit = 256 * kRowBytes;           // 32 KB
+  constexpr int kDmaPerWave = kUnit / 1024 / NW;   // 1 KB loads per wave and unit
+  constexpr int kWaveRows = 256 / NW;              // unit rows each wave loads
   __shared__ __attribute__((aligned(1024))) char smem[kUnits * kUnit];
 
   const int nbx = Npad / kBN;
@@ -309,8 +362,9 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
   const int lrow = lane & 31, lhalf = lane >> 5;
   const size_t row_bytes_g = (size_t)K * 2;
 
-  // DMA of a unit: wave w fills its rows 32w .. 32w+31 in 4 blocks of 8
-  // rows; lane l covers row r = 8i + l/8, slot l%8 = chunk ^ ((r >> 1) & 7).
+  // DMA of a unit: wave w fills its kWaveRows rows in blocks of 8 rows;
+  // lane l covers row r = 8i + l/8, slot l%8 = chunk ^ ((r >> 1) & 7)
+  // (kWaveRows is a multiple of 16, so the slot depends on i & 1 only).
   uint32_t lane_off[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -320,10 +374,10 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
   }
   const uint32_t lds_base = (uint32_t)(uintptr_t)(lds_char*)smem + (uint32_t)(w * kDmaPerWave * 1024);
   auto abase = [&](const Tile& tl) -> const char* {
-    return reinterpret_cast<const char*>(A + ((size_t)tl.row0 + 32 * w) * K);
+    return reinterpret_cast<const char*>(A + ((size_t)tl.row0 + kWaveRows * w) * K);
   };
   auto bbase = [&](const Tile& tl) -> const char* {
-    return reinterpret_cast<const char*>(B + ((size_t)tl.expert * Npad + tl.n0 + 32 * w) * K);
+    return reinterpret_cast<const char*>(B + ((size_t)tl.expert * Npad + tl.n0 + kWaveRows * w) * K);
   };
 
   // Cursor over units: (work item dwk, slab dkt, operand dop), ring slot
@@ -333,24 +387,22 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
   bool dvalid = true;
   const char* dga = abase(cur.tile);
   const char* dgb = bbase(cur.tile);
-  int ahead = 0;   // units issued and not yet waited for
-  auto advance = [&]() __attribute__((always_inline)) {
-    if (dvalid) {
-      const char* g = (dop ? dgb : dga) + (size_t)dkt * kRowBytes;
-      const uint32_t dst = lds_base + (uint32_t)(dslot * kUnit);
-#pragma unroll
-      for (int i = 0; i < kDmaPerWave; ++i)
-        dma16(g + (size_t)(i * 8) * row_bytes_g + lane_off[i & 1], dst + i * 1024);
-      ++ahead;
-    }
+  const char* dlast = dga;
+  // Source and ring slot of the next unit.  Past the end of the block's
+  // work it repeats the last real unit (in bounds, into a freed slot), so
+  // every slab issues the same loads and waits the same way.
+  auto next_unit = [&](const char*& g, uint32_t& dst) __attribute__((always_inline)) {
+    if (dvalid) dlast = (dop ? dgb : dga) + (size_t)dkt * kRowBytes;
+    g = dlast;
+    dst = lds_base + (uint32_t)(dslot * kUnit);
     dslot = dslot + 1 == kUnits ? 0 : dslot + 1;
     if (dop == 0) {
       dop = 1;
     } else {
       dop = 0;
-      if (++dkt == dwk.k1) {
+      if (dvalid && ++dkt == dwk.k1) {
         dt += G;
-        if (dvalid) dvalid = locate_work(sc, plan, E, nbx, KT, dt, &dwk);
+        dvalid = locate_work(sc, plan, E, nbx, KT, dt, &dwk);
         if (dvalid) {
           dkt = dwk.k0;
           dga = abase(dwk.tile);
@@ -359,14 +411,26 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
       }
     }
   };
-  // B_s: units 2s and 2s+1 landed with unit 2s+2 possibly in flight; all
-  // waves done with slab s-1, whose two units are then refilled.
-  auto next_slab_barrier = [&]() __attribute__((always_inline)) {
-    ahead -= 2;
-    if (ahead >= 1) slab_barrier<kDmaPerWave>();
-    else slab_barrier<0>();
-    advance();
-    advance();
+  auto dma_loads = [&](const char* g, uint32_t dst, int i0, int n) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = i0; i < i0 + n; ++i)
+      dma16(g + (size_t)(i * 8) * row_bytes_g + lane_off[i & 1], dst + i * 1024);
+  };
+  // The two units refilled after barrier B_s (weights of slab s+1, then
+  // activations of slab s+2, into the slots of slab s-1) are issued a
+  // quarter at a time in the four MFMA segments that follow, so that the
+  // loads queue behind MFMAs instead of 64 of them reaching the load unit
+  // together at the barrier.  B_s waits for units 2s and 2s+1 with the four
+  // loads of unit 2s+2 still allowed in flight.
+  const char* ug[2];
+  uint32_t ud[2];
+  auto quarter = [&](int q) __attribute__((always_inline)) {
+    dma_loads(ug[q >> 1], ud[q >> 1], (q & 1) * (kDmaPerWave / 2), kDmaPerWave / 2);
+  };
+  auto slab_wait = [&]() __attribute__((always_inline)) {
+    slab_barrier<kDmaPerWave>();
+    next_unit(ug[0], ud[0]);
+    next_unit(ug[1], ud[1]);
   };
 
   const int x_row = (wm * W::WTM + lrow) * kRowBytes;
@@ -389,11 +453,15 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
       ws[j] = *reinterpret_cast<const bf16x8*>(sb + j * 32 * kRowBytes + cofs);
   };
 
-  // Prologue: units 0, 1, 2 (A0 B0 A1).
-  advance();
-  advance();
-  advance();
-  next_slab_barrier();
+  // Prologue: units 0, 1, 2 (A0 B0 A1), then B_0 and the first quarter.
+  for (int u = 0; u < 3; ++u) {
+    const char* g;
+    uint32_t dst;
+    next_unit(g, dst);
+    dma_loads(g, dst, 0, kDmaPerWave);
+  }
+  slab_wait();
+  quarter(0);
   frags(0, 0, xf[0], wf[0]);
   int aslot = 0;
 
@@ -412,6 +480,7 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         if (ks + 1 < 4) {
+          quarter(ks + 1);
           frags(aslot, ks + 1, xf[(ks + 1) & 1], wf[(ks + 1) & 1]);
         } else {
           // next slab; after the block's last slab this reads stale units
@@ -419,7 +488,8 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
           // LDS wait counting exact)
           aslot += 2;
           if (aslot >= kUnits) aslot -= kUnits;
-          next_slab_barrier();
+          slab_wait();
+          quarter(0);
           frags(aslot, 0, xf[0], wf[0]);
         }
 #pragma unroll
@@ -436,25 +506,30 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
         __builtin_amdgcn_sched_group_barrier(0x008, kTM * kTN - (kTM + kTN), 0);
       }
     }
+    mfma_drain<NW>();
     if (cur.sidx < 0) {
-      store_tile<EPI, 8>(acc, cur.tile, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out,
-                         ldo);
+      store_tile<EPI, NW>(acc, cur.tile, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out,
+                          ldo);
     } else {
       float4* P = reinterpret_cast<float4*>(partials + (size_t)cur.sidx * kPartialFloats) + tid;
 #pragma unroll
-      for (int j = 0; j < kTN; ++j)
+      for (int j = 0; j < kTN; ++j) {
 #pragma unroll
-        for (int i = 0; i < kTM; ++i)
+        for (int i = 0; i < kTM; ++i) {
+          const f32x16 a = acc_fetch<NW>(acc[j][i]);
 #pragma unroll
           for (int v4 = 0; v4 < 4; ++v4)
-            P[((j * kTM + i) * 4 + v4) * 512] =
-                make_float4(acc[j][i][4 * v4], acc[j][i][4 * v4 + 1], acc[j][i][4 * v4 + 2],
-                            acc[j][i][4 * v4 + 3]);
+            P[((j * kTM + i) * 4 + v4) * W::kThreads] =
+                make_float4(a[4 * v4], a[4 * v4 + 1], a[4 * v4 + 2], a[4 * v4 + 3]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     if (!have_next) break;
     t += G;
     cur = nxt;
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeated tail loads
 }
 
 
@@ -462,18 +537,18 @@ __global__ __launch_bounds__(512) void gemm_ring5_kernel(
 // epilogue, one output quad (4 features of one token) per thread and
 // iteration: the s float4 loads of a quad are independent, so each thread
 // keeps them all in flight, and the quads of all split tiles are spread over
-// the whole grid.  The (thread, slot) -> (token, feature) mapping is the one
-// store_tile applies to the GEMM's accumulators.
-template <int EPI>
+// the whole grid.  The (GEMM thread, slot) -> (token, feature) mapping is
+// the one store_tile applies to the GEMM's accumulators.
+template <int EPI, int NW>
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     const float* __restrict__ partials, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
     int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, int G) {
-  using W = Waves<8>;
-  constexpr int kTM = W::TM;
+  using W = Waves<NW>;
+  constexpr int kTM = W::TM, kT = W::kThreads;
   constexpr bool kGU = EPI == kEpiGateUp;
   // quads per tile: gate/up pairs two slots (gate j, up j+1) into one quad
-  constexpr int kQuads = 512 * W::TN * kTM * 4 / (kGU ? 2 : 1);
+  constexpr int kQuads = kT * W::TN * kTM * 4 / (kGU ? 2 : 1);
   const int nbx = Npad / kBN;
   const int KT = K / 64;
   SegScan sc;
@@ -482,11 +557,12 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
   plan.init(sc.tm * nbx, G, KT, true);
   if (plan.s == 1) return;
   const int total = plan.rem * kQuads;
+  // kQuads is a multiple of 256, so r (and the tile) is uniform per block
   for (int u = blockIdx.x * 256 + threadIdx.x; u < total; u += gridDim.x * 256) {
     const int r = u / kQuads, uq = u % kQuads;
     Tile tile;
     if (!locate_tile(sc, E, nbx, plan.full + r, &tile)) return;
-    const int tid = uq % 512, qq = uq / 512;
+    const int tid = uq % kT, qq = uq / kT;
     const int w = tid / kWave, lane = tid % kWave;
     const int wn = w % W::WN, wm = w / W::WN, lrow = lane & 31, lhalf = lane >> 5;
     const int g = qq % 4, i = (qq / 4) % kTM, j = qq / (4 * kTM);   // j: column group (pair)
@@ -497,8 +573,8 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
       const int qg = ((2 * j) * kTM + i) * 4 + g, qu = ((2 * j + 1) * kTM + i) * 4 + g;
       float4 ga = make_float4(0.f, 0.f, 0.f, 0.f), ua = ga;
       for (int p = 0; p < plan.s; ++p) {
-        const float4 x = P[(size_t)p * (kPartialFloats / 4) + qg * 512];
-        const float4 y = P[(size_t)p * (kPartialFloats / 4) + qu * 512];
+        const float4 x = P[(size_t)p * (kPartialFloats / 4) + qg * kT];
+        const float4 y = P[(size_t)p * (kPartialFloats / 4) + qu * kT];
         ga.x += x.x; ga.y += x.y; ga.z += x.z; ga.w += x.w;
         ua.x += y.x; ua.y += y.y; ua.z += y.z; ua.w += y.w;
       }
@@ -517,7 +593,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
       const int q = (j * kTM + i) * 4 + g;
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
       for (int p = 0; p < plan.s; ++p) {
-        const float4 x = P[(size_t)p * (kPartialFloats / 4) + q * 512];
+        const float4 x = P[(size_t)p * (kPartialFloats / 4) + q * kT];
         a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
       }
       const int f = cb + 8 * g + 4 * lhalf;
@@ -528,6 +604,10 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
   }
 }
 
+#ifndef MGPT_RING_WAVES
+#define MGPT_RING_WAVES 8
+#endif
+constexpr int kRingWaves = MGPT_RING_WAVES;
 
 }  // namespace
 
@@ -548,14 +628,18 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                            int n_store, int bias_ld, bf16_t* out, int ldo, int max_mtiles,
                            float* partials, int num_cus, hipStream_t stream) {
   if (max_mtiles <= 0) return hipSuccess;
-  if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0 || num_cus <= 0)
+  // 16-byte output vectors: ldo and the output base must keep 8-element alignment
+  if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0 || num_cus <= 0 || ldo % 8 != 0 ||
+      (reinterpret_cast<uintptr_t>(out) & 15) != 0)
     return hipErrorInvalidValue;
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
-  hipLaunchKernelGGL((gemm_ring5_kernel<EPI>), dim3(grid), dim3(8 * kWave), 0, stream, A, B, bias0,
-                     bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo, partials);
+  hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves>), dim3(grid), dim3(kRingWaves * kWave), 0,
+                     stream, A, B, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
+                     partials);
   if (partials)
-    hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI>), dim3(8 * grid), dim3(256), 0, stream,
+    hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256), 0,
+                       stream,
                        partials, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
                        grid);
   return hipGetLastError();
