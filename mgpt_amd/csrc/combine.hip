@@ -8,7 +8,7 @@
 // This kernel gathers instead of scattering (no atomics, deterministic):
 // one wave per token sorts its k choices by expert id and accumulates the
 // k rows in that order with the same two roundings per term (the file is
-// built with -ffp-contract=off), reading 16 bytes per lane per row.
+// built with -ffp-contract=off), reading 16 bytes per lane per row chunk.
 #include "common.hpp"
 
 namespace mgpt {
@@ -19,8 +19,7 @@ struct Vec16;
 template <>
 struct Vec16<bf16_t> {
   static constexpr int n = 8;
-  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
+  static __device__ __forceinline__ void unpack(const uint4 u, float (&v)[8]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -41,56 +40,192 @@ struct Vec16<bf16_t> {
 template <>
 struct Vec16<float> {
   static constexpr int n = 4;
-  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
-    const float4 u = *reinterpret_cast<const float4*>(p);
-    v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+  static __device__ __forceinline__ void unpack(const uint4 u, float (&v)[4]) {
+    v[0] = __uint_as_float(u.x);
+    v[1] = __uint_as_float(u.y);
+    v[2] = __uint_as_float(u.z);
+    v[3] = __uint_as_float(u.w);
   }
   static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
     *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
   }
 };
 
-constexpr int kTokPerBlock = 4;   // one wave per token
+constexpr int kWavesPerBlock = 4;
+// Tokens per wave of the k = 2 kernel.  Measured on MI355X at cfg3 shapes:
+// 1 token (20.3 us) beats 2 (20.8 us); the extra loads in flight do not pay
+// for the halved wave count.
+constexpr int kTokensPerWave2 = 1;
 
-template <typename ActT>
+// Each wave combines TPW consecutive tokens.  KT choices per token (0: the
+// runtime k, one row at a time) and CH 16-byte chunks per lane and row.
+// With KT fixed, all TPW * KT * CH chunk loads of a wave are issued before
+// any is used, so each wave keeps them all in flight.
+template <typename ActT, int TPW, int KT, int CH>
 __global__ __launch_bounds__(256) void combine_kernel(const ActT* __restrict__ out_rows,
                                                       const int32_t* __restrict__ topk_idx,
                                                       const float* __restrict__ topk_p,
                                                       const int32_t* __restrict__ slot_of, int N,
                                                       int C, int k, ActT* __restrict__ y) {
-  __shared__ int s_slot[kTokPerBlock][kMaxTopK];
-  __shared__ float s_p[kTokPerBlock][kMaxTopK];
+  static_assert(TPW * kMaxTopK <= kWave, "one lane per (token, choice)");
+  __shared__ int s_slot[kWavesPerBlock][TPW][kMaxTopK];
+  __shared__ float s_p[kWavesPerBlock][TPW][kMaxTopK];
+  if constexpr (KT > 0) k = KT;
   const int w = threadIdx.x / kWave;
   const int l = lane_id();
-  const int t = blockIdx.x * kTokPerBlock + w;
-  if (t >= N) return;   // whole wave exits together; no block barrier below
-  if (l < k) {
-    const int e = topk_idx[(size_t)t * k + l];
-    // rank of this choice among the token's k choices by expert id
-    int rank = 0;
-    for (int j = 0; j < k; ++j) {
-      const int ej = topk_idx[(size_t)t * k + j];
-      rank += (ej < e) || (ej == e && j < l);
+  const int t0 = (blockIdx.x * kWavesPerBlock + w) * TPW;
+  if (t0 >= N) return;   // whole wave exits together; no block barrier below
+  {
+    // lane u * kMaxTopK + j: choice j of token t0 + u
+    const int u = l / kMaxTopK, j = l % kMaxTopK, t = t0 + u;
+    if (u < TPW && j < k && t < N) {
+      const int e = topk_idx[(size_t)t * k + j];
+      // rank of this choice among the token's k choices by expert id
+      int rank = 0;
+      for (int i = 0; i < k; ++i) {
+        const int ei = topk_idx[(size_t)t * k + i];
+        rank += (ei < e) || (ei == e && i < j);
+      }
+      s_slot[w][u][rank] = slot_of[(size_t)t * k + j];
+      s_p[w][u][rank] = topk_p[(size_t)t * k + j];
     }
-    s_slot[w][rank] = slot_of[(size_t)t * k + l];
-    s_p[w][rank] = topk_p[(size_t)t * k + l];
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   constexpr int VN = Vec16<ActT>::n;
-  for (int c = l * VN; c < C; c += kWave * VN) {
-    float acc[VN];
+  for (int c0 = 0; c0 < C; c0 += kWave * VN * CH) {
+    float acc[TPW][CH][VN];
 #pragma unroll
-    for (int i = 0; i < VN; ++i) acc[i] = 0.0f;
-    for (int a = 0; a < k; ++a) {
-      float v[VN];
-      Vec16<ActT>::load(out_rows + (size_t)s_slot[w][a] * C + c, v);
-      const float p = s_p[w][a];
+    for (int u = 0; u < TPW; ++u)
 #pragma unroll
-      for (int i = 0; i < VN; ++i) acc[i] = acc[i] + v[i] * p;
+      for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+        for (int i = 0; i < VN; ++i) acc[u][ch][i] = 0.0f;
+    auto add_row = [&](int u, const uint4 (&raw)[CH], float p) __attribute__((always_inline)) {
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        float v[VN];
+        Vec16<ActT>::unpack(raw[ch], v);
+#pragma unroll
+        for (int i = 0; i < VN; ++i) acc[u][ch][i] = acc[u][ch][i] + v[i] * p;
+      }
+    };
+    auto load_row = [&](int u, int a, uint4 (&raw)[CH]) __attribute__((always_inline)) {
+      const ActT* src = out_rows + (size_t)s_slot[w][u][a] * C;
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        const int c = c0 + (ch * kWave + l) * VN;
+        raw[ch] = c < C ? *reinterpret_cast<const uint4*>(src + c) : make_uint4(0, 0, 0, 0);
+      }
+    };
+    const int nt = min(TPW, N - t0);
+    if constexpr (KT > 0) {
+      uint4 raw[TPW][KT][CH];
+#pragma unroll
+      for (int u = 0; u < TPW; ++u)
+        if (u < nt)
+#pragma unroll
+          for (int a = 0; a < KT; ++a) load_row(u, a, raw[u][a]);
+#pragma unroll
+      for (int u = 0; u < TPW; ++u)
+        if (u < nt)
+#pragma unroll
+          for (int a = 0; a < KT; ++a) add_row(u, raw[u][a], s_p[w][u][a]);
+    } else {
+      for (int u = 0; u < nt; ++u)
+        for (int a = 0; a < k; ++a) {
+          uint4 raw[CH];
+          load_row(u, a, raw);
+          add_row(u, raw, s_p[w][u][a]);
+        }
     }
-    Vec16<ActT>::store(y + (size_t)t * C + c, acc);
+#pragma unroll
+    for (int u = 0; u < TPW; ++u)
+      if (u < nt)
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+          const int c = c0 + (ch * kWave + l) * VN;
+          if (c < C) Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc[u][ch]);
+        }
   }
+}
+
+// k = 2: each wave combines TPW tokens whose two choices come from
+// wave-uniform (scalar) loads of slot_of / topk_p; no LDS, no rank loop.  The
+// rows are added in ascending slot order, which is ascending expert id:
+// slots are expert-major and a token's choices are distinct experts.  All
+// TPW * 2 * CH chunk loads are issued before any is used.
+template <typename ActT, int TPW, int CH>
+__global__ __launch_bounds__(256) void combine2_kernel(const ActT* __restrict__ out_rows,
+                                                       const float* __restrict__ topk_p,
+                                                       const int32_t* __restrict__ slot_of, int N,
+                                                       int C, ActT* __restrict__ y) {
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int l = lane_id();
+  const int t0 = (blockIdx.x * kWavesPerBlock + w) * TPW;
+  if (t0 >= N) return;
+  const int nt = min(TPW, N - t0);
+  int sl[TPW][2];
+  float pr[TPW][2];
+#pragma unroll
+  for (int u = 0; u < TPW; ++u) {
+    const int t = min(t0 + u, N - 1);
+    int s0 = __builtin_amdgcn_readfirstlane(slot_of[2 * t]);
+    int s1 = __builtin_amdgcn_readfirstlane(slot_of[2 * t + 1]);
+    float p0 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(topk_p[2 * t])));
+    float p1 = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(topk_p[2 * t + 1])));
+    if (s1 < s0) {
+      const int ts = s0; s0 = s1; s1 = ts;
+      const float tp = p0; p0 = p1; p1 = tp;
+    }
+    sl[u][0] = s0; sl[u][1] = s1;
+    pr[u][0] = p0; pr[u][1] = p1;
+  }
+  constexpr int VN = Vec16<ActT>::n;
+  for (int c0 = 0; c0 < C; c0 += kWave * VN * CH) {
+    uint4 raw[TPW][2][CH];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u)
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const ActT* src = out_rows + (size_t)sl[u][a] * C;
+#pragma unroll
+        for (int ch = 0; ch < CH; ++ch) {
+          const int c = c0 + (ch * kWave + l) * VN;
+          raw[u][a][ch] = (c < C && u < nt) ? *reinterpret_cast<const uint4*>(src + c)
+                                            : make_uint4(0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+    for (int u = 0; u < TPW; ++u)
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) {
+        float acc[VN], v[VN];
+#pragma unroll
+        for (int i = 0; i < VN; ++i) acc[i] = 0.0f;
+#pragma unroll
+        for (int a = 0; a < 2; ++a) {
+          Vec16<ActT>::unpack(raw[u][a][ch], v);
+#pragma unroll
+          for (int i = 0; i < VN; ++i) acc[i] = acc[i] + v[i] * pr[u][a];
+        }
+        const int c = c0 + (ch * kWave + l) * VN;
+        if (c < C && u < nt) Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc);
+      }
+  }
+}
+
+template <typename ActT, int TPW, int KT>
+void launch_combine_k(int chunks, hipStream_t stream, const ActT* out_rows,
+                      const int32_t* topk_idx, const float* topk_p, const int32_t* slot_of, int N,
+                      int C, int k, ActT* y) {
+  const dim3 grid((N + kWavesPerBlock * TPW - 1) / (kWavesPerBlock * TPW));
+  if (chunks >= 2)
+    hipLaunchKernelGGL((combine_kernel<ActT, TPW, KT, 2>), grid, dim3(256), 0, stream, out_rows,
+                       topk_idx, topk_p, slot_of, N, C, k, y);
+  else
+    hipLaunchKernelGGL((combine_kernel<ActT, TPW, KT, 1>), grid, dim3(256), 0, stream, out_rows,
+                       topk_idx, topk_p, slot_of, N, C, k, y);
 }
 
 }  // namespace
@@ -100,9 +235,25 @@ hipError_t launch_combine(const ActT* out_rows, const int32_t* topk_idx, const f
                           const int32_t* slot_of, int N, int C, int k, ActT* y,
                           hipStream_t stream) {
   if (N == 0) return hipSuccess;
-  const int nb = (N + kTokPerBlock - 1) / kTokPerBlock;
-  hipLaunchKernelGGL(combine_kernel<ActT>, dim3(nb), dim3(256), 0, stream, out_rows, topk_idx,
-                     topk_p, slot_of, N, C, k, y);
+  if (k < 1 || k > kMaxTopK) return hipErrorInvalidValue;
+  const int per_chunk = kWave * Vec16<ActT>::n;   // elements one chunk covers
+  const int chunks = (C + per_chunk - 1) / per_chunk;
+  switch (k) {
+    case 2: {
+      const dim3 grid((N + kWavesPerBlock * kTokensPerWave2 - 1) /
+                      (kWavesPerBlock * kTokensPerWave2));
+      if (chunks >= 2)
+        hipLaunchKernelGGL((combine2_kernel<ActT, kTokensPerWave2, 2>), grid, dim3(256), 0,
+                           stream, out_rows, topk_p, slot_of, N, C, y);
+      else
+        hipLaunchKernelGGL((combine2_kernel<ActT, kTokensPerWave2, 1>), grid, dim3(256), 0,
+                           stream, out_rows, topk_p, slot_of, N, C, y);
+      break;
+    }
+    default:
+      launch_combine_k<ActT, 1, 0>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
+                                   y);
+  }
   return hipGetLastError();
 }
 
