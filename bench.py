@@ -34,15 +34,15 @@ CALIB_MIB = 512               # known-size elementwise copy for counter calibrat
 def stage_of(kernel_name: str):
     """Forward stage of a kernel in a rocprofv3 trace (None: not a forward kernel)."""
     short = kernel_name.replace("(anonymous namespace)", "").split("(")[0]
-    if "router_topk" in short:
+    if re.search(r"router_(?:topk|logits|softmax)", short):
         return "router_topk"
     if "expert_scan" in short:
         return "expert_scan"
     if "permute_kernel" in short:
         return "permute"
-    if "combine_kernel" in short:
+    if re.search(r"combine\d?_kernel", short):
         return "combine"
-    m = re.search(r"gemm_(?:dma|ring5)_kernel<(\d)[,>]", short)
+    m = re.search(r"gemm_(?:dma|ring5|decode|split_reduce)_kernel<(\d)[,>]", short)
     if m:
         return ("gemm_gateup", "gemm_down")[int(m.group(1))]
     m = re.search(r"grouped_gemm_kernel<([^>]*)>", short)
@@ -55,7 +55,9 @@ def stage_of(kernel_name: str):
 
 
 def _counter_means(d: str, counter: str):
-    """Mean counter value per dispatch, by stage, from a rocprofv3 --pmc csv."""
+    """Counter value per forward, by stage, from a rocprofv3 --pmc csv: the
+    mean per dispatch of each kernel, summed over the kernels of a stage (the
+    down GEMM stage, for one, is the GEMM plus its split-K reduction)."""
     import csv
     vals = {}
     with open(os.path.join(d, "run_counter_collection.csv")) as f:
@@ -64,11 +66,18 @@ def _counter_means(d: str, counter: str):
                 continue
             st = stage_of(r["Kernel_Name"])
             if st:
-                vals.setdefault(st, []).append(float(r["Counter_Value"]))
-    if "calib_copy" in vals:      # the 512 MiB copies only, not torch's small multiplies
-        big = max(vals["calib_copy"])
-        vals["calib_copy"] = [v for v in vals["calib_copy"] if v > 0.5 * big]
-    return {k: sum(v) / len(v) for k, v in vals.items()}
+                vals.setdefault(st, {}).setdefault(r["Kernel_Name"], []).append(
+                    float(r["Counter_Value"]))
+    out = {}
+    for st, kerns in vals.items():
+        if st == "calib_copy":    # the 512 MiB copies only, not torch's small multiplies
+            allv = [v for vs in kerns.values() for v in vs]
+            big = max(allv)
+            allv = [v for v in allv if v > 0.5 * big]
+            out[st] = sum(allv) / len(allv)
+        else:
+            out[st] = sum(sum(vs) / len(vs) for vs in kerns.values())
+    return out
 
 
 def summarize_traffic(fetch_dir: str, write_dir: str, workload: str, commands) -> dict:
