@@ -25,6 +25,7 @@ import time
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+PEAK_F32_TFLOPS = 157.3      # MI355X dense fp32 matrix
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
@@ -278,6 +279,13 @@ def main() -> int:
         "combine_GBs": combine_bytes / (stages["combine"] * 1e-3) / 1e9,
     }
     total_flops = 2.0 * N * C * E + 6.0 * A * C * H
+    # fp32 runs on the fp32 matrix cores (v_mfma_f32_32x32x2f32), whose peak differs
+    peak_mm = PEAK_F32_TFLOPS if cfg.weights == "f32" else PEAK_BF16_TFLOPS
+    used = sum(1 for c_ in counts if c_ > 0)
+    # decode shape with fp8 weights: the gate/up launch streams 2*H*C weight
+    # bytes (plus fp32 scales) for every expert that received a token
+    weight_stream = cfg.weights == "fp8" and A < 64 * E
+    gu_weight_bytes = used * (2.0 * H * C * w + 2 * H * 4)
     result = {
         "metric": METRIC,
         "value": round(N / (ms_per_step * 1e-3), 1),
@@ -296,17 +304,22 @@ def main() -> int:
                    "seq_len": cfg.T, "parallelism": "single GPU"},
         "layer_tflops": round(total_flops / (ms_per_step * 1e-3) / 1e12, 2),
         "expert_gemm_tflops": round(gemm_tflops, 2),
-        "expert_gemm_mfma_frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+        "expert_gemm_mfma_frac": round(gemm_tflops / peak_mm, 4),
         "stage_ms": {kk: round(v, 4) for kk, v in stages.items()},
         "stage_ms_forwards_averaged": n_prof,
         "hbm_frac": {kk.replace("_GBs", ""): round(v / PEAK_HBM_GBS, 4) for kk, v in hbm.items()},
         "expert_counts_max_over_mean": round(max(counts) / (sum(counts) / len(counts)), 3),
-        "roofline": {
+        "roofline": ({
+            "kernel": "gate/up fp8 weight-streaming GEMM + SwiGLU epilogue",
+            "bound": "hbm", "achieved": round(gu_weight_bytes / t_gu / 1e9, 1),
+            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": round(gu_weight_bytes / t_gu / 1e9 / PEAK_HBM_GBS, 4), "traffic": None,
+        } if weight_stream else {
             "kernel": "grouped_gemm gate/up + SwiGLU epilogue",
-            "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": round(gu_tflops / PEAK_BF16_TFLOPS, 4),
+            "bound": "mfma", "achieved": round(gu_tflops, 2), "peak": peak_mm,
+            "unit": "TFLOP/s", "frac": round(gu_tflops / peak_mm, 4),
             "traffic": None,
-        },
+        }),
         "wall_s_timed": round(wall, 3),
     }
     traffic = load_traffic(cfg)
