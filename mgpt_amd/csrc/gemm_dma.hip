@@ -52,6 +52,11 @@ struct Waves {
 
 typedef __attribute__((address_space(3))) char lds_char;
 
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+
 // One 1 KB direct-to-LDS load: lane l's 16 bytes at g land at LDS address
 // lds + 16*l.  Written as inline asm so that the compiler does not track it:
 // for the builtin it places a vmcnt(0) wait before every LDS read that it
@@ -476,35 +481,55 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][i][v] = 0.0f;
 
-    for (int kt = cur.k0; kt < cur.k1; ++kt) {
+    // The k loop for MT live 32-token sub-tiles of this wave (the rest of
+    // its 128 tokens lie past the segment: their MFMAs would only multiply
+    // padding rows, which costs time and, the chip being power-limited,
+    // clock).  Loads, fragment reads and barriers are the same for all MT.
+    auto kloop = [&](auto mt_c) __attribute__((always_inline)) {
+      constexpr int MT = decltype(mt_c)::value;
+      constexpr int kReads = kTM + kTN, kMfma = kTN * MT;
+      constexpr int kPairs = kReads < kMfma ? kReads : kMfma;
+      for (int kt = cur.k0; kt < cur.k1; ++kt) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        if (ks + 1 < 4) {
-          quarter(ks + 1);
-          frags(aslot, ks + 1, xf[(ks + 1) & 1], wf[(ks + 1) & 1]);
-        } else {
-          // next slab; after the block's last slab this reads stale units
-          // whose values are never used (one code path keeps the compiler's
-          // LDS wait counting exact)
-          aslot += 2;
-          if (aslot >= kUnits) aslot -= kUnits;
-          slab_wait();
-          quarter(0);
-          frags(aslot, 0, xf[0], wf[0]);
+        for (int ks = 0; ks < 4; ++ks) {
+          if (ks + 1 < 4) {
+            quarter(ks + 1);
+            frags(aslot, ks + 1, xf[(ks + 1) & 1], wf[(ks + 1) & 1]);
+          } else {
+            // next slab; after the block's last slab this reads stale units
+            // whose values are never used (one code path keeps the
+            // compiler's LDS wait counting exact)
+            aslot += 2;
+            if (aslot >= kUnits) aslot -= kUnits;
+            slab_wait();
+            quarter(0);
+            frags(aslot, 0, xf[0], wf[0]);
+          }
+#pragma unroll
+          for (int j = 0; j < kTN; ++j)
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+              acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][j], xf[ks & 1][i],
+                                                                  acc[j][i], 0, 0, 0);
+#pragma unroll
+          for (int q = 0; q < kPairs; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
+          }
+          if constexpr (kMfma > kPairs) __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kPairs, 0);
+          if constexpr (kReads > kPairs) __builtin_amdgcn_sched_group_barrier(0x100, kReads - kPairs, 0);
         }
-#pragma unroll
-        for (int j = 0; j < kTN; ++j)
-#pragma unroll
-          for (int i = 0; i < kTM; ++i)
-            acc[j][i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wf[ks & 1][j], xf[ks & 1][i],
-                                                                acc[j][i], 0, 0, 0);
-#pragma unroll
-        for (int q = 0; q < kTM + kTN; ++q) {
-          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
-          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // one LDS read
-        }
-        __builtin_amdgcn_sched_group_barrier(0x008, kTM * kTN - (kTM + kTN), 0);
       }
+    };
+    const int wrows = cur.tile.row_end - (cur.tile.row0 + wm * W::WTM);
+    const int mt_live = wrows <= 0 ? 0 : min(kTM, (wrows + 31) / 32);
+    static_assert(kTM == 4, "sub-tile dispatch below");
+    switch (mt_live) {
+      case 0: kloop(IntC<0>{}); break;
+      case 1: kloop(IntC<1>{}); break;
+      case 2: kloop(IntC<2>{}); break;
+      case 3: kloop(IntC<3>{}); break;
+      default: kloop(IntC<4>{}); break;
     }
     mfma_drain<NW>();
     if (cur.sidx < 0) {
