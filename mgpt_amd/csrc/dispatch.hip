@@ -118,31 +118,36 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
   }
   __syncthreads();
-  // Row copy of this slice's 16-byte chunks [q0, q1): wave w handles tokens
-  // w, w+4, ..., four tokens per step so that four loads are in flight
-  // before their k stores each.
-  const int w = tid / kWave;
-  const int l = lane_id();
+  // Row copy of this slice's 16-byte chunks [q0, q1): thread t takes chunk
+  // q0 + t % W of tokens t / W, t / W + R, ... (W = min(slice width, 256)
+  // consecutive threads per row, R = 256 / W rows per step), four tokens in
+  // flight before their k stores each.  A narrow slice still keeps (nearly)
+  // every lane busy.
   const int chunks = C * (int)sizeof(ActT) / 16;
   const int q0 = (int)((long)blockIdx.y * chunks / gridDim.y);
   const int q1 = (int)((long)(blockIdx.y + 1) * chunks / gridDim.y);
+  const int W = min(q1 - q0, 256);
+  const int R = 256 / W;
+  const int rr = tid / W;
   constexpr int U = 4;
-  for (int r0 = w; r0 < ntok; r0 += 4 * U) {
-    for (int q = q0 + l; q < q1; q += kWave) {
-      V16 v[U];
+  if (rr < R) {
+    for (int q = q0 + tid % W; q < q1; q += W) {
+      for (int r0 = rr; r0 < ntok; r0 += R * U) {
+        V16 v[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int r = min(r0 + 4 * u, ntok - 1);
-        v[u] = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C)[q];
-      }
+        for (int u = 0; u < U; ++u) {
+          const int r = min(r0 + R * u, ntok - 1);
+          v[u] = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C)[q];
+        }
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int r = r0 + 4 * u;
-        if (r >= ntok) break;
-        for (int j = 0; j < k; ++j) {
-          const int slot = s_slot[r * k + j];
-          if (slot < 0) continue;
-          reinterpret_cast<V16*>(xg + (size_t)slot * C)[q] = v[u];
+        for (int u = 0; u < U; ++u) {
+          const int r = r0 + R * u;
+          if (r >= ntok) break;
+          for (int j = 0; j < k; ++j) {
+            const int slot = s_slot[r * k + j];
+            if (slot < 0) continue;
+            reinterpret_cast<V16*>(xg + (size_t)slot * C)[q] = v[u];
+          }
         }
       }
     }
@@ -164,9 +169,10 @@ hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t*
   const int TB = router_tokens_per_block(E);
   const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
-  // Column slices: enough blocks for ~512 in all, each slice >= 64 chunks.
+  // Column slices: enough blocks for ~512 in all, each slice >= 8 chunks
+  // (128 bytes of a row).
   const int chunks = C * (int)sizeof(ActT) / 16;
-  const int slices = max(1, min(chunks / 64, (512 + nb - 1) / nb));
+  const int slices = max(1, min(chunks / 8, (512 + nb - 1) / nb));
   hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb, slices), dim3(256), 0, stream, x, topk_idx,
                      counts, base, nb, N, C, E, k, perm, slot_of, xg);
   return hipGetLastError();
