@@ -27,9 +27,12 @@ constexpr int kRouterTokens = 64;
 __host__ __device__ inline int router_tokens_per_block(int /*E*/) { return kRouterTokens; }
 
 // Router experts per wave (the router block has ceil(E / RE) <= 16 waves);
-// router weights are packed [ceil(E/RE)][C][RE], zero-padded.
+// router weights are packed [ceil(E/RE)][C][RE], zero-padded.  Two experts
+// per wave share the activation loads and conversions of their chains:
+// measured on MI355X at cfg3 (E = 16), 8 waves x 2 experts take 33.7 us,
+// 16 x 1 take 37 us and 4 x 4 take 46 us.
 __host__ __device__ inline int router_experts_per_wave(int E) {
-  return E <= 16 ? 1 : (E <= 32 ? 2 : 4);
+  return E <= 8 ? 1 : (E <= 32 ? 2 : 4);
 }
 
 // Grouped-GEMM epilogues (gemm.hip).
