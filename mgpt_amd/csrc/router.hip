@@ -47,23 +47,81 @@ __device__ __forceinline__ void topk_insert(float (&ov)[K], int (&oi)[K], float 
   }
 }
 
-template <int K>
-__device__ __forceinline__ void softmax_topk_token(const float* __restrict__ ex, float inv, int E,
-                                                   int32_t* __restrict__ idx_out,
-                                                   float* __restrict__ p_out, int* s_hist) {
-  float ov[K];
-  int oi[K];
+// Top-k of one token shared by the four lanes of a quad (lanes 4r .. 4r+3
+// of a wave): lane q runs the reference's insertion top-k over its experts
+// v = q, q+4, ... in ascending order, then two merge rounds with the partner
+// lanes (q^1, then q^2) combine the lists.  The insertion top-k with a
+// strict '>' over ascending ids keeps exactly the k largest under the total
+// order (p descending, id ascending), so merging lists under that order
+// gives the reference's result.  A merge takes the elementwise better of
+// one list and the other reversed (the top KP of both, as a bitonic
+// sequence) and sorts it with a bitonic network.
+__device__ __forceinline__ bool topk_before(float pa, int ea, float pb, int eb) {
+  return pa > pb || (pa == pb && ea < eb);
+}
+
+template <int KP>
+__device__ __forceinline__ void topk_merge_lanes(float (&ov)[KP], int (&oi)[KP], int mask) {
+  float pv[KP];
+  int pi[KP];
 #pragma unroll
-  for (int j = 0; j < K; ++j) { ov[j] = -1e9f; oi[j] = -1; }
-  for (int v = 0; v < E; ++v) {
-    const float p = fminf(fmaxf(ex[v] * inv, 1e-7f), 1.0f);
-    topk_insert<K>(ov, oi, p, v);
+  for (int j = 0; j < KP; ++j) {
+    pv[j] = __shfl_xor(ov[j], mask);
+    pi[j] = __shfl_xor(oi[j], mask);
   }
 #pragma unroll
-  for (int j = 0; j < K; ++j) {
-    idx_out[j] = oi[j];
-    p_out[j] = ov[j];
-    if (oi[j] >= 0) atomicAdd(&s_hist[oi[j]], 1);
+  for (int j = 0; j < KP; ++j) {
+    if (!topk_before(ov[j], oi[j], pv[KP - 1 - j], pi[KP - 1 - j])) {
+      ov[j] = pv[KP - 1 - j];
+      oi[j] = pi[KP - 1 - j];
+    }
+  }
+#pragma unroll
+  for (int d = KP / 2; d >= 1; d /= 2)
+#pragma unroll
+    for (int i = 0; i < KP; ++i)
+      if ((i & d) == 0 && !topk_before(ov[i], oi[i], ov[i + d], oi[i + d])) {
+        const float tp = ov[i];
+        ov[i] = ov[i + d];
+        ov[i + d] = tp;
+        const int ti = oi[i];
+        oi[i] = oi[i + d];
+        oi[i + d] = ti;
+      }
+}
+
+template <int K>
+__device__ __forceinline__ void softmax_topk_quad(const float* __restrict__ ex, float inv, int E,
+                                                  int q, bool write,
+                                                  int32_t* __restrict__ idx_out,
+                                                  float* __restrict__ p_out, int* s_hist) {
+  constexpr int KP = K <= 1 ? 1 : (K <= 2 ? 2 : (K <= 4 ? 4 : 8));
+  float lv[K];
+  int li[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) { lv[j] = -1e9f; li[j] = -1; }
+  for (int v = q; v < E; v += 4) {
+    const float p = fminf(fmaxf(ex[v] * inv, 1e-7f), 1.0f);
+    topk_insert<K>(lv, li, p, v);
+  }
+  // unfilled entries (a lane with fewer than k experts) sort last
+  float ov[KP];
+  int oi[KP];
+#pragma unroll
+  for (int j = 0; j < KP; ++j) {
+    const bool real = j < K && li[j < K ? j : 0] >= 0;
+    ov[j] = real ? lv[j < K ? j : 0] : -1e9f;
+    oi[j] = real ? li[j < K ? j : 0] : 0x7fffffff;
+  }
+  topk_merge_lanes<KP>(ov, oi, 1);
+  topk_merge_lanes<KP>(ov, oi, 2);
+  if (write && q == 0) {
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      idx_out[j] = oi[j];
+      p_out[j] = ov[j];
+      atomicAdd(&s_hist[oi[j]], 1);
+    }
   }
 }
 
@@ -218,22 +276,36 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
 }
 
 // Softmax, top-k and the block histogram of kRT tokens whose logits are in
-// s_l (all threads of the block call it).  Per token: max with strict '>'
-// from element 0 (as the reference, so NaN handling matches), the
-// exponentials in parallel with glibc's expf algorithm, then the sequential
-// sum, the clamp and the insertion top-k.  The histogram counts are written
-// expert-major as hist[e][block].
+// s_l (all threads of the block call it).  Per token (a quad of lanes): the
+// max as the reference's strict '>' scan from element 0 computes it (so NaN
+// handling matches), the exponentials in parallel with glibc's expf
+// algorithm, then the sequential sum, the clamp and the top-k
+// (softmax_topk_quad).  The histogram counts are written expert-major as
+// hist[e][block].
 __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1], float* s_m,
                                                    int* s_hist, int tok0, int N, int E, int k,
                                                    int32_t* __restrict__ topk_idx,
                                                    float* __restrict__ topk_p,
                                                    int32_t* __restrict__ hist, int num_blocks) {
   const int tid = threadIdx.x;
-  if (tid < kRT) {
-    float m = s_l[tid][0];
-    for (int v = 1; v < E; ++v)
-      if (s_l[tid][v] > m) m = s_l[tid][v];
-    s_m[tid] = m;
+  const int q = tid & 3;
+  const int quads = blockDim.x / 4;   // blockDim is a multiple of 64
+  // max per token, a quad per token: the maximum over the non-NaN logits,
+  // unless logit 0 is NaN (the reference's running max starts at element 0
+  // and '>' never replaces a NaN, nor picks one later)
+  for (int r = tid >> 2; r < kRT; r += quads) {
+    float m = -INFINITY;
+    for (int v = q; v < E; v += 4) {
+      const float l = s_l[r][v];
+      if (l > m) m = l;
+    }
+    float o = __shfl_xor(m, 1);
+    if (o > m) m = o;
+    o = __shfl_xor(m, 2);
+    if (o > m) m = o;
+    const float l0 = s_l[r][0];
+    if (l0 != l0) m = l0;
+    if (q == 0) s_m[r] = m;
   }
   __syncthreads();
   for (int p = tid; p < kRT * E; p += blockDim.x) {
@@ -241,22 +313,23 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
     s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], c_exp2_tab);
   }
   __syncthreads();
-  if (tid < kRT && tok0 + tid < N) {
-    const float* ex = s_l[tid];
-    float sum = 0.0f;
+  for (int r = tid >> 2; r < kRT; r += quads) {
+    const float* ex = s_l[r];
+    float sum = 0.0f;   // sequential, in expert order (every lane of the quad)
     for (int v = 0; v < E; ++v) sum = sum + ex[v];
     const float inv = 1.0f / fmaxf(sum, 1e-15f);
-    int32_t* io = topk_idx + (size_t)(tok0 + tid) * k;
-    float* po = topk_p + (size_t)(tok0 + tid) * k;
+    const bool write = tok0 + r < N;
+    int32_t* io = topk_idx + (size_t)(tok0 + r) * k;
+    float* po = topk_p + (size_t)(tok0 + r) * k;
     switch (k) {
-      case 1: softmax_topk_token<1>(ex, inv, E, io, po, s_hist); break;
-      case 2: softmax_topk_token<2>(ex, inv, E, io, po, s_hist); break;
-      case 3: softmax_topk_token<3>(ex, inv, E, io, po, s_hist); break;
-      case 4: softmax_topk_token<4>(ex, inv, E, io, po, s_hist); break;
-      case 5: softmax_topk_token<5>(ex, inv, E, io, po, s_hist); break;
-      case 6: softmax_topk_token<6>(ex, inv, E, io, po, s_hist); break;
-      case 7: softmax_topk_token<7>(ex, inv, E, io, po, s_hist); break;
-      default: softmax_topk_token<8>(ex, inv, E, io, po, s_hist); break;
+      case 1: softmax_topk_quad<1>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 2: softmax_topk_quad<2>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 3: softmax_topk_quad<3>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 4: softmax_topk_quad<4>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 5: softmax_topk_quad<5>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 6: softmax_topk_quad<6>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 7: softmax_topk_quad<7>(ex, inv, E, q, write, io, po, s_hist); break;
+      default: softmax_topk_quad<8>(ex, inv, E, q, write, io, po, s_hist); break;
     }
   }
   __syncthreads();
