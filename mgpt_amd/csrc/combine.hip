@@ -250,6 +250,15 @@ hipError_t launch_combine(const ActT* out_rows, const int32_t* topk_idx, const f
                            stream, out_rows, topk_p, slot_of, N, C, y);
       break;
     }
+    // fixed k: every row chunk of a token in flight at once
+    case 6:
+      launch_combine_k<ActT, 1, 6>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
+                                   y);
+      break;
+    case 8:
+      launch_combine_k<ActT, 1, 8>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
+                                   y);
+      break;
     default:
       launch_combine_k<ActT, 1, 0>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
                                    y);
