@@ -290,6 +290,11 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
   const int tid = threadIdx.x;
   const int q = tid & 3;
   const int quads = blockDim.x / 4;   // blockDim is a multiple of 64
+  // expf's 2^(i/32) table in LDS: read per lane at a data-dependent index,
+  // from global memory each lookup would put a load round trip on the
+  // critical path of every exponential
+  __shared__ uint64_t s_tab[32];
+  if (tid < 32) s_tab[tid] = c_exp2_tab[tid];
   // max per token, a quad per token: the maximum over the non-NaN logits,
   // unless logit 0 is NaN (the reference's running max starts at element 0
   // and '>' never replaces a NaN, nor picks one later)
@@ -310,7 +315,7 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
   __syncthreads();
   for (int p = tid; p < kRT * E; p += blockDim.x) {
     const int r = p / E, e = p % E;
-    s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], c_exp2_tab);
+    s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], s_tab);
   }
   __syncthreads();
   for (int r = tid >> 2; r < kRT; r += quads) {
