@@ -153,6 +153,39 @@ def test_split_k_last_round():
     check_close(y[rows], O.tokens(inp, ref["idx"], ref["topp"], rows), TOL["bf16"], "split_k")
 
 
+ROUTER_SHAPES = [
+    # (E, k, tweak): experts-per-wave groupings 1 / 2 / 4 at their boundaries,
+    # E below and not a multiple of 4 (the top-k quad has lanes with fewer
+    # experts than k, or none), k up to 8, and tie-heavy logits where the
+    # lanes' lists hold equal probabilities and the merges decide by id
+    (2, 2, ""), (3, 2, ""), (5, 4, ""), (8, 8, ""), (9, 3, ""), (17, 5, ""),
+    (32, 2, ""), (33, 7, ""), (63, 8, ""), (64, 1, ""),
+    (7, 3, "tie_router"), (37, 5, "tie_router"), (64, 8, "tie_router"),
+    (13, 4, "wide_router"), (40, 6, "wide_router"),
+]
+
+
+@pytest.mark.parametrize("E,k,tweak", ROUTER_SHAPES)
+def test_router_shapes_against_oracle(E, k, tweak):
+    """Routing bit for bit and outputs at 1e-5 (fp32) against the oracle over
+    expert counts and ties that the fixtures do not cover (the oracle is
+    pinned to the reference by tests/test_oracle.py)."""
+    cfg = wl.MoEConfig(f"router_E{E}_k{k}", 70, 64, E, k, 64, "f32", "f32", "normal")
+    inp = wl.make_inputs(cfg, C.SEED + E * 10 + k, bias_std=0.05)
+    if tweak == "tie_router":
+        inp.Wr[:] = inp.Wr[:, :1]
+        inp.br[:] = 0.0
+    elif tweak == "wide_router":
+        inp.Wr[:] = inp.Wr * np.float32(100.0)
+    layer, y, r, _, _ = run_gpu(inp)
+    ref = O.forward(inp)
+    assert np.array_equal(r["counts"], ref["counts"]), "counts"
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["topk_p"].view(np.uint32), ref["topp"].view(np.uint32)), "topk_p"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    check_close(y, ref["y"], TOL["f32"], cfg.name)
+
+
 def test_deterministic_and_repeatable():
     case = C.ALL_CASES["bf16_e64_k6"]
     inp = C.build_inputs(case)
