@@ -186,6 +186,34 @@ def test_router_shapes_against_oracle(E, k, tweak):
     check_close(y, ref["y"], TOL["f32"], cfg.name)
 
 
+GEMM_SHAPES = [
+    # (N, C, H, E, k): bf16 prefill shapes on the direct-to-LDS GEMM with
+    # padded hidden (H % 128 != 0) and padded output features (C % 256 != 0),
+    # ragged segments, zero-count experts and split last rounds of several
+    # sizes; sampled rows against the oracle's per-token forward
+    (3000, 320, 200, 5, 2),
+    (5000, 1088, 704, 12, 3),
+    (2048, 64, 128, 3, 1),
+    (9000, 512, 1000, 20, 4),
+]
+
+
+@pytest.mark.parametrize("N,Cm,H,E,k", GEMM_SHAPES)
+def test_bf16_gemm_shapes(N, Cm, H, E, k):
+    cfg = wl.MoEConfig(f"gemm_{N}_{Cm}_{H}_{E}_{k}", N, Cm, E, k, H, "bf16", "bf16", "zipf")
+    inp = wl.make_inputs(cfg, C.SEED + N + E, bias_std=0.02)
+    inp.x[:] = wl.bf16_round(inp.x)
+    inp.Wr[:] = wl.bf16_round(inp.Wr)
+    layer, y, r, _, _ = run_gpu(inp)
+    ref = O.forward(inp, with_y=False)
+    assert np.array_equal(r["counts"], ref["counts"]), "counts"
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    print(f"{cfg.name}: counts {ref['counts'].tolist()}", flush=True)
+    rows = C.sample_rows(N, 128)
+    check_close(y[rows], O.tokens(inp, ref["idx"], ref["topp"], rows), TOL["bf16"], cfg.name)
+
+
 def test_deterministic_and_repeatable():
     case = C.ALL_CASES["bf16_e64_k6"]
     inp = C.build_inputs(case)
