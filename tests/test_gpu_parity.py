@@ -214,6 +214,31 @@ def test_bf16_gemm_shapes(N, Cm, H, E, k):
     check_close(y[rows], O.tokens(inp, ref["idx"], ref["topp"], rows), TOL["bf16"], cfg.name)
 
 
+DECODE_SHAPES = [
+    # (N, C, H, E, k): fp8-weight decode shapes (N*k < 64*E) on the
+    # weight-streaming GEMM: experts with more than one 32-row m-tile, many
+    # experts without tokens, a hidden size that is not a multiple of 256
+    (200, 512, 384, 16, 4),
+    (8, 256, 256, 64, 2),
+    (33, 1024, 640, 32, 8),
+]
+
+
+@pytest.mark.parametrize("N,Cm,H,E,k", DECODE_SHAPES)
+def test_fp8_decode_shapes(N, Cm, H, E, k):
+    cfg = wl.MoEConfig(f"decode_{N}_{Cm}_{H}_{E}_{k}", N, Cm, E, k, H, "bf16", "fp8", "normal")
+    inp = wl.make_inputs(cfg, C.SEED + 7 * N + E, bias_std=0.02)
+    inp.x[:] = wl.bf16_round(inp.x)
+    inp.Wr[:] = wl.bf16_round(inp.Wr)
+    layer, y, r, _, _ = run_gpu(inp)
+    ref = O.forward(inp)
+    assert np.array_equal(r["counts"], ref["counts"]), "counts"
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    print(f"{cfg.name}: counts {ref['counts'].tolist()}", flush=True)
+    check_close(y, ref["y"], TOL["fp8"], cfg.name)
+
+
 def test_deterministic_and_repeatable():
     case = C.ALL_CASES["bf16_e64_k6"]
     inp = C.build_inputs(case)
