@@ -37,8 +37,6 @@ def stage_of(kernel_name: str):
     short = kernel_name.replace("(anonymous namespace)", "").split("(")[0]
     if re.search(r"router_(?:topk|logits|softmax)", short):
         return "router_topk"
-    if "expert_scan" in short:
-        return "expert_scan"
     if "permute_kernel" in short:
         return "permute"
     if re.search(r"combine\d?_kernel", short):

@@ -122,10 +122,10 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
  * forward records HIP events on its stream at the stage boundaries (into a
  * ring of the last 64 forwards; enabling resets it).  mgpt_moe_stage_times
  * waits for the last profiled forward and returns the mean stage durations
- * in ms over the recorded forwards: [0] router+top-k, [1] dispatch scan,
- * [2] permute, [3] gate/up GEMM + SwiGLU, [4] down GEMM, [5] combine; if
- * n > 6, ms[6] receives the number of forwards averaged. */
-#define MGPT_MOE_NUM_STAGES 6
+ * in ms over the recorded forwards: [0] router+top-k+histogram, [1] dispatch
+ * (count scan + permutation), [2] gate/up GEMM + SwiGLU, [3] down GEMM,
+ * [4] combine; if n > 5, ms[5] receives the number of forwards averaged. */
+#define MGPT_MOE_NUM_STAGES 5
 int mgpt_moe_set_profiling(mgpt_moe* h, int enable);
 int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n);
 

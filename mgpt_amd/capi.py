@@ -23,8 +23,8 @@ MGPT_ERR_HIP = 5
 MGPT_ERR_OUT_OF_MEMORY = 6
 
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8_E4M3 = 0, 1, 2
-NUM_STAGES = 6
-STAGE_NAMES = ["router_topk", "expert_scan", "permute", "gemm_gateup", "gemm_down", "combine"]
+NUM_STAGES = 5
+STAGE_NAMES = ["router_topk", "permute", "gemm_gateup", "gemm_down", "combine"]
 
 
 class Config(ctypes.Structure):

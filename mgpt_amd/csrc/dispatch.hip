@@ -7,8 +7,11 @@
 // expert's segment holds its assignments in ascending i.  Here that order is
 // rebuilt as a counting sort that needs no host round-trip:
 //   counts[e]      = sum over router blocks b of hist[e][b]
-//   base[e][b]     = offset[e] + sum_{b' < b} hist[e][b']      (scan kernel)
+//   base[e][b]     = offset[e] + sum_{b' < b} hist[e][b']
 //   slot(i)        = base[e][block(i)] + #{i' < i in block(i) : e(i') = e}
+// For small dispatches each permute block sums the histogram columns it
+// needs itself (E x nb ints, L2-resident), so the scan costs no launch of
+// its own; large ones scan first (expert_scan_kernel).
 // The within-block rank comes from wave ballots over 64 consecutive ids at
 // a time (6 ballots give the lanes holding the same expert id, E <= 64).
 // The permute kernel then copies each token's row once from HBM into all k
@@ -18,9 +21,9 @@
 namespace mgpt {
 namespace {
 
-// One block per expert: exclusive scan of hist[e][0..nb) -> base[e][.],
-// total -> counts[e].  (offset[e] is added by the consumers, which read the
-// E <= 64 counts themselves.)
+// Large dispatches (E x nb beyond kFoldScan): one block per expert scans
+// hist[e][0..nb) into base[e][.] (the assignments of the router blocks
+// before b) and counts[e]; the permute blocks then read their bases.
 __global__ __launch_bounds__(256) void expert_scan_kernel(const int32_t* __restrict__ hist, int nb,
                                                           int32_t* __restrict__ base,
                                                           int32_t* __restrict__ counts) {
@@ -47,6 +50,13 @@ __global__ __launch_bounds__(256) void expert_scan_kernel(const int32_t* __restr
   if (tid == 0) counts[e] = s_carry;
 }
 
+// Histogram entries (E x nb) up to which each permute block sums the
+// columns it needs itself instead of a scan launch: quadratic in nb, so
+// cheap only for small dispatches (cfg1-cfg3, decode); measured on MI355X
+// the fold saves ~5 us at cfg1/cfg2 and costs ~28 us at cfg4 (E x nb =
+// 32768).
+constexpr int kFoldScan = 8192;
+
 // 16-byte vector of activations.
 struct alignas(16) V16 {
   uint32_t w[4];
@@ -60,10 +70,12 @@ struct alignas(16) V16 {
 template <typename ActT>
 __global__ __launch_bounds__(256) void permute_kernel(
     const ActT* __restrict__ x, const int32_t* __restrict__ topk_idx,
-    const int32_t* __restrict__ counts, const int32_t* __restrict__ base, int nb, int N, int C,
-    int E, int k, int32_t* __restrict__ perm, int32_t* __restrict__ slot_of,
-    ActT* __restrict__ xg) {
+    const int32_t* __restrict__ hist, const int32_t* __restrict__ base, int nb, int N, int C,
+    int E, int k, int32_t* __restrict__ counts, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slot_of, ActT* __restrict__ xg) {
   __shared__ int s_base[kMaxExperts];
+  __shared__ int s_pre[kMaxExperts];
+  __shared__ int s_tot[kMaxExperts];
   __shared__ int s_run[kMaxExperts];
   __shared__ int s_slot[kRouterTokens * kMaxTopK];
   const int tid = threadIdx.x;
@@ -76,14 +88,49 @@ __global__ __launch_bounds__(256) void permute_kernel(
   const size_t flat0 = (size_t)tok0 * k;
 
   for (int f = tid; f < kRouterTokens * kMaxTopK; f += 256) s_slot[f] = -1;
+  if (base) {
+    // scanned by expert_scan_kernel
+    if (tid < E) {
+      s_pre[tid] = base[(size_t)tid * nb + b];
+      s_tot[tid] = counts[tid];
+    }
+  } else {
+    // Per expert: the assignments of the router blocks before this one and
+    // of all blocks.  G consecutive lanes of one wave share an expert (G =
+    // 256 / E rounded to a power of two, at most 64), each summing every
+    // G-th block, then reduce across the group.
+    int ep = 1;
+    while (ep < E) ep <<= 1;
+    const int G = min(kWave, 256 / ep);
+    const int e = tid / G, part = tid % G;
+    int pre = 0, tot = 0;
+    if (e < E) {
+      for (int bb = part; bb < nb; bb += G) {
+        const int v = hist[(size_t)e * nb + bb];
+        tot += v;
+        if (bb < b) pre += v;
+      }
+    }
+    for (int d = G / 2; d >= 1; d >>= 1) {
+      pre += __shfl_xor(pre, d, kWave);
+      tot += __shfl_xor(tot, d, kWave);
+    }
+    if (e < E && part == 0) {
+      s_pre[e] = pre;
+      s_tot[e] = tot;
+    }
+  }
+  __syncthreads();
   if (tid < kWave) {
-    // Exclusive offsets of the experts, then this block's bases.
+    // Exclusive offsets of the experts, then this block's bases; block
+    // (0, 0) publishes the counts for the GEMMs and the caller.
     const int l = tid;
-    const int cnt = (l < E) ? counts[l] : 0;
+    const int cnt = (l < E) ? s_tot[l] : 0;
     const int excl = wave_incl_scan(cnt) - cnt;
     if (l < E) {
-      s_base[l] = excl + base[(size_t)l * nb + b];
+      s_base[l] = excl + s_pre[l];
       s_run[l] = 0;
+      if (!base && writer && b == 0) counts[l] = cnt;
     }
   }
   __syncthreads();
@@ -156,33 +203,30 @@ __global__ __launch_bounds__(256) void permute_kernel(
 
 }  // namespace
 
-hipError_t launch_expert_scan(const int32_t* hist, int nb, int E, int32_t* base, int32_t* counts,
-                              hipStream_t stream) {
-  hipLaunchKernelGGL(expert_scan_kernel, dim3(E), dim3(256), 0, stream, hist, nb, base, counts);
-  return hipGetLastError();
-}
-
 template <typename ActT>
-hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t* counts,
-                          const int32_t* base, int N, int C, int E, int k, int32_t* perm,
-                          int32_t* slot_of, ActT* xg, hipStream_t stream) {
+hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t* hist,
+                          int32_t* base, int N, int C, int E, int k, int32_t* counts,
+                          int32_t* perm, int32_t* slot_of, ActT* xg, hipStream_t stream) {
   const int TB = router_tokens_per_block(E);
   const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
+  const bool fold = E * nb <= kFoldScan;
+  if (!fold)
+    hipLaunchKernelGGL(expert_scan_kernel, dim3(E), dim3(256), 0, stream, hist, nb, base, counts);
   // Column slices: enough blocks for ~512 in all, each slice >= 8 chunks
   // (128 bytes of a row).
   const int chunks = C * (int)sizeof(ActT) / 16;
   const int slices = max(1, min(chunks / 8, (512 + nb - 1) / nb));
   hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb, slices), dim3(256), 0, stream, x, topk_idx,
-                     counts, base, nb, N, C, E, k, perm, slot_of, xg);
+                     hist, fold ? nullptr : base, nb, N, C, E, k, counts, perm, slot_of, xg);
   return hipGetLastError();
 }
 
-template hipError_t launch_permute<float>(const float*, const int32_t*, const int32_t*,
-                                          const int32_t*, int, int, int, int, int32_t*, int32_t*,
+template hipError_t launch_permute<float>(const float*, const int32_t*, const int32_t*, int32_t*,
+                                          int, int, int, int, int32_t*, int32_t*, int32_t*,
                                           float*, hipStream_t);
 template hipError_t launch_permute<bf16_t>(const bf16_t*, const int32_t*, const int32_t*,
-                                           const int32_t*, int, int, int, int, int32_t*,
+                                           int32_t*, int, int, int, int, int32_t*, int32_t*,
                                            int32_t*, bf16_t*, hipStream_t);
 
 }  // namespace mgpt

@@ -28,10 +28,9 @@ template <typename ActT>
 hipError_t launch_router(const ActT*, const float*, const float*, const float*, int, int, int,
                          int, int32_t*, float*, int32_t*, float*, hipStream_t);
 hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
-hipError_t launch_expert_scan(const int32_t*, int, int, int32_t*, int32_t*, hipStream_t);
 template <typename ActT>
-hipError_t launch_permute(const ActT*, const int32_t*, const int32_t*, const int32_t*, int, int,
-                          int, int, int32_t*, int32_t*, ActT*, hipStream_t);
+hipError_t launch_permute(const ActT*, const int32_t*, const int32_t*, int32_t*, int, int, int,
+                          int, int32_t*, int32_t*, int32_t*, ActT*, hipStream_t);
 template <typename ActT>
 hipError_t launch_combine(const ActT*, const int32_t*, const float*, const int32_t*, int, int, int,
                           ActT*, hipStream_t);
@@ -407,16 +406,14 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
   float* logits = h->router_split(N) ? (float*)(ws + L.logits) : nullptr;
   HIP_TRY(launch_router<ActT>(x, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits, st));
   HIP_TRY(mark(1));
-  HIP_TRY(launch_expert_scan(hist, nb, E, base, counts, st));
+  HIP_TRY(launch_permute<ActT>(x, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg, st));
   HIP_TRY(mark(2));
-  HIP_TRY(launch_permute<ActT>(x, idx, counts, base, N, C, E, k, perm, slot_of, xg, st));
-  HIP_TRY(mark(3));
   if constexpr (sizeof(ActT) == 4) {
     const int mt = (int)((A + 63) / 64) + E;
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiGateUp, float>(
         xg, (const float*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp,
         mt, st)));
-    HIP_TRY(mark(4));
+    HIP_TRY(mark(3));
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiDown, float>(
         hb, (const float*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
         st)));
@@ -428,14 +425,14 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
         // weight streaming: the persistent direct-to-LDS decode kernel
         HIP_TRY(launch_gemm_decode<kEpiGateUp>(xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu,
                                                counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt, st));
-        HIP_TRY(mark(4));
+        HIP_TRY(mark(3));
         HIP_TRY(launch_gemm_decode<kEpiDown>(hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr,
                                              counts, E, Hp, Cp, C, Cp, ob, C, mt, st));
       } else if (fp8) {
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
             xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
             Hp, mt, st)));
-        HIP_TRY(mark(4));
+        HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiDown, bf16_t>(
             hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
             st)));
@@ -443,7 +440,7 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiGateUp, bf16_t>(
             xg, (const bf16_t*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp,
             hb, Hp, mt, st)));
-        HIP_TRY(mark(4));
+        HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiDown, bf16_t>(
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
             mt, st)));
@@ -457,7 +454,7 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
       HIP_TRY(launch_gemm_dma<kEpiGateUp>(xg, (const bf16_t*)h->wgu, h->bg, h->bu, counts, E, C,
                                           2 * Hp, 2 * Hp, Hp, hb, Hp, mt, nullptr, h->num_cus,
                                           st));
-      HIP_TRY(mark(4));
+      HIP_TRY(mark(3));
       HIP_TRY(launch_gemm_dma<kEpiDown>(hb, (const bf16_t*)h->wd, h->bd, nullptr, counts, E, Hp,
                                         Cp, C, Cp, ob, C, mt, part, h->num_cus, st));
     } else {
@@ -466,7 +463,7 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
             xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
             Hp, mt, st)));
-        HIP_TRY(mark(4));
+        HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, fp8_t, kEpiDown, bf16_t>(
             hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
             st)));
@@ -474,16 +471,16 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiGateUp, bf16_t>(
             xg, (const bf16_t*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp,
             hb, Hp, mt, st)));
-        HIP_TRY(mark(4));
+        HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiDown, bf16_t>(
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
             mt, st)));
       }
     }
   }
-  HIP_TRY(mark(5));
+  HIP_TRY(mark(4));
   HIP_TRY(launch_combine<ActT>(ob, idx, topp, slot_of, N, C, k, y, st));
-  HIP_TRY(mark(6));
+  HIP_TRY(mark(5));
   if (prof) ++h->prof_count;
   HIP_TRY(hipEventRecord(h->done, st));
   h->done_valid = true;
