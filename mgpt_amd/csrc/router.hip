@@ -47,10 +47,10 @@ __device__ __forceinline__ void topk_insert(float (&ov)[K], int (&oi)[K], float 
   }
 }
 
-// Top-k of one token shared by the four lanes of a quad (lanes 4r .. 4r+3
-// of a wave): lane q runs the reference's insertion top-k over its experts
-// v = q, q+4, ... in ascending order, then two merge rounds with the partner
-// lanes (q^1, then q^2) combine the lists.  The insertion top-k with a
+// Top-k of one token shared by L lanes of a wave (L a power of two, lanes
+// L*r .. L*r+L-1): lane q runs the reference's insertion top-k over its
+// experts v = q, q+L, ... in ascending order, then log2(L) merge rounds
+// with the partner lanes (q^1, q^2, ...) combine the lists.  The insertion top-k with a
 // strict '>' over ascending ids keeps exactly the k largest under the total
 // order (p descending, id ascending), so merging lists under that order
 // gives the reference's result.  A merge takes the elementwise better of
@@ -91,8 +91,8 @@ __device__ __forceinline__ void topk_merge_lanes(float (&ov)[KP], int (&oi)[KP],
 }
 
 template <int K>
-__device__ __forceinline__ void softmax_topk_quad(const float* __restrict__ ex, float inv, int E,
-                                                  int q, bool write,
+__device__ __forceinline__ void softmax_topk_lanes(const float* __restrict__ ex, float inv, int E,
+                                                  int q, int L, bool write,
                                                   int32_t* __restrict__ idx_out,
                                                   float* __restrict__ p_out, int* s_hist) {
   constexpr int KP = K <= 1 ? 1 : (K <= 2 ? 2 : (K <= 4 ? 4 : 8));
@@ -100,7 +100,7 @@ __device__ __forceinline__ void softmax_topk_quad(const float* __restrict__ ex, 
   int li[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) { lv[j] = -1e9f; li[j] = -1; }
-  for (int v = q; v < E; v += 4) {
+  for (int v = q; v < E; v += L) {
     const float p = fminf(fmaxf(ex[v] * inv, 1e-7f), 1.0f);
     topk_insert<K>(lv, li, p, v);
   }
@@ -113,8 +113,7 @@ __device__ __forceinline__ void softmax_topk_quad(const float* __restrict__ ex, 
     ov[j] = real ? lv[j < K ? j : 0] : -1e9f;
     oi[j] = real ? li[j < K ? j : 0] : 0x7fffffff;
   }
-  topk_merge_lanes<KP>(ov, oi, 1);
-  topk_merge_lanes<KP>(ov, oi, 2);
+  for (int mask = 1; mask < L; mask <<= 1) topk_merge_lanes<KP>(ov, oi, mask);
   if (write && q == 0) {
 #pragma unroll
     for (int j = 0; j < K; ++j) {
@@ -276,11 +275,11 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
 }
 
 // Softmax, top-k and the block histogram of kRT tokens whose logits are in
-// s_l (all threads of the block call it).  Per token (a quad of lanes): the
+// s_l (all threads of the block call it).  Per token (L lanes): the
 // max as the reference's strict '>' scan from element 0 computes it (so NaN
 // handling matches), the exponentials in parallel with glibc's expf
 // algorithm, then the sequential sum, the clamp and the top-k
-// (softmax_topk_quad).  The histogram counts are written expert-major as
+// (softmax_topk_lanes).  The histogram counts are written expert-major as
 // hist[e][block].
 __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1], float* s_m,
                                                    int* s_hist, int tok0, int N, int E, int k,
@@ -288,26 +287,30 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
                                                    float* __restrict__ topk_p,
                                                    int32_t* __restrict__ hist, int num_blocks) {
   const int tid = threadIdx.x;
-  const int q = tid & 3;
-  const int quads = blockDim.x / 4;   // blockDim is a multiple of 64
+  // L lanes per token: the largest power of two <= min(16, blockDim / 64),
+  // so that the kRT tokens use (most of) the block
+  int L = 1;
+  while (2 * L <= 16 && 2 * L * kRT <= (int)blockDim.x) L *= 2;
+  const int q = tid & (L - 1);
+  const int groups = blockDim.x / L;
   // expf's 2^(i/32) table in LDS: read per lane at a data-dependent index,
   // from global memory each lookup would put a load round trip on the
   // critical path of every exponential
   __shared__ uint64_t s_tab[32];
   if (tid < 32) s_tab[tid] = c_exp2_tab[tid];
-  // max per token, a quad per token: the maximum over the non-NaN logits,
+  // max per token (its L lanes): the maximum over the non-NaN logits,
   // unless logit 0 is NaN (the reference's running max starts at element 0
   // and '>' never replaces a NaN, nor picks one later)
-  for (int r = tid >> 2; r < kRT; r += quads) {
+  for (int r = tid / L; r < kRT; r += groups) {
     float m = -INFINITY;
-    for (int v = q; v < E; v += 4) {
+    for (int v = q; v < E; v += L) {
       const float l = s_l[r][v];
       if (l > m) m = l;
     }
-    float o = __shfl_xor(m, 1);
-    if (o > m) m = o;
-    o = __shfl_xor(m, 2);
-    if (o > m) m = o;
+    for (int mask = 1; mask < L; mask <<= 1) {
+      const float o = __shfl_xor(m, mask);
+      if (o > m) m = o;
+    }
     const float l0 = s_l[r][0];
     if (l0 != l0) m = l0;
     if (q == 0) s_m[r] = m;
@@ -318,23 +321,23 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
     s_l[r][e] = mgpt_expf::expf_glibc(s_l[r][e] - s_m[r], s_tab);
   }
   __syncthreads();
-  for (int r = tid >> 2; r < kRT; r += quads) {
+  for (int r = tid / L; r < kRT; r += groups) {
     const float* ex = s_l[r];
-    float sum = 0.0f;   // sequential, in expert order (every lane of the quad)
+    float sum = 0.0f;   // sequential, in expert order (every lane of the token)
     for (int v = 0; v < E; ++v) sum = sum + ex[v];
     const float inv = 1.0f / fmaxf(sum, 1e-15f);
     const bool write = tok0 + r < N;
     int32_t* io = topk_idx + (size_t)(tok0 + r) * k;
     float* po = topk_p + (size_t)(tok0 + r) * k;
     switch (k) {
-      case 1: softmax_topk_quad<1>(ex, inv, E, q, write, io, po, s_hist); break;
-      case 2: softmax_topk_quad<2>(ex, inv, E, q, write, io, po, s_hist); break;
-      case 3: softmax_topk_quad<3>(ex, inv, E, q, write, io, po, s_hist); break;
-      case 4: softmax_topk_quad<4>(ex, inv, E, q, write, io, po, s_hist); break;
-      case 5: softmax_topk_quad<5>(ex, inv, E, q, write, io, po, s_hist); break;
-      case 6: softmax_topk_quad<6>(ex, inv, E, q, write, io, po, s_hist); break;
-      case 7: softmax_topk_quad<7>(ex, inv, E, q, write, io, po, s_hist); break;
-      default: softmax_topk_quad<8>(ex, inv, E, q, write, io, po, s_hist); break;
+      case 1: softmax_topk_lanes<1>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      case 2: softmax_topk_lanes<2>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      case 3: softmax_topk_lanes<3>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      case 4: softmax_topk_lanes<4>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      case 5: softmax_topk_lanes<5>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      case 6: softmax_topk_lanes<6>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      case 7: softmax_topk_lanes<7>(ex, inv, E, q, L, write, io, po, s_hist); break;
+      default: softmax_topk_lanes<8>(ex, inv, E, q, L, write, io, po, s_hist); break;
     }
   }
   __syncthreads();
@@ -393,7 +396,7 @@ __global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
   if (e < E && tok0 + lane < N) logits[(size_t)(tok0 + lane) * E + e] = acc[0] + br[e];
 }
 
-__global__ __launch_bounds__(256) void router_softmax_kernel(const float* __restrict__ logits,
+__global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __restrict__ logits,
                                                              int N, int E, int k,
                                                              int32_t* __restrict__ topk_idx,
                                                              float* __restrict__ topk_p,
@@ -427,7 +430,7 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
     hipLaunchKernelGGL(router_logits_kernel<ActT>,
                        dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
                        dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits);
-    hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(256), 0, stream, logits, N, E, k,
+    hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(1024), 0, stream, logits, N, E, k,
                        topk_idx, topk_p, hist, nb);
     return hipGetLastError();
   }
