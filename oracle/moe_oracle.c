@@ -1,19 +1,26 @@
 /*
- * moe_oracle.c -- CPU restatement of mgpt's MoE block forward.
+ * moe_oracle.c -- CPU restatement of mgpt's MoE block forward and backward.
  *
  * TEST INFRASTRUCTURE ONLY (see moe_oracle.h): the checker for the HIP path,
  * never part of it.  Build with -O2/-O3 and -ffp-contract=off; FMA
  * contraction changes the bits (the reference is pinned with the same flag).
  *
  * Pinning (each function has at least one check that a plausible mistake
- * fails; tests/test_oracle.py):
+ * fails; tests/test_oracle.py, tests/test_oracle_backward.py):
  *   - all functions: bit-for-bit against the compiled reference on committed
  *     golden fixtures (tests/golden/, made by tests/golden/make_golden.py
  *     from oracle/_ref/ref_driver);
  *   - router/softmax/topk/dispatch/scatter: closed forms and brute force
  *     (one-hot W_r, softmax([1,2,3]), clamp and NaN cases, stable sort);
  *   - experts: fp64 textbook SwiGLU within an error bound, and the
- *     "all experts identical" invariant y = (sum_j p_j) * FFN(x).
+ *     "all experts identical" invariant y = (sum_j p_j) * FFN(x);
+ *   - backward: every gradient against float64 central finite differences
+ *     of the differentiated loss, plus softmax-Jacobian and routing
+ *     invariants.  The ORACLE_PLANT_* macros each build a copy with one
+ *     plausible mistake (dropped load-balance term, wrong sign in the SiLU
+ *     derivative, ungated expert gradient); the tests build those copies
+ *     and show that both the golden and the finite-difference checks
+ *     reject them.  The shipped build defines none of them.
  */
 #include "moe_oracle.h"
 #include <math.h>
@@ -222,6 +229,203 @@ int oracle_moe_tokens(int C, int H, int E, int k, int n_sel, const int32_t* tok,
     }
   }
   free(g); free(u); free(o);
+  return 0;
+}
+
+/* Backward of one Linear layer over `rows` rows, utils/Tensor.cpp CPU
+ * branches as reached from layers/LinearLayer.cpp:33-80:
+ *   db[j] += sum_r dout[r][j]            sum_rows_into :1599-1617, add_grad
+ *                                        :638-650 (r ascending from 0)
+ *   dW[i][j] += sum_r in[r][i]*dout[r][j] transpose + matmul2d_raw :567-577
+ *                                        (i-k-j: the sum runs over r
+ *                                        ascending, from 0, then add_grad)
+ *   din[r][i] = sum_j dout[r][j]*W[i][j] matmul2d_raw against W^T (j asc.)
+ * Input rows are addressed through in_rows[r], so gathered rows need no copy. */
+static void linear_backward(int rows, int Kin, int Nout, const float* const* in_rows,
+                            const float* dout, const float* W, float* dW,
+                            float* db, float* din, float* tmp) {
+  for (int j = 0; j < Nout; ++j) tmp[j] = 0.0f;
+  for (int r = 0; r < rows; ++r)
+    for (int j = 0; j < Nout; ++j) tmp[j] += dout[(size_t)r * Nout + j];
+  for (int j = 0; j < Nout; ++j) db[j] += tmp[j];
+  for (int i = 0; i < Kin; ++i) {
+    for (int j = 0; j < Nout; ++j) tmp[j] = 0.0f;
+    for (int r = 0; r < rows; ++r) {
+      const float a = in_rows[r][i];
+      const float* dr = dout + (size_t)r * Nout;
+      for (int j = 0; j < Nout; ++j) tmp[j] += a * dr[j];
+    }
+    float* wr = dW + (size_t)i * Nout;
+    for (int j = 0; j < Nout; ++j) wr[j] += tmp[j];
+  }
+  for (int r = 0; r < rows; ++r) {
+    const float* dr = dout + (size_t)r * Nout;
+    float* o = din + (size_t)r * Kin;
+    for (int i = 0; i < Kin; ++i) {
+      const float* wi = W + (size_t)i * Nout;
+      float acc = 0.0f;
+      for (int j = 0; j < Nout; ++j) acc += dr[j] * wi[j];
+      o[i] = acc;
+    }
+  }
+}
+
+/* layers/MoELayer.cpp:130-223 (backward_into), CPU path, after the forward
+ * of :28-128 on the same inputs:
+ *   B1 scatter backward, utils/Tensor.cpp:1410-1438: per slot (ascending),
+ *      dgo[slot] = dy[t]*p and dp[flat] = sum_c o[slot][c]*dy[t][c];
+ *   B2 per expert in id order over its slots (layers/MoELayer.cpp:158-180),
+ *      SwiGLU backward layers/SwiGLU.cpp:57-96: down Linear, then the fused
+ *      swiglu_backward utils/Tensor.cpp:2006-2030 (sig = 1/(1+exp(-g));
+ *      d_up = dd*(g*sig); d_gate = (dd*u)*(sig*(1+g*(1-sig)))), then the gate
+ *      and up Linears, and din = d_gate_proj + d_up_proj;
+ *   B3 gather backward utils/Tensor.cpp:1440-1460 into a zeroed dx, slots
+ *      ascending;
+ *   B4 scatter_indices_into :1462-1484: dP[t][idx] = dp (other entries 0);
+ *   B5 load-balance term layers/MoELayer.cpp:193-200: dP[t][e] +=
+ *      (0.01*E*f_e)/N with f_e = counts[e]/N (operator+ broadcast :331-342);
+ *   B6 softmax backward on the clamped probs :885-905: s = sum_e dP*P
+ *      (ascending); dL = P*(dP - s);
+ *   B7 router Linear backward (as linear_backward);
+ *   B8 dx = dx + router_din (Tensor::add_into :1579-1597). */
+int oracle_moe_backward(int N, int C, int H, int E, int k, const float* x,
+                        const float* Wr, const float* br, const float* Wg,
+                        const float* bg, const float* Wu, const float* bu,
+                        const float* Wd, const float* bd, const float* dy,
+                        float* dx, float* dWr, float* dbr, float* dWg,
+                        float* dbg, float* dWu, float* dbu, float* dWd,
+                        float* dbd) {
+  if (N < 0 || C <= 0 || H <= 0 || E <= 0 || k <= 0 || k > E) return 1;
+  const size_t A = (size_t)N * k;
+  const size_t NE = (size_t)N * E;
+  float* L = (float*)malloc(sizeof(float) * (NE + 1));
+  float* P = (float*)malloc(sizeof(float) * (NE + 1));
+  int32_t* I = (int32_t*)malloc(sizeof(int32_t) * (A + 1));
+  float* TP = (float*)malloc(sizeof(float) * (A + 1));
+  int32_t* CN = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+  int32_t* OF = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+  int32_t* PM = (int32_t*)malloc(sizeof(int32_t) * (A + 1));
+  float* G = (float*)malloc(sizeof(float) * (A * H + 1));   /* gate pre-act */
+  float* U = (float*)malloc(sizeof(float) * (A * H + 1));   /* up */
+  float* Act = (float*)malloc(sizeof(float) * (A * H + 1)); /* silu(g)*u */
+  float* O = (float*)malloc(sizeof(float) * (A * C + 1));   /* expert outputs */
+  float* dgo = (float*)malloc(sizeof(float) * (A * C + 1));
+  float* dgi = (float*)malloc(sizeof(float) * (A * C + 1));
+  float* dTP = (float*)malloc(sizeof(float) * (A + 1));
+  float* dD = (float*)malloc(sizeof(float) * (A * H + 1)); /* d(act) */
+  float* dGt = (float*)malloc(sizeof(float) * (A * H + 1));
+  float* dUp = (float*)malloc(sizeof(float) * (A * H + 1));
+  float* dinU = (float*)malloc(sizeof(float) * (A * C + 1));
+  float* dP = (float*)malloc(sizeof(float) * (NE + 1));
+  float* dL = (float*)malloc(sizeof(float) * (NE + 1));
+  float* rdin = (float*)malloc(sizeof(float) * ((size_t)N * C + 1));
+  const float** rows = (const float**)malloc(sizeof(float*) * (A + 1));
+  const int tmpn = (C > H ? C : H) > E ? (C > H ? C : H) : E;
+  float* tmp = (float*)malloc(sizeof(float) * (size_t)tmpn);
+
+  oracle_router_logits(N, C, E, x, Wr, br, L);
+  oracle_softmax(N, E, L, P);
+  oracle_topk(N, E, k, P, I, TP);
+  oracle_dispatch(N, E, k, I, CN, OF, PM);
+
+  /* Forward activations per slot (the caches the reference keeps). */
+  for (size_t slot = 0; slot < A; ++slot) {
+    const int t = PM[slot] / k, e = I[PM[slot]];
+    float* g = G + slot * H;
+    float* u = U + slot * H;
+    float* a = Act + slot * H;
+    linear_row(C, H, x + (size_t)t * C, Wg + (size_t)e * C * H, bg + (size_t)e * H, g);
+    linear_row(C, H, x + (size_t)t * C, Wu + (size_t)e * C * H, bu + (size_t)e * H, u);
+    for (int h = 0; h < H; ++h) {
+      float gs = g[h] / (1.0f + expf(-g[h]));
+      a[h] = gs * u[h];
+    }
+    linear_row(H, C, a, Wd + (size_t)e * H * C, bd + (size_t)e * C, O + slot * C);
+  }
+
+  /* B1 */
+  for (size_t slot = 0; slot < A; ++slot) {
+    const int flat = PM[slot], t = flat / k;
+    const float pr = TP[flat];
+    const float* d = dy + (size_t)t * C;
+    const float* o = O + slot * C;
+    float* dg = dgo + slot * C;
+    float dot = 0.0f;
+    for (int c = 0; c < C; ++c) {
+#ifndef ORACLE_PLANT_UNGATED
+      dg[c] = d[c] * pr;
+#else
+      dg[c] = d[c];
+#endif
+      dot += o[c] * d[c];
+    }
+    dTP[flat] = dot;
+  }
+
+  /* B2 */
+  for (int e = 0; e < E; ++e) {
+    const int cnt = CN[e];
+    if (cnt == 0) continue;
+    const size_t s0 = (size_t)OF[e];
+    for (int r = 0; r < cnt; ++r) rows[r] = Act + (s0 + r) * H;
+    linear_backward(cnt, H, C, rows, dgo + s0 * C, Wd + (size_t)e * H * C,
+                    dWd + (size_t)e * H * C, dbd + (size_t)e * C, dD + s0 * H, tmp);
+    for (size_t i = s0 * H; i < (s0 + cnt) * H; ++i) {
+      const float dd = dD[i], u = U[i], g = G[i];
+      const float sig = 1.0f / (1.0f + expf(-g));
+      dUp[i] = dd * (g * sig);
+#ifndef ORACLE_PLANT_SILU_SIGN
+      dGt[i] = (dd * u) * (sig * (1.0f + g * (1.0f - sig)));
+#else
+      dGt[i] = (dd * u) * (sig * (1.0f - g * (1.0f - sig)));
+#endif
+    }
+    for (int r = 0; r < cnt; ++r) rows[r] = x + (size_t)(PM[s0 + r] / k) * C;
+    linear_backward(cnt, C, H, rows, dGt + s0 * H, Wg + (size_t)e * C * H,
+                    dWg + (size_t)e * C * H, dbg + (size_t)e * H, dgi + s0 * C, tmp);
+    linear_backward(cnt, C, H, rows, dUp + s0 * H, Wu + (size_t)e * C * H,
+                    dWu + (size_t)e * C * H, dbu + (size_t)e * H, dinU + s0 * C, tmp);
+    for (size_t i = s0 * C; i < (s0 + cnt) * C; ++i) dgi[i] = dgi[i] + dinU[i];
+  }
+
+  /* B3 */
+  memset(dx, 0, sizeof(float) * (size_t)N * C);
+  for (size_t slot = 0; slot < A; ++slot) {
+    float* o = dx + (size_t)(PM[slot] / k) * C;
+    const float* g = dgi + slot * C;
+    for (int c = 0; c < C; ++c) o[c] += g[c];
+  }
+
+  /* B4, B5 */
+  memset(dP, 0, sizeof(float) * NE);
+  for (size_t f = 0; f < A; ++f) dP[(f / k) * E + I[f]] = dTP[f];
+  for (int e = 0; e < E; ++e) {
+    const float fe = (float)CN[e] / (float)N;
+    tmp[e] = (0.01f * (float)E * fe) / (float)N;
+  }
+#ifndef ORACLE_PLANT_NO_LOAD_BALANCE
+  for (size_t i = 0; i < NE; ++i) dP[i] = dP[i] + tmp[i % E];
+#endif
+
+  /* B6 */
+  for (int t = 0; t < N; ++t) {
+    const float* p = P + (size_t)t * E;
+    const float* d = dP + (size_t)t * E;
+    float* o = dL + (size_t)t * E;
+    float s = 0.0f;
+    for (int e = 0; e < E; ++e) s += d[e] * p[e];
+    for (int e = 0; e < E; ++e) o[e] = p[e] * (d[e] - s);
+  }
+
+  /* B7, B8 */
+  for (int t = 0; t < N; ++t) rows[t] = x + (size_t)t * C;
+  linear_backward(N, C, E, rows, dL, Wr, dWr, dbr, rdin, tmp);
+  for (size_t i = 0; i < (size_t)N * C; ++i) dx[i] = dx[i] + rdin[i];
+
+  free(L); free(P); free(I); free(TP); free(CN); free(OF); free(PM);
+  free(G); free(U); free(Act); free(O); free(dgo); free(dgi); free(dTP);
+  free(dD); free(dGt); free(dUp); free(dinU); free(dP); free(dL); free(rdin);
+  free(rows); free(tmp);
   return 0;
 }
 

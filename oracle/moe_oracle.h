@@ -1,5 +1,5 @@
 /*
- * moe_oracle.h -- CPU restatement of mgpt's MoE block forward.
+ * moe_oracle.h -- CPU restatement of mgpt's MoE block forward and backward.
  *
  * TEST INFRASTRUCTURE ONLY.  This library is the checker that the parity
  * tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg compare the
@@ -61,6 +61,20 @@ int oracle_moe_tokens(int C, int H, int E, int k, int n_sel, const int32_t* tok,
                       const float* Wg, const float* bg, const float* Wu,
                       const float* bu, const float* Wd, const float* bd,
                       float* y_sel);
+
+/* Backward of the block after a forward on the same inputs (B1-B9).
+ * dx[N,C] is written; the parameter gradients are ACCUMULATED into
+ * dWr[C,E], dbr[E], dWg[E,C,H], dbg[E,H], dWu[E,C,H], dbu[E,H], dWd[E,H,C],
+ * dbd[E,C] like the reference's add_grad, so a caller that wants the
+ * gradient of one call passes zeroed buffers.  Experts no token chose keep
+ * their gradients untouched.  Returns 0, or 1 for a bad shape. */
+int oracle_moe_backward(int N, int C, int H, int E, int k, const float* x,
+                        const float* Wr, const float* br, const float* Wg,
+                        const float* bg, const float* Wu, const float* bu,
+                        const float* Wd, const float* bd, const float* dy,
+                        float* dx, float* dWr, float* dbr, float* dWg,
+                        float* dbg, float* dWu, float* dbu, float* dWd,
+                        float* dbd);
 
 /* x_hat[N,C] = RMSNorm(x) with gamma = 1 (input preparation, a1). */
 void oracle_rmsnorm(int N, int C, float eps, const float* x, float* out);

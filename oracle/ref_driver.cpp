@@ -7,6 +7,7 @@
 // for bench.py's cpu_baseline leg.  Nothing in the product links it.
 //
 //   ref_driver run  <in.bin> <out.bin>
+//   ref_driver backward <in.bin> <dy.bin> <grad.bin>
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
 //
 // in.bin : "MGPTMOE1", int32 N C H E k, then float32 x[N*C] and the 2+6E
@@ -16,6 +17,11 @@
 // out.bin: "MGPTOUT1", int32 N C E k, float32 y[N*C], int32 idx[N*k],
 //          float32 topp[N*k], int32 counts[E], int32 offsets[E],
 //          int32 perm[N*k], float32 logits[N*E], float32 probs[N*E].
+// dy.bin : float32 dy[N*C] (the upstream gradient).
+// grad.bin: "MGPTGRD1", int32 N C H E k, float32 dx[N*C], then the .grad of
+//          every parameter in get_parameters() order (sizes as in in.bin),
+//          after one forward_into and one backward_into
+//          (layers/MoELayer.cpp:130-223) on a fresh layer.
 #include <algorithm>
 #include <chrono>
 #include <cmath>
@@ -26,6 +32,7 @@
 #include <cstring>
 #include <functional>
 #include <iostream>
+#include <memory>
 #include <random>
 #include <stdexcept>
 #include <string>
@@ -45,21 +52,21 @@ bool read_exact(FILE* f, void* dst, size_t bytes) {
   return std::fread(dst, 1, bytes, f) == bytes;
 }
 
-int run(const char* in_path, const char* out_path) {
+// Reads in.bin into x and a fresh layer's parameters; returns 0 on success.
+int load(const char* in_path, int32_t dims[5], Tensor& x, std::unique_ptr<MoELayer>& layer) {
   FILE* f = std::fopen(in_path, "rb");
   if (!f) { std::perror(in_path); return 2; }
   char magic[8];
-  int32_t dims[5];
   if (!read_exact(f, magic, 8) || std::memcmp(magic, "MGPTMOE1", 8) != 0 ||
-      !read_exact(f, dims, sizeof(dims))) {
+      !read_exact(f, dims, sizeof(int32_t) * 5)) {
     std::fprintf(stderr, "bad input header\n");
     return 2;
   }
   const int N = dims[0], C = dims[1], H = dims[2], E = dims[3], k = dims[4];
-  Tensor x({1, N, C}, 0.0f, Device::CPU);
+  x = Tensor({1, N, C}, 0.0f, Device::CPU);
   if (!read_exact(f, x.data.data(), sizeof(float) * (size_t)N * C)) return 3;
-  MoELayer layer(C, H, E, k);
-  std::vector<Tensor*> params = layer.get_parameters();
+  layer.reset(new MoELayer(C, H, E, k));
+  std::vector<Tensor*> params = layer->get_parameters();
   if ((int)params.size() != 2 + 6 * E) {
     std::fprintf(stderr, "unexpected parameter count %zu\n", params.size());
     return 4;
@@ -67,6 +74,16 @@ int run(const char* in_path, const char* out_path) {
   for (Tensor* p : params)
     if (!read_exact(f, p->data.data(), sizeof(float) * p->size())) return 3;
   std::fclose(f);
+  return 0;
+}
+
+int run(const char* in_path, const char* out_path) {
+  int32_t dims[5];
+  Tensor x;
+  std::unique_ptr<MoELayer> owner;
+  if (int rc = load(in_path, dims, x, owner)) return rc;
+  MoELayer& layer = *owner;
+  const int N = dims[0], C = dims[1], E = dims[3], k = dims[4];
 
   Tensor y;
   layer.forward_into(x, y);
@@ -91,6 +108,39 @@ int run(const char* in_path, const char* out_path) {
   std::fwrite(perm.data(), sizeof(int32_t), A, o);
   std::fwrite(layer.cached_router_logits.data.data(), sizeof(float), (size_t)N * E, o);
   std::fwrite(layer.cached_router_probs.data.data(), sizeof(float), (size_t)N * E, o);
+  std::fclose(o);
+  return 0;
+}
+
+int backward(const char* in_path, const char* dy_path, const char* out_path) {
+  int32_t dims[5];
+  Tensor x;
+  std::unique_ptr<MoELayer> owner;
+  if (int rc = load(in_path, dims, x, owner)) return rc;
+  MoELayer& layer = *owner;
+  const int N = dims[0], C = dims[1];
+  Tensor dy({1, N, C}, 0.0f, Device::CPU);
+  FILE* f = std::fopen(dy_path, "rb");
+  if (!f) { std::perror(dy_path); return 2; }
+  if (!read_exact(f, dy.data.data(), sizeof(float) * (size_t)N * C)) return 3;
+  std::fclose(f);
+
+  Tensor y, dx;
+  layer.forward_into(x, y);
+  layer.backward_into(dy, dx);
+
+  FILE* o = std::fopen(out_path, "wb");
+  if (!o) { std::perror(out_path); return 2; }
+  std::fwrite("MGPTGRD1", 1, 8, o);
+  std::fwrite(dims, sizeof(int32_t), 5, o);
+  std::fwrite(dx.data.data(), sizeof(float), (size_t)N * C, o);
+  for (Tensor* p : layer.get_parameters()) {
+    if (p->grad.size() != p->size()) {
+      std::fprintf(stderr, "parameter without a gradient buffer\n");
+      return 4;
+    }
+    std::fwrite(p->grad.data(), sizeof(float), p->size(), o);
+  }
   std::fclose(o);
   return 0;
 }
@@ -135,9 +185,10 @@ int bench(int N, int C, int H, int E, int k, int reps) {
 
 int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
+  if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
   if (argc == 8 && std::string(argv[1]) == "bench")
     return bench(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]),
                  std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]));
-  std::fprintf(stderr, "usage: ref_driver run <in> <out> | bench N C H E k reps\n");
+  std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | bench N C H E k reps\n");
   return 1;
 }

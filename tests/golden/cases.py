@@ -89,6 +89,33 @@ def build_inputs(case: Case) -> wl.MoEInputs:
     return inp
 
 
+# Cases whose backward the reference is run on (tests/golden/backward/):
+# every unit case plus two benchmark shapes whose expert gradients still
+# fit a CPU run of a few seconds.
+BACKWARD_CASES = [c.name for c in UNIT_CASES] + ["cfg1", "cfg2"]
+
+
+def build_dy(case: Case) -> np.ndarray:
+    """Upstream gradient dy [N,C] of a case (standard normal, seeded; bf16
+    values for bf16 cases so the HIP path reads it exactly).  The all-ones
+    case takes dout = 1 like the reference's own backward test
+    (tests/networkTest/moeTests.cpp:22-39)."""
+    if case.tweak == "ones":
+        return np.ones((case.cfg.N, case.cfg.C), np.float32)
+    rng = np.random.default_rng([SEED, 11])
+    dy = rng.standard_normal((case.cfg.N, case.cfg.C)).astype(np.float32)
+    if case.cfg.act == "bf16":
+        dy = wl.bf16_round(dy)
+    return dy
+
+
+def sample_flat(n: int, m: int = 256) -> np.ndarray:
+    """Deterministic sample of flat indices of an n-element gradient."""
+    if n <= m:
+        return np.arange(n, dtype=np.int64)
+    return np.unique(np.linspace(0, n - 1, m).round().astype(np.int64))
+
+
 def sample_rows(N: int, n: int = 32) -> np.ndarray:
     """Deterministic sample of token rows whose outputs fixtures store."""
     if N <= n:

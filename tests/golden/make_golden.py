@@ -11,7 +11,20 @@ tests/golden/<case>.npz with the reference's outputs:
   rows [r], y_rows [r,C]                       outputs of sampled tokens
 
 Inputs are not stored: they are rebuilt from the case definition and seed.
-Usage: python tests/golden/make_golden.py [case ...]   (default: all cases)
+
+With --backward it runs the reference's backward (ref_driver backward: one
+forward_into and one backward_into on a fresh layer) on the cases of
+cases.BACKWARD_CASES with dy = cases.build_dy(case), and stores
+tests/golden/backward/<case>.npz with
+
+  sha256 digests of dx and of the 8 stacked gradients (NaN canonicalised)
+  rows [r], dx_rows [r,C]                        dx of sampled tokens
+  <grad>_at [m], <grad>_val [m]                   sampled flat entries
+  dx and every gradient in full                  cases with full_arrays and
+                                                 at most 1e5 gradient values
+
+Usage: python tests/golden/make_golden.py [--backward] [case ...]
+(default: all cases)
 """
 from __future__ import annotations
 
@@ -81,6 +94,75 @@ def run_reference(inp: wl.MoEInputs):
         return read_output(op)
 
 
+GRAD_NAMES = ("dWr", "dbr", "dWg", "dbg", "dWu", "dbu", "dWd", "dbd")
+
+
+def canonical_digest(a: np.ndarray) -> str:
+    """Digest with every NaN replaced by one quiet NaN (payload bits of NaNs
+    are not part of the contract)."""
+    a = np.array(a, dtype=np.float32, copy=True)
+    a[np.isnan(a)] = np.float32("nan")
+    return wl.digest(a)
+
+
+def run_reference_backward(inp: wl.MoEInputs, dy: np.ndarray) -> dict:
+    cfg = inp.cfg
+    N, Cc, H, E = cfg.N, cfg.C, cfg.H, cfg.E
+    with tempfile.TemporaryDirectory() as d:
+        ip, dp, op = (os.path.join(d, n) for n in ("in.bin", "dy.bin", "grad.bin"))
+        write_input(ip, inp)
+        np.ascontiguousarray(dy, dtype=np.float32).tofile(dp)
+        subprocess.run([REF, "backward", ip, dp, op], check=True)
+        raw = open(op, "rb").read()
+    assert raw[:8] == b"MGPTGRD1", "bad reference gradient file"
+    off = 8 + 5 * 4
+
+    def take(n):
+        nonlocal off
+        a = np.frombuffer(raw, dtype=np.float32, count=n, offset=off).copy()
+        off += 4 * n
+        return a
+
+    out = {"dx": take(N * Cc).reshape(N, Cc), "dWr": take(Cc * E).reshape(Cc, E),
+           "dbr": take(E)}
+    per = {n: [] for n in GRAD_NAMES[2:]}
+    for _ in range(E):  # SwiGLU::get_parameters order: gate W,b; up W,b; down W,b
+        per["dWg"].append(take(Cc * H).reshape(Cc, H))
+        per["dbg"].append(take(H))
+        per["dWu"].append(take(Cc * H).reshape(Cc, H))
+        per["dbu"].append(take(H))
+        per["dWd"].append(take(H * Cc).reshape(H, Cc))
+        per["dbd"].append(take(Cc))
+    assert off == len(raw), "trailing bytes in the reference gradient file"
+    for n, v in per.items():
+        out[n] = np.stack(v)
+    return out
+
+
+def make_backward(case: C.Case) -> None:
+    t0 = time.time()
+    inp = C.build_inputs(case)
+    ref = run_reference_backward(inp, C.build_dy(case))
+    rows = C.sample_rows(case.cfg.N)
+    fx = {"rows": rows, "dx_rows": ref["dx"][rows],
+          "sha_dx": np.array(canonical_digest(ref["dx"]))}
+    total = 0
+    for n in GRAD_NAMES:
+        g = ref[n]
+        total += g.size
+        at = C.sample_flat(g.size)
+        fx["sha_" + n] = np.array(canonical_digest(g))
+        fx[n + "_at"] = at
+        fx[n + "_val"] = g.reshape(-1)[at]
+    if case.full_arrays and total <= 100000:
+        for n in ("dx",) + GRAD_NAMES:
+            fx[n] = ref[n]
+    os.makedirs(os.path.join(HERE, "backward"), exist_ok=True)
+    np.savez_compressed(os.path.join(HERE, "backward", case.name + ".npz"), **fx)
+    print(f"{case.name} backward: {total} gradient values ({time.time() - t0:.1f}s)",
+          flush=True)
+
+
 def make_case(case: C.Case) -> None:
     t0 = time.time()
     inp = C.build_inputs(case)
@@ -105,6 +187,10 @@ def make_case(case: C.Case) -> None:
 def main(argv):
     if not os.path.exists(REF):
         sys.exit("oracle/_ref/ref_driver missing: run `make -C oracle ref` first")
+    if argv and argv[0] == "--backward":
+        for n in argv[1:] or C.BACKWARD_CASES:
+            make_backward(C.ALL_CASES[n])
+        return
     names = argv or list(C.ALL_CASES)
     for n in names:
         make_case(C.ALL_CASES[n])

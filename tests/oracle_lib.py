@@ -39,6 +39,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_moe_tokens.argtypes = [i] * 5 + [vp] * 11
         L.oracle_moe_tokens.restype = i
         L.oracle_rmsnorm.argtypes = [i, i, ctypes.c_float, vp, vp]
+        L.oracle_moe_backward.argtypes = [i] * 5 + [vp] * 19
+        L.oracle_moe_backward.restype = i
         _LIB = L
     return _LIB
 
@@ -126,6 +128,36 @@ def tokens(inp, idx, topp, rows) -> np.ndarray:
                                  _p(idx), _p(topp), *[_p(a) for a in arrs[1:]], _p(y))
     assert rc == 0
     return y
+
+
+GRAD_NAMES = ("dWr", "dbr", "dWg", "dbg", "dWu", "dbu", "dWd", "dbd")
+
+
+def load_variant(path: str) -> ctypes.CDLL:
+    """Binds a separately built copy of the oracle (planted-mistake builds)."""
+    L = ctypes.CDLL(path)
+    L.oracle_moe_backward.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 19
+    L.oracle_moe_backward.restype = ctypes.c_int
+    return L
+
+
+def backward(inp, dy, library=None) -> dict:
+    """Reference-order backward of a workload.MoEInputs for upstream dy:
+    dx [N,C] and the parameter gradients of one call (zero-started), with
+    expert gradients stacked over experts like the weights."""
+    cfg = inp.cfg
+    N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
+    arrs = [_f32(a) for a in (inp.x, inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu,
+                              inp.Wd, inp.bd)]
+    dy = _f32(dy)
+    assert dy.shape == (N, C)
+    out = {"dx": np.empty((N, C), np.float32)}
+    for name, a in zip(GRAD_NAMES, arrs[1:]):
+        out[name] = np.zeros(a.shape, np.float32)
+    rc = (library or lib()).oracle_moe_backward(N, C, H, E, k, *[_p(a) for a in arrs], _p(dy),
+                                   _p(out["dx"]), *[_p(out[n]) for n in GRAD_NAMES])
+    assert rc == 0
+    return out
 
 
 def rmsnorm(x, eps=1e-5):
