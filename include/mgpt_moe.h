@@ -1,5 +1,6 @@
 /*
- * mgpt_moe.h -- C ABI of the MI355X (gfx950) Mixture-of-Experts block forward.
+ * mgpt_moe.h -- C ABI of the MI355X (gfx950) Mixture-of-Experts block
+ * forward and backward.
  *
  * Drop-in device path for mgpt's MoELayer (mrtcemberci/mgpt,
  * src/main/neuralnetwork/layers/MoELayer.{h,cpp}).  The engine's C++ layer
@@ -112,6 +113,55 @@ typedef struct mgpt_moe_routing {
 } mgpt_moe_routing;
 int mgpt_moe_get_routing(const mgpt_moe* h, int num_tokens, void* workspace,
                          mgpt_moe_routing* out);
+
+/* ---------------------------------------------------------------- training
+ * The reference layer is trainable: forward_into caches what backward_into
+ * needs, backward_into returns dL/dx and adds every parameter's gradient to
+ * its Tensor::grad (add_grad, utils/Tensor.cpp:638-650).  Here the training
+ * forward keeps those caches in the workspace, the backward reads them, and
+ * the handle owns fp32 gradient buffers in the parameters' reference
+ * layouts.  Training needs weight_dtype == act_dtype (fp32 or bf16);
+ * fp8 handles return MGPT_ERR_UNSUPPORTED.  bf16 handles compute the
+ * gradient products in bf16 with fp32 accumulation (within 2e-2 of the
+ * fp32 reference). */
+
+/* Workspace for mgpt_moe_forward_train + mgpt_moe_backward on num_tokens
+ * tokens (the forward workspace plus the router probabilities, the gate/up
+ * pre-activations and the backward's scratch).  Replaces the training part
+ * of MoELayer::get_footprint (layers/MoELayer.cpp:238-251). */
+int mgpt_moe_train_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes);
+
+/* mgpt_moe_forward that also keeps, in `workspace` (>= train workspace
+ * bytes), the router probabilities and the gate/up pre-activations next to
+ * the routing, gathered rows, SwiGLU outputs and expert outputs: the caches
+ * of MoELayer::forward_into (layers/MoELayer.cpp:28-128) and
+ * SwiGLU::forward_into (layers/SwiGLU.cpp:23-50). */
+int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* dx[N,C] = dL/dx for the upstream gradient dy[N,C], given the workspace of
+ * the preceding mgpt_moe_forward_train on the same x (which must be passed
+ * again, unchanged) and the same num_tokens; adds dL/dW for all 2 + 6E
+ * parameters to the handle's gradient buffers, including the load-balance
+ * term 0.01 * E * f_e / N on the router probabilities (f_e = count_e / N).
+ * Experts no token chose get no gradient, as in the reference.  x, dy, dx
+ * are act_dtype, device memory; dx must not overlap x or dy.  The workspace
+ * is consumed (a second backward needs a new training forward).  Replaces
+ * MoELayer::backward_into (layers/MoELayer.cpp:130-223) on the device. */
+int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* Sets every gradient to zero on `stream`.  Replaces Tensor::zero_grad
+ * (utils/Tensor.cpp:181-187) over this layer's parameters. */
+int mgpt_moe_zero_grad(mgpt_moe* h, void* stream);
+
+/* Copies the 2 + 6E fp32 gradients to grads[i] in get_parameters() order
+ * and each parameter's reference layout (as in mgpt_moe_load_parameters);
+ * grads_on_device = 1 for device destinations, 0 for host.  Returns once
+ * the copies are complete.  Replaces reading Tensor::grad of the layer's
+ * parameters (utils/Tensor.h:21). */
+int mgpt_moe_get_gradients(mgpt_moe* h, float* const* grads, int num_params,
+                           int grads_on_device, void* stream);
 
 /* Copies the per-expert token counts of the last forward to host memory,
  * waiting for that forward to finish.  Replaces MoELayer::get_expert_counts

@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "lib")
 OBJ = os.path.join(HERE, "_build")
 
 HIP_SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_dma.hip", "gemm_decode.hip", "combine.hip",
-               "pack.hip", "moe_capi.hip"]
+               "pack.hip", "backward.hip", "wgrad.hip", "moe_capi.hip"]
 ARCH = os.environ.get("MGPT_OFFLOAD_ARCH", "gfx950")
 
 # -ffp-contract=off: the router must round every product and sum separately

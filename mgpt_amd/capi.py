@@ -75,6 +75,11 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_stage_times": [vp, vp, i],
         "mgpt_moe_export_fp8": [vp, i, i, vp, vp],
         "mgpt_moe_device_expf": [vp, vp, i, vp],
+        "mgpt_moe_train_workspace_bytes": [vp, i, ctypes.POINTER(sz)],
+        "mgpt_moe_forward_train": [vp, vp, vp, i, vp, sz, vp],
+        "mgpt_moe_backward": [vp, vp, vp, vp, i, vp, sz, vp],
+        "mgpt_moe_zero_grad": [vp, vp],
+        "mgpt_moe_get_gradients": [vp, ctypes.POINTER(vp), i, i, vp],
     }
     for name, args in sig.items():
         f = getattr(L, name)

@@ -35,8 +35,17 @@ __host__ __device__ inline int router_experts_per_wave(int E) {
   return E <= 8 ? 1 : (E <= 32 ? 2 : 4);
 }
 
-// Grouped-GEMM epilogues (gemm.hip).
-enum Epilogue { kEpiGateUp = 0, kEpiDown = 1 };
+// Grouped-GEMM epilogues (gemm.hip, gemm_dma.hip).  kEpiGateUp: SwiGLU of
+// the interleaved gate/up columns (optionally also saving the pre-activations
+// for the backward pass); kEpiDown: + bias (none when the bias pointer is
+// null); kEpiSwigluBwd: the backward of SwiGLU applied to the product
+// d(act) = dY . W_down^T, reading the saved pre-activations and writing
+// d(gate), d(up) in the same interleaved layout.
+enum Epilogue { kEpiGateUp = 0, kEpiDown = 1, kEpiSwigluBwd = 2 };
+
+// Column of hidden unit h (and, +32, of its up partner) in the gate/up
+// interleaved layout [32 gate | 32 up] per 32 hidden units.
+__host__ __device__ __forceinline__ int packed_gate_col(int h) { return (h >> 5) * 64 + (h & 31); }
 
 __device__ __forceinline__ float bf16_to_f32(bf16_t v) {
   return __uint_as_float(((uint32_t)v) << 16);

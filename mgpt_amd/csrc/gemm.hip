@@ -20,8 +20,18 @@
 // Epilogues: GATEUP (B rows interleaved in 64-row groups [32 gate | 32 up]
 // for the same 32 hidden units, so a wave's two adjacent 32x32 tiles hold
 // g and u of the same (row, h) in the same lane) computes
-// h = silu(g*s_g + b_g) * (u*s_u + b_u) and stores bf16/fp32 h;
-// DOWN stores o = acc*s + b_d in the activation dtype.
+// h = silu(g*s_g + b_g) * (u*s_u + b_u) and stores bf16/fp32 h, and, when
+// `aux` is given, also the pre-activations g, u in the interleaved layout
+// (aux[row][packed column], the caches of layers/SwiGLU.cpp:30-31 that the
+// backward pass reads);
+// DOWN stores o = acc*s + b_d in the activation dtype (no bias if bias0 is
+// null);
+// SWIGLU_BWD treats the product as d(act)[row][h] and applies the CPU
+// swiglu_backward of utils/Tensor.cpp:2006-2030 with the saved g, u read
+// from aux: sig = 1/(1+exp(-g)), d_up = d*(g*sig),
+// d_gate = (d*u)*(sig*(1+g*(1-sig))), written to out in the interleaved
+// layout (out may equal aux: each element is read before it is written by
+// the same thread).
 #include "common.hpp"
 
 namespace mgpt {
@@ -52,7 +62,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
     const AT* __restrict__ A, const WT* __restrict__ B, const float* __restrict__ wscale,
     const float* __restrict__ bias0, const float* __restrict__ bias1,
     const int32_t* __restrict__ counts, int E, int K, int Npad, int n_store, int bias_ld,
-    OutT* __restrict__ out, int ldo) {
+    OutT* out, int ldo, OutT* aux, int aux_ld) {
   constexpr int BK = KSlab<AT>::BK;
   constexpr int PAD = 16 / (int)sizeof(AT);
   constexpr int LDK = BK + PAD;
@@ -227,6 +237,35 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
             const float ex = kF32 ? expf(-g) : __expf(-g);
             const float hv = (g / (1.0f + ex)) * u;
             store_act(out + (size_t)row * ldo + hcol, hv);
+            if (aux) {
+              store_act(aux + (size_t)row * aux_ld + prow, g);
+              store_act(aux + (size_t)row * aux_ld + prow + 32, u);
+            }
+          }
+        }
+      }
+    }
+  } else if constexpr (EPI == kEpiSwigluBwd) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int h = n0 + wn * WTN + j * 32 + lrow;
+      if (h >= n_store) continue;
+      const int pc = packed_gate_col(h);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int row = row_base + i * 32 + 8 * (v / 4) + 4 * lhalf + (v % 4);
+          if (row < ti.row_end) {
+            const float d = acc[i][j][v];
+            const float g = to_f32(aux[(size_t)row * aux_ld + pc]);
+            const float u = to_f32(aux[(size_t)row * aux_ld + pc + 32]);
+            const float ex = kF32 ? expf(-g) : __expf(-g);
+            const float sig = 1.0f / (1.0f + ex);
+            const float d_up = d * (g * sig);
+            const float d_gate = (d * u) * (sig * (1.0f + g * (1.0f - sig)));
+            store_act(out + (size_t)row * ldo + pc, d_gate);
+            store_act(out + (size_t)row * ldo + pc + 32, d_up);
           }
         }
       }
@@ -237,7 +276,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
       const int col = n0 + wn * WTN + j * 32 + lrow;
       if (col >= n_store) continue;
       const float s = kFp8 ? wscale[(size_t)e * Npad + col] : 1.0f;
-      const float b = bias0[(size_t)e * bias_ld + col];
+      const float b = bias0 ? bias0[(size_t)e * bias_ld + col] : 0.0f;
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
 #pragma unroll
@@ -258,23 +297,26 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
 
 // Host launcher.  max_mtiles must bound sum_e ceil(count_e / BM) (the
 // caller uses ceil(A / BM) + E); surplus blocks exit after find_tile.
+// aux / aux_ld: the pre-activation save of GATEUP (null: none) or the saved
+// pre-activations SWIGLU_BWD reads (required).
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT* A, const WT* B, const float* wscale, const float* bias0,
                                const float* bias1, const int32_t* counts, int E, int K, int Npad,
                                int n_store, int bias_ld, OutT* out, int ldo, int max_mtiles,
-                               hipStream_t stream) {
+                               OutT* aux, int aux_ld, hipStream_t stream) {
   if (max_mtiles <= 0) return hipSuccess;
+  if (EPI == kEpiSwigluBwd && aux == nullptr) return hipErrorInvalidValue;
   dim3 grid(Npad / BN, max_mtiles);
   hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WM, WN, AT, WT, EPI, OutT>), grid, dim3(256), 0,
                      stream, A, B, wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out,
-                     ldo);
+                     ldo, aux, aux_ld);
   return hipGetLastError();
 }
 
 #define MGPT_INST_GEMM(BM, BN, WM, WN, AT, WT, EPI, OT)                                     \
   template hipError_t launch_grouped_gemm<BM, BN, WM, WN, AT, WT, EPI, OT>(                 \
       const AT*, const WT*, const float*, const float*, const float*, const int32_t*, int, int, \
-      int, int, int, OT*, int, int, hipStream_t);
+      int, int, int, OT*, int, int, OT*, int, hipStream_t);
 
 // Large-M tiles (prefill-shaped segments).
 MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, bf16_t, kEpiGateUp, bf16_t)
@@ -289,5 +331,9 @@ MGPT_INST_GEMM(32, 256, 1, 4, bf16_t, fp8_t, kEpiDown, bf16_t)
 // fp32 path.
 MGPT_INST_GEMM(64, 128, 2, 2, float, float, kEpiGateUp, float)
 MGPT_INST_GEMM(64, 128, 2, 2, float, float, kEpiDown, float)
+// Backward data-gradient products (d(act) with the SwiGLU backward; dX).
+MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t)
+MGPT_INST_GEMM(32, 256, 1, 4, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t)
+MGPT_INST_GEMM(64, 128, 2, 2, float, float, kEpiSwigluBwd, float)
 
 }  // namespace mgpt

@@ -206,7 +206,8 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
                                            const Tile& cur, int wn, int wm, int lrow, int lhalf,
                                            const float* __restrict__ bias0,
                                            const float* __restrict__ bias1, int n_store,
-                                           int bias_ld, bf16_t* __restrict__ out, int ldo) {
+                                           int bias_ld, bf16_t* __restrict__ out, int ldo,
+                                           bf16_t* __restrict__ save, int save_ld) {
   using W = Waves<NW>;
   const int tok_base = cur.row0 + wm * W::WTM + lrow;
   if constexpr (EPI == kEpiGateUp) {
@@ -241,6 +242,21 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
                             silu_mul_fast(ga[v + 3] + bg[v + 3], ua[v + 3] + bu[v + 3]));
         }
         store_group32(out + (size_t)row * ldo + hb, q, lhalf, row < cur.row_end);
+        if (save) {
+          // pre-activations for the backward pass, in the packed column order
+          const int pc = cur.n0 + wn * W::WTN + 64 * gi;
+          uint2 sg[4], su[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int v = 4 * g;
+            sg[g] = pack4_bf16(ga[v] + bg[v], ga[v + 1] + bg[v + 1], ga[v + 2] + bg[v + 2],
+                               ga[v + 3] + bg[v + 3]);
+            su[g] = pack4_bf16(ua[v] + bu[v], ua[v + 1] + bu[v + 1], ua[v + 2] + bu[v + 2],
+                               ua[v + 3] + bu[v + 3]);
+          }
+          store_group32(save + (size_t)row * save_ld + pc, sg, lhalf, row < cur.row_end);
+          store_group32(save + (size_t)row * save_ld + pc + 32, su, lhalf, row < cur.row_end);
+        }
       }
       // one column group at a time: keeps the scheduler from hoisting every
       // accumulator read (TN * TM * 16 values) ahead of the stores
@@ -339,7 +355,8 @@ template <int EPI, int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
-    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, float* __restrict__ partials) {
+    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, float* __restrict__ partials,
+    bf16_t* __restrict__ save, int save_ld) {
   using W = Waves<NW>;
   constexpr int kTN = W::TN, kTM = W::TM;
   constexpr int kUnits = 5;
@@ -534,7 +551,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     mfma_drain<NW>();
     if (cur.sidx < 0) {
       store_tile<EPI, NW>(acc, cur.tile, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out,
-                          ldo);
+                          ldo, save, save_ld);
     } else {
       float4* P = reinterpret_cast<float4*>(partials + (size_t)cur.sidx * kPartialFloats) + tid;
 #pragma unroll
@@ -640,7 +657,9 @@ constexpr int kRingWaves = MGPT_RING_WAVES;
 // max_mtiles bounds sum_e ceil(count_e / 256); it only caps the grid.
 // partials (num_cus * kPartialFloats floats, or null to disable) holds the
 // split last round; the reduce kernel that follows exits at once when the
-// counts leave nothing to split.  Measured on MI355X (cfg3 shapes, skewed
+// counts leave nothing to split.  save (gate/up only, and only without
+// partials) also stores the pre-activations g + b_g, u + b_u as bf16 in the
+// packed column order, save[row][n] with leading dimension save_ld.  Measured on MI355X (cfg3 shapes, skewed
 // counts): the split 5-unit ring (gate/up 1035, down 871 TFLOP/s) beats a
 // 2-slab ring of 64 KB slabs (1034, 827) and 32-column slabs (4 x 32: 938,
 // 724; 5 x 32 with 2 per barrier: 970, 786), whose 64-byte row segments
@@ -651,17 +670,21 @@ template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                            const float* bias1, const int32_t* counts, int E, int K, int Npad,
                            int n_store, int bias_ld, bf16_t* out, int ldo, int max_mtiles,
-                           float* partials, int num_cus, hipStream_t stream) {
+                           float* partials, int num_cus, bf16_t* save, int save_ld,
+                           hipStream_t stream) {
   if (max_mtiles <= 0) return hipSuccess;
   // 16-byte output vectors: ldo and the output base must keep 8-element alignment
   if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0 || num_cus <= 0 || ldo % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(out) & 15) != 0)
     return hipErrorInvalidValue;
+  if (save && (EPI != kEpiGateUp || partials || save_ld % 8 != 0 ||
+               (reinterpret_cast<uintptr_t>(save) & 15) != 0))
+    return hipErrorInvalidValue;
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
   hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves>), dim3(grid), dim3(kRingWaves * kWave), 0,
                      stream, A, B, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
-                     partials);
+                     partials, save, save_ld);
   if (partials)
     hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256), 0,
                        stream,
@@ -672,9 +695,11 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
 
 template hipError_t launch_gemm_dma<kEpiGateUp>(const bf16_t*, const bf16_t*, const float*,
                                                 const float*, const int32_t*, int, int, int, int,
-                                                int, bf16_t*, int, int, float*, int, hipStream_t);
+                                                int, bf16_t*, int, int, float*, int, bf16_t*, int,
+                                                hipStream_t);
 template hipError_t launch_gemm_dma<kEpiDown>(const bf16_t*, const bf16_t*, const float*,
                                               const float*, const int32_t*, int, int, int, int,
-                                              int, bf16_t*, int, int, float*, int, hipStream_t);
+                                              int, bf16_t*, int, int, float*, int, bf16_t*, int,
+                                              hipStream_t);
 
 }  // namespace mgpt

@@ -1,5 +1,5 @@
 // moe_capi.hip -- the C ABI (include/mgpt_moe.h): handle, parameter packing,
-// workspace layout and the forward pipeline.
+// workspace layout, the forward pipeline and the backward pipeline.
 //
 // Forward = 6 stream-ordered launches and no host synchronisation:
 //   router+top-k -> per-expert scan -> permute -> gate/up GEMM (+SwiGLU)
@@ -8,6 +8,15 @@
 // host prefix sum (layers/MoELayer.cpp:61-80) are replaced by device-side
 // scans; the per-expert host loop of GEMM launches (:94-118) by one grouped
 // launch per projection.
+//
+// Backward (layers/MoELayer.cpp:130-223) = 8 launches, again without host
+// synchronisation: scatter backward -> d(act) product with the SwiGLU
+// backward in its epilogue -> dX product -> down and gate/up weight
+// gradients (with their bias sums) -> per-token gather + softmax + router
+// backward -> router weight gradient (partials + in-order reduction).  It
+// reads what the training forward kept in the workspace: the routing, the
+// gathered rows, h, the expert outputs, the router probabilities and the
+// gate/up pre-activations.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -26,7 +35,7 @@ namespace mgpt {
 // kernels (router.hip, dispatch.hip, gemm.hip, combine.hip, pack.hip)
 template <typename ActT>
 hipError_t launch_router(const ActT*, const float*, const float*, const float*, int, int, int,
-                         int, int32_t*, float*, int32_t*, float*, hipStream_t);
+                         int, int32_t*, float*, int32_t*, float*, float*, hipStream_t);
 hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
 template <typename ActT>
 hipError_t launch_permute(const ActT*, const int32_t*, const int32_t*, int32_t*, int, int, int,
@@ -36,8 +45,8 @@ hipError_t launch_combine(const ActT*, const int32_t*, const float*, const int32
                           ActT*, hipStream_t);
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT*, const WT*, const float*, const float*, const float*,
-                               const int32_t*, int, int, int, int, int, OutT*, int, int,
-                               hipStream_t);
+                               const int32_t*, int, int, int, int, int, OutT*, int, int, OutT*,
+                               int, hipStream_t);
 template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
@@ -46,7 +55,25 @@ hipError_t launch_pack_router(const float*, int, int, int, float*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
                            const int32_t*, int, int, int, int, int, bf16_t*, int, int, float*, int,
-                           hipStream_t);
+                           bf16_t*, int, hipStream_t);
+// backward (backward.hip, wgrad.hip)
+template <typename ActT>
+hipError_t launch_scatter_bwd(const ActT*, const ActT*, const int32_t*, const float*, int, int,
+                              int, ActT*, float*, hipStream_t);
+template <typename ActT>
+hipError_t launch_token_bwd(const ActT*, const int32_t*, const int32_t*, const float*,
+                            const float*, const int32_t*, const float*, int, int, int, int, int,
+                            ActT*, float*, hipStream_t);
+int router_wgrad_chunks(int N);
+template <typename ActT>
+hipError_t launch_router_wgrad(const ActT*, const float*, int, int, int, float*, float*, float*,
+                               float*, hipStream_t);
+template <typename T>
+hipError_t launch_transpose_pad(const T*, int, int, size_t, T*, int, int, size_t, int,
+                                hipStream_t);
+template <typename T, int MODE>
+hipError_t launch_wgrad(const T*, int, int, const T*, int, int, const int32_t*, int, float*,
+                        float*, int, size_t, int, int, float*, float*, size_t, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
                               const float*, const int32_t*, int, int, int, int, int, bf16_t*, int,
@@ -85,8 +112,13 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 struct Layout {
-  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, partials,
-      total;
+  size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, partials;
+  // training only (after the forward regions, so those keep their offsets):
+  // router probabilities [N][E] f32, gate/up pre-activations (then their
+  // gradients) [A+pad][2Hp], dgo [A+pad][C], d(top-k p) [A] f32,
+  // d(logits) [N][E] f32, router weight-gradient partials
+  size_t probs, gu, dgo, dtp, dlog, rw_part, rw_part_b;
+  size_t total;
 };
 
 }  // namespace
@@ -108,6 +140,18 @@ struct mgpt_moe {
   float* bu = nullptr;     // [E][Hp]
   float* bd = nullptr;     // [E][Cp]
   bool loaded = false;
+  // Backward: the weights in the layouts the data-gradient products read,
+  // derived from the forward packs on the first backward after a load
+  // (wdb [E][Hq][C]: W_down rows h; wgub [E][Cp][2Hp]: W_gate/W_up rows c,
+  // columns in the packed gate/up order), and the fp32 gradients.
+  int Hq = 0;
+  void* wdb = nullptr;
+  void* wgub = nullptr;
+  bool bwd_ready = false;
+  float* grad = nullptr;   // gWr [C][E], gbr [E], gWg [E][C][H], gbg [E][H],
+                           // gWu [E][C][H], gbu [E][H], gWd [E][H][C], gbd [E][C]
+  size_t g_off[8] = {};
+  size_t g_total = 0;
   // Profiling ring: forward i records its stage boundaries into slot
   // i % kProfSlots; stage_times averages over the recorded slots.
   static constexpr int kProfSlots = 64;
@@ -129,7 +173,7 @@ struct mgpt_moe {
   }
   size_t w_bytes() const { return wdt == MGPT_DTYPE_FP8_E4M3 ? 1 : (wdt == MGPT_DTYPE_BF16 ? 2 : 4); }
   // h (SwiGLU output) is kept in the activation dtype.
-  Layout layout(int N) const {
+  Layout layout(int N, bool train = false) const {
     Layout L{};
     const size_t A = (size_t)N * k;
     const size_t TB = router_tokens_per_block(E);
@@ -153,6 +197,16 @@ struct mgpt_moe {
     L.obuf = take((A + kRowPad) * C * act_bytes());
     // fp32 partial tiles of the large-M GEMMs' split last round (one per CU)
     L.partials = take(uses_gemm_dma(N) ? (size_t)num_cus * kGemmPartialBytes : 0);
+    if (train) {
+      L.probs = take((size_t)N * E * 4);
+      L.gu = take((A + kRowPad) * 2 * Hp * act_bytes());
+      L.dgo = take((A + kRowPad) * C * act_bytes());
+      L.dtp = take(A * 4);
+      L.dlog = take((size_t)N * E * 4);
+      const size_t chunks = (size_t)(N + 255) / 256;
+      L.rw_part = take(chunks * C * E * 4);
+      L.rw_part_b = take(chunks * E * 4);
+    }
     L.total = off;
     return L;
   }
@@ -184,12 +238,58 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_g, h->wr1, h->br, h->wgu, h->wd, h->sgu, h->sd, h->bg, h->bu, h->bd};
+  void* ptrs[] = {h->wr_g, h->wr1, h->br, h->wgu, h->wd, h->sgu, h->sd,
+                  h->bg,   h->bu,  h->bd, h->wdb, h->wgub};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   h->wr_g = h->wr1 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
-  h->wgu = h->wd = nullptr;
+  h->wgu = h->wd = h->wdb = h->wgub = nullptr;
   h->loaded = false;
+  h->bwd_ready = false;
+}
+
+// Training is built for bf16 x bf16 and fp32 x fp32 handles (fp8 weights
+// are an inference format here).
+bool trainable(const mgpt_moe* h) { return h->wdt == h->act; }
+
+// Allocates and zeroes the gradient buffer on first use (stream-ordered).
+int ensure_grad(mgpt_moe* h, hipStream_t st) {
+  if (h->grad) return MGPT_OK;
+  const size_t C = h->C, H = h->H, E = h->E;
+  const size_t sizes[8] = {C * E, E, E * C * H, E * H, E * C * H, E * H, E * H * C, E * C};
+  size_t off = 0;
+  for (int i = 0; i < 8; ++i) {
+    h->g_off[i] = off;
+    off += sizes[i];
+  }
+  h->g_total = off;
+  HIP_TRY(hipMalloc(&h->grad, sizeof(float) * off));
+  HIP_TRY(hipMemsetAsync(h->grad, 0, sizeof(float) * off, st));
+  return MGPT_OK;
+}
+
+// The backward weight layouts, transposed from the forward packs.
+int ensure_bwd_weights(mgpt_moe* h, hipStream_t st) {
+  if (h->bwd_ready) return MGPT_OK;
+  const int C = h->C, E = h->E, Hp = h->Hp, Cp = h->Cp;
+  h->Hq = round_up(Hp, 256);
+  const size_t eb = h->act_bytes();
+  if (!h->wdb) HIP_TRY(hipMalloc(&h->wdb, eb * E * h->Hq * C));
+  if (!h->wgub) HIP_TRY(hipMalloc(&h->wgub, eb * E * Cp * 2 * Hp));
+  if (h->act == MGPT_DTYPE_BF16) {
+    HIP_TRY(launch_transpose_pad<bf16_t>((const bf16_t*)h->wd, Cp, Hp, (size_t)Cp * Hp,
+                                         (bf16_t*)h->wdb, h->Hq, C, (size_t)h->Hq * C, E, st));
+    HIP_TRY(launch_transpose_pad<bf16_t>((const bf16_t*)h->wgu, 2 * Hp, C, (size_t)2 * Hp * C,
+                                         (bf16_t*)h->wgub, Cp, 2 * Hp, (size_t)Cp * 2 * Hp, E,
+                                         st));
+  } else {
+    HIP_TRY(launch_transpose_pad<float>((const float*)h->wd, Cp, Hp, (size_t)Cp * Hp,
+                                        (float*)h->wdb, h->Hq, C, (size_t)h->Hq * C, E, st));
+    HIP_TRY(launch_transpose_pad<float>((const float*)h->wgu, 2 * Hp, C, (size_t)2 * Hp * C,
+                                        (float*)h->wgub, Cp, 2 * Hp, (size_t)Cp * 2 * Hp, E, st));
+  }
+  h->bwd_ready = true;
+  return MGPT_OK;
 }
 
 // Tile choice for the bf16 grouped GEMMs: decode-shaped (few rows per
@@ -240,6 +340,7 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
 int mgpt_moe_destroy(mgpt_moe* h) {
   if (!h) return MGPT_OK;
   free_weights(h);
+  if (h->grad) (void)hipFree(h->grad);
   for (auto& slot : h->ev)
     for (auto& ev : slot)
       if (ev) (void)hipEventDestroy(ev);
@@ -383,10 +484,10 @@ int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes) {
 namespace {
 
 template <typename ActT>
-int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream_t st) {
-  const Layout L = h->layout(N);
+int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool train,
+                 hipStream_t st) {
+  const Layout L = h->layout(N, train);
   const int C = h->C, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
-  const int nb = (N + router_tokens_per_block(E) - 1) / router_tokens_per_block(E);
   const size_t A = (size_t)N * k;
   int32_t* idx = (int32_t*)(ws + L.topk_idx);
   float* topp = (float*)(ws + L.topk_p);
@@ -404,7 +505,11 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
 
   HIP_TRY(mark(0));
   float* logits = h->router_split(N) ? (float*)(ws + L.logits) : nullptr;
-  HIP_TRY(launch_router<ActT>(x, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits, st));
+  // training: keep the router probabilities and the gate/up pre-activations
+  float* probs = train ? (float*)(ws + L.probs) : nullptr;
+  ActT* gu = train ? (ActT*)(ws + L.gu) : nullptr;
+  HIP_TRY(launch_router<ActT>(x, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits,
+                              probs, st));
   HIP_TRY(mark(1));
   HIP_TRY(launch_permute<ActT>(x, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg, st));
   HIP_TRY(mark(2));
@@ -412,11 +517,11 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
     const int mt = (int)((A + 63) / 64) + E;
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiGateUp, float>(
         xg, (const float*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp,
-        mt, st)));
+        mt, gu, 2 * Hp, st)));
     HIP_TRY(mark(3));
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiDown, float>(
         hb, (const float*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
-        st)));
+        nullptr, 0, st)));
   } else {
     const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
     if (small_m(h, N)) {
@@ -431,19 +536,19 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
       } else if (fp8) {
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
             xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
-            Hp, mt, st)));
+            Hp, mt, nullptr, 0, st)));
         HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiDown, bf16_t>(
             hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
-            st)));
+            nullptr, 0, st)));
       } else {
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiGateUp, bf16_t>(
             xg, (const bf16_t*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp,
-            hb, Hp, mt, st)));
+            hb, Hp, mt, gu, 2 * Hp, st)));
         HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiDown, bf16_t>(
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
-            mt, st)));
+            mt, nullptr, 0, st)));
       }
     } else if (h->gemm_tile == 256 && !fp8) {
       // bf16 weights, prefill-shaped segments: 256x256 direct-to-LDS kernel.
@@ -453,28 +558,28 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
       // partial last round costs little; only the down GEMM splits it.
       HIP_TRY(launch_gemm_dma<kEpiGateUp>(xg, (const bf16_t*)h->wgu, h->bg, h->bu, counts, E, C,
                                           2 * Hp, 2 * Hp, Hp, hb, Hp, mt, nullptr, h->num_cus,
-                                          st));
+                                          (bf16_t*)gu, 2 * Hp, st));
       HIP_TRY(mark(3));
       HIP_TRY(launch_gemm_dma<kEpiDown>(hb, (const bf16_t*)h->wd, h->bd, nullptr, counts, E, Hp,
-                                        Cp, C, Cp, ob, C, mt, part, h->num_cus, st));
+                                        Cp, C, Cp, ob, C, mt, part, h->num_cus, nullptr, 0, st));
     } else {
       const int mt = (int)((A + 127) / 128) + E;
       if (fp8) {
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, fp8_t, kEpiGateUp, bf16_t>(
             xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb,
-            Hp, mt, st)));
+            Hp, mt, nullptr, 0, st)));
         HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, fp8_t, kEpiDown, bf16_t>(
             hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
-            st)));
+            nullptr, 0, st)));
       } else {
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiGateUp, bf16_t>(
             xg, (const bf16_t*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp,
-            hb, Hp, mt, st)));
+            hb, Hp, mt, gu, 2 * Hp, st)));
         HIP_TRY(mark(3));
         HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiDown, bf16_t>(
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
-            mt, st)));
+            mt, nullptr, 0, st)));
       }
     }
   }
@@ -488,12 +593,75 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, hipStream
   return MGPT_OK;
 }
 
-}  // namespace
+template <typename ActT>
+int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, char* ws,
+                  hipStream_t st) {
+  const Layout L = h->layout(N, true);
+  const int C = h->C, H = h->H, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
+  const int A = N * k;
+  if (int rc = ensure_grad(h, st)) return rc;
+  if (int rc = ensure_bwd_weights(h, st)) return rc;
+  const int32_t* idx = (const int32_t*)(ws + L.topk_idx);
+  const float* topp = (const float*)(ws + L.topk_p);
+  const int32_t* slot_of = (const int32_t*)(ws + L.slot_of);
+  const int32_t* perm = (const int32_t*)(ws + L.perm);
+  const int32_t* counts = (const int32_t*)(ws + L.counts);
+  const ActT* xg = (const ActT*)(ws + L.xg);
+  const ActT* hb = (const ActT*)(ws + L.hbuf);
+  ActT* ob = (ActT*)(ws + L.obuf);   // expert outputs, then dX of the experts
+  const float* probs = (const float*)(ws + L.probs);
+  ActT* gu = (ActT*)(ws + L.gu);     // pre-activations, then d(gate) / d(up)
+  ActT* dgo = (ActT*)(ws + L.dgo);
+  float* dtp = (float*)(ws + L.dtp);
+  float* dlog = (float*)(ws + L.dlog);
+  float* g = h->grad;
+  const ActT* wdb = (const ActT*)h->wdb;
+  const ActT* wgub = (const ActT*)h->wgub;
 
-extern "C" {
+  HIP_TRY(launch_scatter_bwd<ActT>(dy, ob, perm, topp, A, C, k, dgo, dtp, st));
+  if constexpr (sizeof(ActT) == 4) {
+    const int mt = (A + 63) / 64 + E;
+    HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiSwigluBwd, float>(
+        dgo, wdb, nullptr, nullptr, nullptr, counts, E, C, h->Hq, Hp, 0, gu, 2 * Hp, mt, gu,
+        2 * Hp, st)));
+    HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiDown, float>(
+        gu, wgub, nullptr, nullptr, nullptr, counts, E, 2 * Hp, Cp, C, 0, ob, C, mt, nullptr, 0,
+        st)));
+  } else if (small_m(h, N)) {
+    const int mt = (A + 31) / 32 + E;
+    HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t>(
+        dgo, wdb, nullptr, nullptr, nullptr, counts, E, C, h->Hq, Hp, 0, gu, 2 * Hp, mt, gu,
+        2 * Hp, st)));
+    HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiDown, bf16_t>(
+        gu, wgub, nullptr, nullptr, nullptr, counts, E, 2 * Hp, Cp, C, 0, ob, C, mt, nullptr, 0,
+        st)));
+  } else {
+    const int mt = (A + 127) / 128 + E;
+    HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t>(
+        dgo, wdb, nullptr, nullptr, nullptr, counts, E, C, h->Hq, Hp, 0, gu, 2 * Hp, mt, gu,
+        2 * Hp, st)));
+    HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiDown, bf16_t>(
+        gu, wgub, nullptr, nullptr, nullptr, counts, E, 2 * Hp, Cp, C, 0, ob, C, mt, nullptr, 0,
+        st)));
+  }
+  // dW_down [H][C] and db_down from (h, dgo); dW_gate/up [C][H] and their
+  // biases from (gathered x, d(gate)/d(up))
+  HIP_TRY((launch_wgrad<ActT, 0>(hb, Hp, Hp, dgo, C, C, counts, E, g + h->g_off[6], nullptr, C,
+                                 (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, st)));
+  HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
+                                 g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
+                                 g + h->g_off[5], (size_t)H, st)));
+  HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wr_g,
+                                 router_experts_per_wave(E), N, C, E, k, dx, dlog, st));
+  HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
+                                    (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
+                                    st));
+  return MGPT_OK;
+}
 
-int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* workspace,
-                     size_t workspace_bytes, void* stream) {
+// Shared argument checks of the forward entry points.
+int check_forward_args(const mgpt_moe* h, const void* x, const void* y, int num_tokens,
+                       const void* workspace, size_t workspace_bytes, bool train) {
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
   if (num_tokens < 0) return fail(MGPT_ERR_INVALID_ARGUMENT, "negative num_tokens");
@@ -503,18 +671,133 @@ int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* 
     return fail(MGPT_ERR_INVALID_ARGUMENT, "x and y must be 16-byte aligned");
   if ((uintptr_t)workspace % kAlign != 0)
     return fail(MGPT_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
-  const size_t need = h->layout(num_tokens).total;
+  const size_t need = h->layout(num_tokens, train).total;
   if (workspace_bytes < need)
     return fail(MGPT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu bytes < required %zu",
                 workspace_bytes, need);
   const size_t xbytes = (size_t)num_tokens * h->C * h->act_bytes();
   if ((const char*)x < (const char*)y + xbytes && (const char*)y < (const char*)x + xbytes)
     return fail(MGPT_ERR_INVALID_ARGUMENT, "y must not overlap x");
+  return MGPT_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* workspace,
+                     size_t workspace_bytes, void* stream) {
+  if (int rc = check_forward_args(h, x, y, num_tokens, workspace, workspace_bytes, false))
+    return rc;
+  if (num_tokens == 0) return MGPT_OK;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
   if (h->act == MGPT_DTYPE_BF16)
-    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, num_tokens, (char*)workspace, st);
-  return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, st);
+    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, num_tokens, (char*)workspace,
+                                false, st);
+  return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, false,
+                             st);
+}
+
+int mgpt_moe_train_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes) {
+  if (!h || !bytes || num_tokens < 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle/bytes or negative num_tokens");
+  *bytes = h->layout(num_tokens, true).total;
+  return MGPT_OK;
+}
+
+int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  if (int rc = check_forward_args(h, x, y, num_tokens, workspace, workspace_bytes, true))
+    return rc;
+  if (!trainable(h))
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  if (num_tokens == 0) return MGPT_OK;
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  if (h->act == MGPT_DTYPE_BF16)
+    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, num_tokens, (char*)workspace,
+                                true, st);
+  return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, true,
+                             st);
+}
+
+int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
+  if (!trainable(h))
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  if (num_tokens < 0) return fail(MGPT_ERR_INVALID_ARGUMENT, "negative num_tokens");
+  if (num_tokens == 0) return MGPT_OK;
+  if (!x || !dy || !dx || !workspace)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "null x, dy, dx or workspace");
+  if (((uintptr_t)x | (uintptr_t)dy | (uintptr_t)dx) % 16 != 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "x, dy and dx must be 16-byte aligned");
+  if ((uintptr_t)workspace % kAlign != 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "workspace must be %zu-byte aligned", kAlign);
+  const size_t need = h->layout(num_tokens, true).total;
+  if (workspace_bytes < need)
+    return fail(MGPT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu bytes < required %zu",
+                workspace_bytes, need);
+  const size_t nbytes = (size_t)num_tokens * h->C * h->act_bytes();
+  auto overlap = [&](const void* a, const void* b) {
+    return (const char*)a < (const char*)b + nbytes && (const char*)b < (const char*)a + nbytes;
+  };
+  if (overlap(dx, dy) || overlap(dx, x))
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "dx must not overlap x or dy");
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  if (h->act == MGPT_DTYPE_BF16)
+    return backward_impl<bf16_t>(h, (const bf16_t*)x, (const bf16_t*)dy, (bf16_t*)dx,
+                                 num_tokens, (char*)workspace, st);
+  return backward_impl<float>(h, (const float*)x, (const float*)dy, (float*)dx, num_tokens,
+                              (char*)workspace, st);
+}
+
+int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
+  if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  if (!trainable(h))
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  const bool fresh = h->grad == nullptr;
+  if (int rc = ensure_grad(h, st)) return rc;
+  if (!fresh) HIP_TRY(hipMemsetAsync(h->grad, 0, sizeof(float) * h->g_total, st));
+  return MGPT_OK;
+}
+
+int mgpt_moe_get_gradients(mgpt_moe* h, float* const* grads, int num_params, int grads_on_device,
+                           void* stream) {
+  if (!h || !grads) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle or grads");
+  if (num_params != 2 + 6 * h->E)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "expected %d gradients (2 + 6*E), got %d",
+                2 + 6 * h->E, num_params);
+  for (int i = 0; i < num_params; ++i)
+    if (!grads[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "gradient %d is null", i);
+  if (!trainable(h))
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  if (int rc = ensure_grad(h, st)) return rc;
+  const size_t C = h->C, H = h->H, E = h->E;
+  const hipMemcpyKind kind = grads_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
+  auto copy = [&](int i, size_t off, size_t n) -> hipError_t {
+    return hipMemcpyAsync(grads[i], h->grad + off, sizeof(float) * n, kind, st);
+  };
+  HIP_TRY(copy(0, h->g_off[0], C * E));
+  HIP_TRY(copy(1, h->g_off[1], E));
+  for (size_t e = 0; e < E; ++e) {
+    const int p = 2 + 6 * (int)e;
+    HIP_TRY(copy(p + 0, h->g_off[2] + e * C * H, C * H));
+    HIP_TRY(copy(p + 1, h->g_off[3] + e * H, H));
+    HIP_TRY(copy(p + 2, h->g_off[4] + e * C * H, C * H));
+    HIP_TRY(copy(p + 3, h->g_off[5] + e * H, H));
+    HIP_TRY(copy(p + 4, h->g_off[6] + e * H * C, H * C));
+    HIP_TRY(copy(p + 5, h->g_off[7] + e * C, C));
+  }
+  HIP_TRY(hipStreamSynchronize(st));
+  return MGPT_OK;
 }
 
 int mgpt_moe_get_routing(const mgpt_moe* h, int num_tokens, void* workspace,

@@ -285,7 +285,8 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
                                                    int* s_hist, int tok0, int N, int E, int k,
                                                    int32_t* __restrict__ topk_idx,
                                                    float* __restrict__ topk_p,
-                                                   int32_t* __restrict__ hist, int num_blocks) {
+                                                   int32_t* __restrict__ hist, int num_blocks,
+                                                   float* __restrict__ probs) {
   const int tid = threadIdx.x;
   // L lanes per token: the largest power of two <= min(16, blockDim / 64),
   // so that the kRT tokens use (most of) the block
@@ -327,6 +328,9 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
     for (int v = 0; v < E; ++v) sum = sum + ex[v];
     const float inv = 1.0f / fmaxf(sum, 1e-15f);
     const bool write = tok0 + r < N;
+    if (probs && write)   // the clamped probabilities, kept for the backward pass
+      for (int v = q; v < E; v += L)
+        probs[(size_t)(tok0 + r) * E + v] = fminf(fmaxf(ex[v] * inv, 1e-7f), 1.0f);
     int32_t* io = topk_idx + (size_t)(tok0 + r) * k;
     float* po = topk_p + (size_t)(tok0 + r) * k;
     switch (k) {
@@ -351,7 +355,7 @@ template <typename ActT, int RE>
 __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
     int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
-    int32_t* __restrict__ hist, int num_blocks) {
+    int32_t* __restrict__ hist, int num_blocks, float* __restrict__ probs) {
   __shared__ float s_l[kRT][kMaxExperts + 1];
   __shared__ float s_m[kRT];
   __shared__ int s_hist[kMaxExperts];
@@ -370,7 +374,7 @@ __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
     if (e < E) s_l[lane][e] = acc[j] + br[e];
   }
   __syncthreads();
-  softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks);
+  softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks, probs);
 }
 
 // Few tokens, many experts (decode shapes): the fused kernel would run a
@@ -401,7 +405,8 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
                                                              int32_t* __restrict__ topk_idx,
                                                              float* __restrict__ topk_p,
                                                              int32_t* __restrict__ hist,
-                                                             int num_blocks) {
+                                                             int num_blocks,
+                                                             float* __restrict__ probs) {
   __shared__ float s_l[kRT][kMaxExperts + 1];
   __shared__ float s_m[kRT];
   __shared__ int s_hist[kMaxExperts];
@@ -413,17 +418,18 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
     s_l[r][e] = tok0 + r < N ? logits[(size_t)(tok0 + r) * E + e] : 0.0f;
   }
   __syncthreads();
-  softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks);
+  softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks, probs);
 }
 
 }  // namespace
 
 // logits == nullptr: the fused kernel.  Otherwise (E > 16, few tokens) the
-// split path through logits [N][E] (wr1 = W_r as [E][C]).
+// split path through logits [N][E] (wr1 = W_r as [E][C]).  probs (nullable)
+// receives the clamped softmax [N][E] (the reference's cached_router_probs).
 template <typename ActT>
 hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, const float* br,
                          int N, int C, int E, int k, int32_t* topk_idx, float* topk_p,
-                         int32_t* hist, float* logits, hipStream_t stream) {
+                         int32_t* hist, float* logits, float* probs, hipStream_t stream) {
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
   if (logits) {
@@ -431,7 +437,7 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
                        dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
                        dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits);
     hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(1024), 0, stream, logits, N, E, k,
-                       topk_idx, topk_p, hist, nb);
+                       topk_idx, topk_p, hist, nb, probs);
     return hipGetLastError();
   }
   const int RE = router_experts_per_wave(E);
@@ -440,25 +446,25 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
   switch (RE) {
     case 1:
       hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 1>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb);
+                         C, E, k, topk_idx, topk_p, hist, nb, probs);
       break;
     case 2:
       hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 2>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb);
+                         C, E, k, topk_idx, topk_p, hist, nb, probs);
       break;
     default:
       hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 4>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb);
+                         C, E, k, topk_idx, topk_p, hist, nb, probs);
   }
   return hipGetLastError();
 }
 
 template hipError_t launch_router<float>(const float*, const float*, const float*, const float*,
                                          int, int, int, int, int32_t*, float*, int32_t*, float*,
-                                         hipStream_t);
+                                         float*, hipStream_t);
 template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*,
                                           const float*, int, int, int, int, int32_t*, float*,
-                                          int32_t*, float*, hipStream_t);
+                                          int32_t*, float*, float*, hipStream_t);
 
 // Device expf over a buffer (tests compare it with the host's glibc expf).
 __global__ void expf_probe_kernel(const float* __restrict__ in, float* __restrict__ out, int n) {

@@ -2,9 +2,11 @@
 
 Mirrors /root/reference/src/main/neuralnetwork/layers/MoELayer.h:9-51 --
 constructor (embed_dim, hidden_dim (-1 -> 4C), num_experts, top_k),
-forward / forward_into on [B, T, C] activations, get_parameters() order for
-loading, get_expert_counts(), get_footprint() -- for Python callers, tests
-and the benchmark.  Activations are torch tensors on the GPU (torch supplies
+forward / forward_into on [B, T, C] activations, backward / backward_into
+(with the parameter gradients accumulated like Tensor::add_grad and read
+back in get_parameters() order), get_parameters() order for loading,
+get_expert_counts(), get_footprint() -- for Python callers, tests and the
+benchmark.  Activations are torch tensors on the GPU (torch supplies
 device memory and the stream, nothing else); all compute runs in
 libmgpt_moe.so.  There is no CPU path: a CPU tensor is rejected.
 """
@@ -40,6 +42,7 @@ class MoELayer:
         self._ws = None
         self._last_n = None
         self._loaded = False
+        self._train_x = None   # input of the last training forward (cached_input)
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -85,13 +88,21 @@ class MoELayer:
         replacement for MoELayer::get_footprint, layers/MoELayer.cpp:238-251)."""
         return self.workspace_bytes(B * T)
 
-    def _workspace(self, n: int, device) -> torch.Tensor:
-        need = self.workspace_bytes(n)
+    def train_workspace_bytes(self, num_tokens: int) -> int:
+        n = ctypes.c_size_t()
+        capi.check(capi.lib().mgpt_moe_train_workspace_bytes(self._h, num_tokens,
+                                                             ctypes.byref(n)))
+        return n.value
+
+    def _workspace(self, n: int, device, train: bool = False) -> torch.Tensor:
+        need = self.train_workspace_bytes(n) if train else self.workspace_bytes(n)
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
             self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=device)
         return self._ws
 
-    def forward_into(self, x: torch.Tensor, out: torch.Tensor) -> None:
+    def forward_into(self, x: torch.Tensor, out: torch.Tensor, train: bool = False) -> None:
+        """out = MoE(x).  train=True also keeps what backward() needs (the
+        reference's forward always does: layers/MoELayer.cpp:28-128)."""
         if not x.is_cuda or not out.is_cuda:
             raise ValueError("MoELayer runs on the GPU only: x and out must be device tensors")
         if x.dtype != self.dtype or out.dtype != self.dtype:
@@ -101,15 +112,59 @@ class MoELayer:
         if not x.is_contiguous() or not out.is_contiguous():
             raise ValueError("x and out must be contiguous")
         n = x.numel() // self.C
-        ws = self._workspace(n, x.device)
+        ws = self._workspace(n, x.device, train)
         stream = torch.cuda.current_stream(x.device).cuda_stream
-        capi.check(capi.lib().mgpt_moe_forward(self._h, x.data_ptr(), out.data_ptr(), n,
-                                               ws.data_ptr(), ws.numel(), stream))
+        fn = capi.lib().mgpt_moe_forward_train if train else capi.lib().mgpt_moe_forward
+        capi.check(fn(self._h, x.data_ptr(), out.data_ptr(), n, ws.data_ptr(), ws.numel(), stream))
         self._last_n = n
+        self._train_x = x if train else None
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, train: bool = False) -> torch.Tensor:
         out = torch.empty_like(x)
-        self.forward_into(x, out)
+        self.forward_into(x, out, train)
+        return out
+
+    # -------------------------------------------------------------- backward
+    def backward_into(self, dout: torch.Tensor, din: torch.Tensor) -> None:
+        """din = dL/dx for upstream gradient dout after forward(x, train=True);
+        adds the parameter gradients to the layer's gradient buffers
+        (MoELayer::backward_into, layers/MoELayer.cpp:130-223)."""
+        x = self._train_x
+        if x is None:
+            raise RuntimeError("backward needs a preceding forward(x, train=True)")
+        if dout.shape != x.shape or din.shape != x.shape:
+            raise ValueError("dout and din must have the input's shape")
+        if dout.dtype != self.dtype or din.dtype != self.dtype:
+            raise TypeError(f"expected {self.dtype} gradients")
+        if not (dout.is_cuda and din.is_cuda and dout.is_contiguous() and din.is_contiguous()):
+            raise ValueError("dout and din must be contiguous device tensors")
+        n = x.numel() // self.C
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        capi.check(capi.lib().mgpt_moe_backward(self._h, x.data_ptr(), dout.data_ptr(),
+                                                din.data_ptr(), n, self._ws.data_ptr(),
+                                                self._ws.numel(), stream))
+
+    def backward(self, dout: torch.Tensor) -> torch.Tensor:
+        din = torch.empty_like(dout)
+        self.backward_into(dout, din)
+        return din
+
+    def zero_grad(self) -> None:
+        stream = torch.cuda.current_stream().cuda_stream
+        capi.check(capi.lib().mgpt_moe_zero_grad(self._h, stream))
+
+    def get_gradients(self) -> list:
+        """The 2+6E fp32 gradients (device tensors) in get_parameters() order
+        and reference layout: W_r [C,E], b_r [1,E], then per expert
+        W_gate [C,H], b_gate [1,H], W_up [C,H], b_up [1,H], W_down [H,C],
+        b_down [1,C]."""
+        C, H, E = self.C, self.H, self.E
+        shapes = [(C, E), (1, E)] + [(C, H), (1, H), (C, H), (1, H), (H, C), (1, C)] * E
+        dev = self._ws.device if self._ws is not None else torch.device("cuda")
+        out = [torch.empty(s, dtype=torch.float32, device=dev) for s in shapes]
+        ptrs = (ctypes.c_void_p * len(out))(*[t.data_ptr() for t in out])
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        capi.check(capi.lib().mgpt_moe_get_gradients(self._h, ptrs, len(out), 1, stream))
         return out
 
     # --------------------------------------------------------------- routing
