@@ -11,6 +11,12 @@ Prints one JSON line: tokens/s (value), ms/step, the roofline of the
 dominant kernel (the gate/up grouped GEMM, MFMA-bound) measured with HIP
 events inside the timed region, and the reference CPU path timed on a
 bounded sample of the same workload on this host.
+
+--pass train measures a training step instead (the training forward, which
+also keeps the backward's caches, then the backward with dy ~ N(0,1)):
+tokens/s of forward + backward, the forward and backward stage times, the
+roofline of the backward's dominant GEMM, and the reference's CPU forward +
+backward on a sample.  The driver's headline line is the default forward.
 """
 from __future__ import annotations
 
@@ -29,6 +35,8 @@ PEAK_F32_TFLOPS = 157.3      # MI355X dense fp32 matrix
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
+METRIC_TRAIN = ("MoE layer training tokens/s, forward + backward "
+                "(N=16384,C=1024,E=16,k=2)")
 CALIB_MIB = 512               # known-size elementwise copy for counter calibration
 
 
@@ -100,15 +108,16 @@ def summarize_traffic(fetch_dir: str, write_dir: str, workload: str, commands) -
             "kernels": kern, "commands": commands}
 
 
-def cpu_baseline(cfg, sample_tokens: int, reps: int):
-    """The reference's own CPU MoE forward (oracle/_ref/ref_driver, built from
-    the unmodified reference sources), single-threaded as the reference is,
-    on `sample_tokens` tokens of the workload's shape."""
+def cpu_baseline(cfg, sample_tokens: int, reps: int, train: bool = False):
+    """The reference's own CPU MoE forward (train: forward + backward)
+    (oracle/_ref/ref_driver, built from the unmodified reference sources),
+    single-threaded as the reference is, on `sample_tokens` tokens of the
+    workload's shape."""
     drv = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
     if not os.path.exists(drv):
         return None
-    cmd = [drv, "bench", str(sample_tokens), str(cfg.C), str(cfg.H), str(cfg.E), str(cfg.k),
-           str(reps)]
+    cmd = [drv, "bench_train" if train else "bench", str(sample_tokens), str(cfg.C), str(cfg.H),
+           str(cfg.E), str(cfg.k), str(reps)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
         return {"error": r.stderr[-500:]}
@@ -123,7 +132,8 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int):
         "kind": "reference",
         "sample": (f"{sample_tokens} of {cfg.N} tokens at the workload's shape "
                    f"(C={cfg.C}, E={cfg.E}, k={cfg.k}, H={cfg.H}), fp32 reference CPU path "
-                   f"(MoELayer::forward_into), 1 warmup + median of {reps}; "
+                   f"({'MoELayer::forward_into + backward_into' if train else 'MoELayer::forward_into'}), "
+                   f"1 warmup + median of {reps}; "
                    f"1 thread of {os.cpu_count()} visible cores, {model}"),
         "median_s": res["median_s"],
     }
@@ -192,6 +202,8 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pass", dest="mode", choices=["forward", "train"], default="forward",
+                    help="forward (default, the headline) or train (forward + backward)")
     ap.add_argument("--calib-copy", action="store_true",
                     help=f"after the timed run, copy {CALIB_MIB} MiB with an elementwise kernel 3 "
                          "times (known-size traffic for calibrating FETCH_SIZE/WRITE_SIZE)")
@@ -236,10 +248,20 @@ def main() -> int:
     x = torch.from_numpy(inp.x).to(dev).to(dt)
     y = torch.empty_like(x)
     del inp
+    train = args.mode == "train"
+    if train:
+        g = torch.Generator(device="cpu").manual_seed(7)
+        dy = torch.randn(x.shape, generator=g).to(dev).to(dt)
+        dx = torch.empty_like(x)
     print(f"setup {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
+    def step():
+        layer.forward_into(x, y, train)
+        if train:
+            layer.backward_into(dy, dx)
+
     for _ in range(args.warmup):
-        layer.forward_into(x, y)
+        step()
     torch.cuda.synchronize()
     counts = layer.get_expert_counts()
 
@@ -249,13 +271,16 @@ def main() -> int:
     w0 = time.perf_counter()
     start.record()
     for _ in range(args.steps):
-        layer.forward_into(x, y)
+        step()
     stop.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     ms_per_step = start.elapsed_time(stop) / args.steps
     stages = layer.stage_times()
     n_prof = stages.pop("forwards")
+    bstages = layer.backward_stage_times() if train else None
+    if bstages:
+        bstages.pop("backwards")
     layer.set_profiling(False)
 
     N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
@@ -320,7 +345,27 @@ def main() -> int:
         }),
         "wall_s_timed": round(wall, 3),
     }
-    traffic = load_traffic(cfg)
+    if train:
+        # backward products: d(act) 2ACH, dX 4ACH, dW_down 2ACH, dW_gate/up 4ACH
+        bw = {"gemm_dact_swiglu_bwd": 2.0 * A * C * H, "gemm_dx": 4.0 * A * C * H,
+              "wgrad_down": 2.0 * A * C * H, "wgrad_gateup": 4.0 * A * C * H}
+        rates = {kk: f / (bstages[kk] * 1e-3) / 1e12 for kk, f in bw.items()}
+        dom = max(bw, key=lambda kk: bstages[kk])
+        train_flops = total_flops + sum(bw.values()) + 4.0 * N * C * E
+        bwd_ms = sum(bstages.values())
+        result.update({
+            "metric": METRIC_TRAIN,
+            "pass": "train (forward_train + backward)",
+            "layer_tflops": round(train_flops / (ms_per_step * 1e-3) / 1e12, 2),
+            "backward_stage_ms": {kk: round(v, 4) for kk, v in bstages.items()},
+            "backward_ms": round(bwd_ms, 4),
+            "backward_gemm_tflops": {kk: round(v, 2) for kk, v in rates.items()},
+            "roofline": {
+                "kernel": f"backward {dom}", "bound": "mfma", "achieved": round(rates[dom], 2),
+                "peak": peak_mm, "unit": "TFLOP/s", "frac": round(rates[dom] / peak_mm, 4),
+                "traffic": None},
+        })
+    traffic = None if train else load_traffic(cfg)
     if traffic:
         gu = traffic["kernels"].get("gemm_gateup")
         result["roofline"]["traffic"] = gu["hbm_bytes"] if gu else None
@@ -339,7 +384,8 @@ def main() -> int:
         result["calib_copy_mib"] = CALIB_MIB
     if not args.no_cpu_baseline:
         print("cpu baseline ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(cfg, min(args.cpu_tokens, N), args.cpu_reps)
+        tokens = min(args.cpu_tokens // 4 if train else args.cpu_tokens, N)
+        result["cpu_baseline"] = cpu_baseline(cfg, tokens, args.cpu_reps, train)
     print(json.dumps(result))
     return 0
 

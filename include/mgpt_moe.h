@@ -179,6 +179,16 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
 int mgpt_moe_set_profiling(mgpt_moe* h, int enable);
 int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n);
 
+/* The same for the backward (measurement, no counterpart in the reference):
+ * while profiling is enabled each mgpt_moe_backward records its stage
+ * boundaries too, and this returns the mean durations in ms of
+ * [0] scatter backward, [1] d(act) product + SwiGLU backward, [2] dX
+ * product, [3] down weight + bias gradients, [4] gate/up weight + bias
+ * gradients, [5] per-token gather + softmax + router input gradient,
+ * [6] router weight gradient; if n > 7, ms[7] = backwards averaged. */
+#define MGPT_MOE_NUM_BWD_STAGES 7
+int mgpt_moe_backward_stage_times(mgpt_moe* h, float* ms, int n);
+
 /* fp8 handles only: copies expert `expert`'s quantised weight `which`
  * (0 = W_gate, 1 = W_up, 2 = W_down) to host in reference layout [in,out]
  * as e4m3 bytes, with its per-output-channel scales [out].  For tests of

@@ -25,6 +25,9 @@ MGPT_ERR_OUT_OF_MEMORY = 6
 DTYPE_F32, DTYPE_BF16, DTYPE_FP8_E4M3 = 0, 1, 2
 NUM_STAGES = 5
 STAGE_NAMES = ["router_topk", "permute", "gemm_gateup", "gemm_down", "combine"]
+NUM_BWD_STAGES = 7
+BWD_STAGE_NAMES = ["scatter_bwd", "gemm_dact_swiglu_bwd", "gemm_dx", "wgrad_down",
+                   "wgrad_gateup", "token_bwd", "router_wgrad"]
 
 
 class Config(ctypes.Structure):
@@ -80,6 +83,7 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_backward": [vp, vp, vp, vp, i, vp, sz, vp],
         "mgpt_moe_zero_grad": [vp, vp],
         "mgpt_moe_get_gradients": [vp, ctypes.POINTER(vp), i, i, vp],
+        "mgpt_moe_backward_stage_times": [vp, vp, i],
     }
     for name, args in sig.items():
         f = getattr(L, name)

@@ -185,43 +185,53 @@ __global__ __launch_bounds__(256) void token_bwd_kernel(
 constexpr int kRwChunk = 256;   // tokens per router_wgrad partial
 
 // partial[chunk][c][e] = sum over the chunk's tokens of x[t][c] * dL[t][e]
-// (thread per column, experts in registers), and in the blocks of the first
-// column range partial_b[chunk][e] = sum_t dL[t][e].
-template <typename ActT>
+// (a thread per column, EP >= E experts in registers, dL rows read from LDS
+// as float4 broadcasts), and in the blocks of the first column range
+// partial_b[chunk][e] = sum_t dL[t][e].
+template <typename ActT, int EP>
 __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restrict__ x,
                                                            const float* __restrict__ dL, int N,
                                                            int C, int E,
                                                            float* __restrict__ partial,
                                                            float* __restrict__ partial_b) {
-  __shared__ float s_dl[64][kMaxExperts];
+  __shared__ float4 s_dl[64][EP / 4];
   const int tid = threadIdx.x;
   const int chunk = blockIdx.y;
   const int c = blockIdx.x * 256 + tid;
   const int t_begin = chunk * kRwChunk, t_end = min(N, t_begin + kRwChunk);
-  float acc[kMaxExperts];
+  float acc[EP];
 #pragma unroll
-  for (int e = 0; e < kMaxExperts; ++e) acc[e] = 0.0f;
+  for (int e = 0; e < EP; ++e) acc[e] = 0.0f;
   float bsum = 0.0f;
   for (int tb = t_begin; tb < t_end; tb += 64) {
     const int nt = min(64, t_end - tb);
     __syncthreads();
-    for (int p = tid; p < nt * E; p += 256) s_dl[p / E][p % E] = dL[(size_t)(tb + p / E) * E + p % E];
+    float* sl = reinterpret_cast<float*>(s_dl);
+    for (int p = tid; p < 64 * EP; p += 256) {
+      const int r = p / EP, e = p % EP;
+      sl[p] = (r < nt && e < E) ? dL[(size_t)(tb + r) * E + e] : 0.0f;
+    }
     __syncthreads();
     if (blockIdx.x == 0 && tid < E)
-      for (int r = 0; r < nt; ++r) bsum += s_dl[r][tid];
+      for (int r = 0; r < nt; ++r) bsum += sl[r * EP + tid];
     if (c < C) {
       for (int r = 0; r < nt; ++r) {
         const float xv = to_f32(x[(size_t)(tb + r) * C + c]);
 #pragma unroll
-        for (int e = 0; e < kMaxExperts; ++e)
-          if (e < E) acc[e] += xv * s_dl[r][e];
+        for (int e4 = 0; e4 < EP / 4; ++e4) {
+          const float4 d = s_dl[r][e4];
+          acc[4 * e4 + 0] += xv * d.x;
+          acc[4 * e4 + 1] += xv * d.y;
+          acc[4 * e4 + 2] += xv * d.z;
+          acc[4 * e4 + 3] += xv * d.w;
+        }
       }
     }
   }
   if (c < C) {
     float* o = partial + ((size_t)chunk * C + c) * E;
 #pragma unroll
-    for (int e = 0; e < kMaxExperts; ++e)
+    for (int e = 0; e < EP; ++e)
       if (e < E) o[e] = acc[e];
   }
   if (blockIdx.x == 0 && tid < E) partial_b[(size_t)chunk * E + tid] = bsum;
@@ -304,8 +314,16 @@ hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int
                                hipStream_t stream) {
   if (N <= 0) return hipSuccess;
   const int chunks = router_wgrad_chunks(N);
-  hipLaunchKernelGGL(router_wgrad_kernel<ActT>, dim3((C + 255) / 256, chunks), dim3(256), 0,
-                     stream, x, dL, N, C, E, partial, partial_b);
+  const dim3 grid((C + 255) / 256, chunks);
+  if (E <= 16)
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16>), grid, dim3(256), 0, stream, x, dL, N, C,
+                       E, partial, partial_b);
+  else if (E <= 32)
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32>), grid, dim3(256), 0, stream, x, dL, N, C,
+                       E, partial, partial_b);
+  else
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64>), grid, dim3(256), 0, stream, x, dL, N, C,
+                       E, partial, partial_b);
   const int CE = C * E;
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 255) / 256), dim3(256), 0, stream,
                      partial, partial_b, chunks, CE, E, gW, gb);

@@ -206,8 +206,8 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
                                            const Tile& cur, int wn, int wm, int lrow, int lhalf,
                                            const float* __restrict__ bias0,
                                            const float* __restrict__ bias1, int n_store,
-                                           int bias_ld, bf16_t* __restrict__ out, int ldo,
-                                           bf16_t* __restrict__ save, int save_ld) {
+                                           int bias_ld, bf16_t* out, int ldo, bf16_t* save,
+                                           int save_ld) {
   using W = Waves<NW>;
   const int tok_base = cur.row0 + wm * W::WTM + lrow;
   if constexpr (EPI == kEpiGateUp) {
@@ -262,20 +262,81 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
       // accumulator read (TN * TM * 16 values) ahead of the stores
       __builtin_amdgcn_sched_barrier(0);
     }
+  } else if constexpr (EPI == kEpiSwigluBwd) {
+    // The features are hidden units h and the accumulators d(act)[row][h];
+    // save holds the pre-activations g, u of h at its packed columns (32 gate
+    // then 32 up per 32 units), and d(gate), d(up) overwrite them there.
+#pragma unroll
+    for (int j = 0; j < W::TN; ++j) {
+      const int hb = cur.n0 + wn * W::WTN + j * 32;
+      if (hb >= n_store) continue;
+      const int pc = packed_gate_col(hb);
+      // the loads of two 32-token sub-tiles at a time: half the memory
+      // round trips of one at a time, within the register budget
+      constexpr int kPair = 2;
+#pragma unroll
+      for (int i2 = 0; i2 < W::TM; i2 += kPair) {
+        uint2 gq[kPair][4], uq[kPair][4];
+#pragma unroll
+        for (int ii = 0; ii < kPair; ++ii) {
+          const int row = tok_base + (i2 + ii) * 32;
+          const bool ok = row < cur.row_end;
+          const bf16_t* src = save + (size_t)row * save_ld + pc + 4 * lhalf;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            gq[ii][g] = ok ? *reinterpret_cast<const uint2*>(src + 8 * g) : make_uint2(0u, 0u);
+            uq[ii][g] = ok ? *reinterpret_cast<const uint2*>(src + 32 + 8 * g) : make_uint2(0u, 0u);
+          }
+        }
+#pragma unroll
+        for (int ii = 0; ii < kPair; ++ii) {
+          const int i = i2 + ii;
+          const int row = tok_base + i * 32;
+          const bool ok = row < cur.row_end;
+          const f32x16 a = acc_fetch<NW>(acc[j][i]);
+          uint2 dq[4], uqo[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float dg[4], du[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t gw = q < 2 ? gq[ii][g].x : gq[ii][g].y;
+              const uint32_t uw = q < 2 ? uq[ii][g].x : uq[ii][g].y;
+              const float gv = __uint_as_float((q & 1) ? (gw & 0xFFFF0000u) : (gw << 16));
+              const float uv = __uint_as_float((q & 1) ? (uw & 0xFFFF0000u) : (uw << 16));
+              const float d = a[4 * g + q];
+              const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-gv));
+              du[q] = d * (gv * sig);
+              dg[q] = (d * uv) * (sig * (1.0f + gv * (1.0f - sig)));
+            }
+            dq[g] = pack4_bf16(dg[0], dg[1], dg[2], dg[3]);
+            uqo[g] = pack4_bf16(du[0], du[1], du[2], du[3]);
+          }
+          store_group32(out + (size_t)row * ldo + pc, dq, lhalf, ok);
+          store_group32(out + (size_t)row * ldo + pc + 32, uqo, lhalf, ok);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < W::TN; ++j) {
       const int cb = cur.n0 + wn * W::WTN + j * 32;
       if (cb >= n_store) continue;   // n_store is a multiple of 64
-      const float* bdp = bias0 + (size_t)cur.expert * bias_ld + cb;
       float b[16];
+      if (bias0) {
+        const float* bdp = bias0 + (size_t)cur.expert * bias_ld + cb;
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float b0 = uniform_load(bdp + 8 * g + q), b1 = uniform_load(bdp + 8 * g + 4 + q);
-          b[4 * g + q] = lhalf ? b1 : b0;
-        }
+          for (int q = 0; q < 4; ++q) {
+            const float b0 = uniform_load(bdp + 8 * g + q), b1 = uniform_load(bdp + 8 * g + 4 + q);
+            b[4 * g + q] = lhalf ? b1 : b0;
+          }
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) b[v] = 0.0f;
+      }
 #pragma unroll
       for (int i = 0; i < W::TM; ++i) {
         const int row = tok_base + i * 32;
@@ -355,8 +416,8 @@ template <int EPI, int NW>
 __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
-    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, float* __restrict__ partials,
-    bf16_t* __restrict__ save, int save_ld) {
+    int n_store, int bias_ld, bf16_t* out, int ldo, float* __restrict__ partials, bf16_t* save,
+    int save_ld) {
   using W = Waves<NW>;
   constexpr int kTN = W::TN, kTM = W::TM;
   constexpr int kUnits = 5;
@@ -639,7 +700,11 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
         a.x += x.x; a.y += x.y; a.z += x.z; a.w += x.w;
       }
       const int f = cb + 8 * g + 4 * lhalf;
-      const float* b = bias0 + (size_t)tile.expert * bias_ld + f;
+      float b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (bias0) {
+        const float* bp = bias0 + (size_t)tile.expert * bias_ld + f;
+        b[0] = bp[0]; b[1] = bp[1]; b[2] = bp[2]; b[3] = bp[3];
+      }
       *reinterpret_cast<uint2*>(out + (size_t)row * ldo + f) =
           pack4_bf16(a.x + b[0], a.y + b[1], a.z + b[2], a.w + b[3]);
     }
@@ -659,7 +724,10 @@ constexpr int kRingWaves = MGPT_RING_WAVES;
 // split last round; the reduce kernel that follows exits at once when the
 // counts leave nothing to split.  save (gate/up only, and only without
 // partials) also stores the pre-activations g + b_g, u + b_u as bf16 in the
-// packed column order, save[row][n] with leading dimension save_ld.  Measured on MI355X (cfg3 shapes, skewed
+// packed column order, save[row][n] with leading dimension save_ld.
+// SWIGLU_BWD (no partials) reads those pre-activations from save and writes
+// d(gate), d(up) to out in the same layout (out may equal save).  DOWN
+// adds no bias when bias0 is null.  Measured on MI355X (cfg3 shapes, skewed
 // counts): the split 5-unit ring (gate/up 1035, down 871 TFLOP/s) beats a
 // 2-slab ring of 64 KB slabs (1034, 827) and 32-column slabs (4 x 32: 938,
 // 724; 5 x 32 with 2 per barrier: 970, 786), whose 64-byte row segments
@@ -677,19 +745,21 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
   if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0 || num_cus <= 0 || ldo % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(out) & 15) != 0)
     return hipErrorInvalidValue;
-  if (save && (EPI != kEpiGateUp || partials || save_ld % 8 != 0 ||
+  if (save && (EPI == kEpiDown || partials || save_ld % 8 != 0 ||
                (reinterpret_cast<uintptr_t>(save) & 15) != 0))
     return hipErrorInvalidValue;
+  if (EPI == kEpiSwigluBwd && !save) return hipErrorInvalidValue;
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
   hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves>), dim3(grid), dim3(kRingWaves * kWave), 0,
                      stream, A, B, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
                      partials, save, save_ld);
-  if (partials)
-    hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256), 0,
-                       stream,
-                       partials, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
-                       grid);
+  if constexpr (EPI != kEpiSwigluBwd) {
+    if (partials)
+      hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256), 0,
+                         stream, partials, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out,
+                         ldo, grid);
+  }
   return hipGetLastError();
 }
 
@@ -701,5 +771,9 @@ template hipError_t launch_gemm_dma<kEpiDown>(const bf16_t*, const bf16_t*, cons
                                               const float*, const int32_t*, int, int, int, int,
                                               int, bf16_t*, int, int, float*, int, bf16_t*, int,
                                               hipStream_t);
+template hipError_t launch_gemm_dma<kEpiSwigluBwd>(const bf16_t*, const bf16_t*, const float*,
+                                                   const float*, const int32_t*, int, int, int,
+                                                   int, int, bf16_t*, int, int, float*, int,
+                                                   bf16_t*, int, hipStream_t);
 
 }  // namespace mgpt

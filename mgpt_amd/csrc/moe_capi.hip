@@ -158,6 +158,8 @@ struct mgpt_moe {
   bool profiling = false;
   hipEvent_t ev[kProfSlots][MGPT_MOE_NUM_STAGES + 1] = {};
   int prof_count = 0;
+  hipEvent_t evb[kProfSlots][MGPT_MOE_NUM_BWD_STAGES + 1] = {};
+  int prof_b_count = 0;
   hipEvent_t done = nullptr;
   bool done_valid = false;
   const int32_t* last_counts = nullptr;
@@ -327,6 +329,9 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
     for (auto& slot : h->ev)
       for (auto& ev : slot)
         if (e == hipSuccess) e = hipEventCreate(&ev);
+    for (auto& slot : h->evb)
+      for (auto& ev : slot)
+        if (e == hipSuccess) e = hipEventCreate(&ev);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->done, hipEventDisableTiming);
   }
   if (e != hipSuccess) {
@@ -342,6 +347,9 @@ int mgpt_moe_destroy(mgpt_moe* h) {
   free_weights(h);
   if (h->grad) (void)hipFree(h->grad);
   for (auto& slot : h->ev)
+    for (auto& ev : slot)
+      if (ev) (void)hipEventDestroy(ev);
+  for (auto& slot : h->evb)
     for (auto& ev : slot)
       if (ev) (void)hipEventDestroy(ev);
   if (h->done) (void)hipEventDestroy(h->done);
@@ -617,21 +625,40 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   float* g = h->grad;
   const ActT* wdb = (const ActT*)h->wdb;
   const ActT* wgub = (const ActT*)h->wgub;
+  const bool prof = h->profiling;
+  hipEvent_t* evs = h->evb[h->prof_b_count % mgpt_moe::kProfSlots];
+  auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
+  HIP_TRY(mark(0));
   HIP_TRY(launch_scatter_bwd<ActT>(dy, ob, perm, topp, A, C, k, dgo, dtp, st));
+  HIP_TRY(mark(1));
   if constexpr (sizeof(ActT) == 4) {
     const int mt = (A + 63) / 64 + E;
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiSwigluBwd, float>(
         dgo, wdb, nullptr, nullptr, nullptr, counts, E, C, h->Hq, Hp, 0, gu, 2 * Hp, mt, gu,
         2 * Hp, st)));
+    HIP_TRY(mark(2));
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiDown, float>(
         gu, wgub, nullptr, nullptr, nullptr, counts, E, 2 * Hp, Cp, C, 0, ob, C, mt, nullptr, 0,
         st)));
+  } else if (h->uses_gemm_dma(N)) {
+    // prefill-shaped segments: the 256x256 direct-to-LDS kernel; the dX
+    // product splits its last round like the forward's down GEMM
+    const int mt = (A + 255) / 256 + E;
+    HIP_TRY(launch_gemm_dma<kEpiSwigluBwd>((const bf16_t*)dgo, (const bf16_t*)wdb, nullptr,
+                                           nullptr, counts, E, C, h->Hq, Hp, 0, (bf16_t*)gu,
+                                           2 * Hp, mt, nullptr, h->num_cus, (bf16_t*)gu, 2 * Hp,
+                                           st));
+    HIP_TRY(mark(2));
+    HIP_TRY(launch_gemm_dma<kEpiDown>((const bf16_t*)gu, (const bf16_t*)wgub, nullptr, nullptr,
+                                      counts, E, 2 * Hp, Cp, C, 0, (bf16_t*)ob, C, mt,
+                                      (float*)(ws + L.partials), h->num_cus, nullptr, 0, st));
   } else if (small_m(h, N)) {
     const int mt = (A + 31) / 32 + E;
     HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t>(
         dgo, wdb, nullptr, nullptr, nullptr, counts, E, C, h->Hq, Hp, 0, gu, 2 * Hp, mt, gu,
         2 * Hp, st)));
+    HIP_TRY(mark(2));
     HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiDown, bf16_t>(
         gu, wgub, nullptr, nullptr, nullptr, counts, E, 2 * Hp, Cp, C, 0, ob, C, mt, nullptr, 0,
         st)));
@@ -640,22 +667,29 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
     HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t>(
         dgo, wdb, nullptr, nullptr, nullptr, counts, E, C, h->Hq, Hp, 0, gu, 2 * Hp, mt, gu,
         2 * Hp, st)));
+    HIP_TRY(mark(2));
     HIP_TRY((launch_grouped_gemm<128, 128, 2, 2, bf16_t, bf16_t, kEpiDown, bf16_t>(
         gu, wgub, nullptr, nullptr, nullptr, counts, E, 2 * Hp, Cp, C, 0, ob, C, mt, nullptr, 0,
         st)));
   }
+  HIP_TRY(mark(3));
   // dW_down [H][C] and db_down from (h, dgo); dW_gate/up [C][H] and their
   // biases from (gathered x, d(gate)/d(up))
   HIP_TRY((launch_wgrad<ActT, 0>(hb, Hp, Hp, dgo, C, C, counts, E, g + h->g_off[6], nullptr, C,
                                  (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, st)));
+  HIP_TRY(mark(4));
   HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
                                  g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
                                  g + h->g_off[5], (size_t)H, st)));
+  HIP_TRY(mark(5));
   HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wr_g,
                                  router_experts_per_wave(E), N, C, E, k, dx, dlog, st));
+  HIP_TRY(mark(6));
   HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
                                     (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
                                     st));
+  HIP_TRY(mark(7));
+  if (prof) ++h->prof_b_count;
   return MGPT_OK;
 }
 
@@ -828,6 +862,27 @@ int mgpt_moe_set_profiling(mgpt_moe* h, int enable) {
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   h->profiling = enable != 0;
   h->prof_count = 0;
+  h->prof_b_count = 0;
+  return MGPT_OK;
+}
+
+int mgpt_moe_backward_stage_times(mgpt_moe* h, float* ms, int n) {
+  constexpr int S = MGPT_MOE_NUM_BWD_STAGES;
+  if (!h || !ms || n < S) return fail(MGPT_ERR_INVALID_ARGUMENT, "need room for %d stage times", S);
+  if (h->prof_b_count == 0) return fail(MGPT_ERR_NOT_READY, "no profiled backward has been run");
+  const int slots = std::min(h->prof_b_count, mgpt_moe::kProfSlots);
+  const int last = (h->prof_b_count - 1) % mgpt_moe::kProfSlots;
+  HIP_TRY(hipEventSynchronize(h->evb[last][S]));
+  for (int i = 0; i < S; ++i) {
+    double sum = 0.0;
+    for (int sl = 0; sl < slots; ++sl) {
+      float t = 0.0f;
+      HIP_TRY(hipEventElapsedTime(&t, h->evb[sl][i], h->evb[sl][i + 1]));
+      sum += t;
+    }
+    ms[i] = (float)(sum / slots);
+  }
+  if (n > S) ms[S] = (float)slots;
   return MGPT_OK;
 }
 

@@ -21,6 +21,15 @@
 // Bias gradients are the column sums of Q: the threads that transpose Q
 // blocks add up their rows while doing so, and the blocks of the first
 // i-tile reduce and accumulate them.
+//
+// Block -> tile map.  An expert's tile grid (Iy x Jx tiles of 256 x 256) is
+// cut into groups of up to 16 tiles (gy x gx rectangles), the groups of all
+// experts are listed heaviest expert first (count descending, then id), and
+// group j goes to XCD j % 8 (the hardware deals workgroup ids round-robin
+// to the 8 XCDs).  The 32 CUs of an XCD thus run two 16-tile rectangles at
+// a time and share their operand panels (gy P panels, gx Q panels) in the
+// XCD's L2, instead of every tile reading both panels from HBM; the
+// longest contractions start first.
 #include "common.hpp"
 
 namespace mgpt {
@@ -43,36 +52,153 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 4)) & 7; }
 
 typedef __attribute__((address_space(3))) char lds_char;
 
+// The tile and expert segment of this block (see the block -> tile map
+// above); false past the last tile or for an expert without rows.  Called
+// by every thread of the block (shared memory and a barrier).
+struct WgTile {
+  int seg0, cnt, e, ty, tx;
+};
+
+__device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, int E, int Iy,
+                                          int Jx, int gy, int gx, WgTile* out) {
+  __shared__ int s_seg[5];
+  if (threadIdx.x < kWave) {
+    const int l = lane_id();
+    const int cnt = l < E ? counts[l] : 0;
+    const int incl = wave_incl_scan(cnt);
+    // rank of expert l in (count descending, id ascending)
+    int rank = 0;
+    for (int e2 = 0; e2 < E; ++e2) {
+      const int c2 = __shfl(cnt, e2, kWave);
+      rank += (c2 > cnt) || (c2 == cnt && e2 < l);
+    }
+    const int ngx = (Jx + gx - 1) / gx;
+    const int ng = ((Iy + gy - 1) / gy) * ngx;   // groups per expert
+    const int b = blockIdx.x, sidx = b / kNumXcd;
+    const int j = (sidx / 16) * kNumXcd + b % kNumXcd, r = sidx % 16;
+    const int pos = j / ng, gi = j % ng;
+    const bool mine = l < E && rank == pos;
+    const unsigned long long m = __ballot(mine);
+    if (l == 0) {
+      const int ty = (gi / ngx) * gy + r / gx, tx = (gi % ngx) * gx + r % gx;
+      const bool ok = m != 0 && r < gy * gx && ty < Iy && tx < Jx;
+      s_seg[2] = ok ? ty : -1;
+      s_seg[3] = tx;
+    }
+    if (mine) {
+      s_seg[0] = incl - cnt;
+      s_seg[1] = cnt;
+      s_seg[4] = l;
+    }
+  }
+  __syncthreads();
+  out->ty = s_seg[2];
+  if (out->ty < 0) return false;
+  out->seg0 = s_seg[0];
+  out->cnt = s_seg[1];
+  out->tx = s_seg[3];
+  out->e = s_seg[4];
+  return out->cnt > 0;
+}
+
+// Accumulates a wave's 128 (i) x 64 (j) block of D into the gradient
+// (+=, like add_grad).  Register v of tile (ti, tj) is D[i][j] with
+// i = 8*(v/4) + 4*lhalf + v%4 and j = lrow inside the tile.  All loads of
+// a 16-value group are issued before any add, so the read-modify-write
+// costs one memory round trip per group instead of one per value; rows
+// past i_store (only in the last row tile) take a guarded path.  MODE 1:
+// the j columns are gate/up interleaved (32 gate, then 32 up, per 32
+// units) and go to out0 / out1 at column h.
+template <int MODE>
+__device__ __forceinline__ void wg_accumulate(const f32x16 (&acc)[4][2], int i_base, int j_base,
+                                              int lrow, int lhalf, int e, float* out0,
+                                              float* out1, int ldo, size_t out_estride,
+                                              int i_store, int j_store) {
+  constexpr int TI = 4, TJ = 2;
+  const bool rows_full = i_base + TI * 32 <= i_store;   // wave-uniform
+#pragma unroll
+  for (int tj = 0; tj < TJ; ++tj) {
+    const int j = j_base + tj * 32 + lrow;
+    float* ob;
+    int col;
+    bool jok;
+    if constexpr (MODE == 0) {
+      ob = out0;
+      col = j;
+      jok = j < j_store;
+    } else {
+      ob = ((j >> 5) & 1) ? out1 : out0;
+      col = (j >> 6) * 32 + (j & 31);
+      jok = col < j_store;
+    }
+    if (!jok) continue;
+    ob += (size_t)e * out_estride + col;
+    float* orow = ob + (size_t)(i_base + 4 * lhalf) * ldo;
+    if (rows_full) {
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti) {
+        float old[16];
+#pragma unroll
+        for (int v = 0; v < 16; ++v) old[v] = orow[(size_t)(ti * 32 + 8 * (v / 4) + (v % 4)) * ldo];
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          orow[(size_t)(ti * 32 + 8 * (v / 4) + (v % 4)) * ldo] = old[v] + acc[ti][tj][v];
+      }
+    } else {
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int di = ti * 32 + 8 * (v / 4) + (v % 4);
+          if (i_base + 4 * lhalf + di < i_store) {
+            float* o = orow + (size_t)di * ldo;
+            *o = *o + acc[ti][tj][v];
+          }
+        }
+    }
+  }
+}
+
+// Adds column sum `sum` of tile column j to the bias gradient.
+template <int MODE>
+__device__ __forceinline__ void wg_bias_add(float sum, int j, int e, float* bias0, float* bias1,
+                                            size_t bias_estride, int j_store) {
+  float* bb;
+  int col;
+  bool ok;
+  if constexpr (MODE == 0) {
+    bb = bias0;
+    col = j;
+    ok = j < j_store;
+  } else {
+    bb = ((j >> 5) & 1) ? bias1 : bias0;
+    col = (j >> 6) * 32 + (j & 31);
+    ok = col < j_store;
+  }
+  if (ok) {
+    float* o = bb + (size_t)e * bias_estride + col;
+    *o = *o + sum;
+  }
+}
+
 template <typename T, int MODE>
 __global__ __launch_bounds__(kThreads) void wgrad_kernel(
     const T* __restrict__ P, int ldp, int p_valid, const T* __restrict__ Q, int ldq, int q_valid,
-    const int32_t* __restrict__ counts, int E, float* __restrict__ out0,
-    float* __restrict__ out1, int ldo, size_t out_estride, int i_store, int j_store,
-    float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride) {
+    const int32_t* __restrict__ counts, int E, int Iy, int Jx, int gy, int gx,
+    float* __restrict__ out0, float* __restrict__ out1, int ldo, size_t out_estride, int i_store,
+    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride) {
   constexpr int BK = WgT<T>::BK, EPV = WgT<T>::EPV;
   constexpr int NB = (BK / EPV) * (256 / EPV) / 256;   // transposed blocks per thread
   constexpr int FB = 256 / EPV;                        // feature blocks per tile
   constexpr bool kBf = sizeof(T) == 2;
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * kOpBytes];
-  __shared__ int s_seg[2];
-
-  const int e = blockIdx.z;
   const int tid = threadIdx.x;
-  if (tid < kWave) {
-    const int l = lane_id();
-    const int cnt = l < E ? counts[l] : 0;
-    const int incl = wave_incl_scan(cnt);
-    if (l == e) {
-      s_seg[0] = incl - cnt;
-      s_seg[1] = cnt;
-    }
-  }
-  __syncthreads();
-  const int seg0 = s_seg[0], cnt = s_seg[1];
-  if (cnt == 0) return;   // block-uniform: an unchosen expert gets no gradient
+  WgTile tl;
+  if (!wg_locate(counts, E, Iy, Jx, gy, gx, &tl)) return;
+  const int seg0 = tl.seg0, cnt = tl.cnt, e = tl.e, ty = tl.ty, tx = tl.tx;
   const int seg_end = seg0 + cnt;
-  const int i0 = blockIdx.y * kTI, j0 = blockIdx.x * kTJ;
-  const bool do_bias = blockIdx.y == 0 && bias0 != nullptr;
+  const int i0 = ty * kTI, j0 = tx * kTJ;
+  const bool do_bias = ty == 0 && bias0 != nullptr;
 
   // Loader role: waves 0-3 transpose P blocks, waves 4-7 Q blocks.
   const int op = tid / 256, tt = tid % 256;
@@ -227,37 +353,8 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(
     __syncthreads();
   }
 
-  // Accumulate: register v of tile (ti, tj) is D[i][j] with
-  // i = 8*(v/4) + 4*lhalf + v%4 and j = lrow inside the tile.
-#pragma unroll
-  for (int tj = 0; tj < TJ; ++tj) {
-    const int j = j0 + wj * 64 + tj * 32 + lrow;
-    float* ob;
-    int col;
-    bool jok;
-    if constexpr (MODE == 0) {
-      ob = out0;
-      col = j;
-      jok = j < j_store;
-    } else {
-      // gate/up interleaved columns: 32 gate, then 32 up, per 32 units
-      ob = ((j >> 5) & 1) ? out1 : out0;
-      col = (j >> 6) * 32 + (j & 31);
-      jok = col < j_store;
-    }
-    if (!jok) continue;
-    ob += (size_t)e * out_estride + col;
-#pragma unroll
-    for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int i = i0 + wi * 128 + ti * 32 + 8 * (v / 4) + 4 * lhalf + (v % 4);
-        if (i < i_store) {
-          float* o = ob + (size_t)i * ldo;
-          *o = *o + acc[ti][tj][v];
-        }
-      }
-  }
+  wg_accumulate<MODE>(acc, i0 + wi * 128, j0 + wj * 64, lrow, lhalf, e, out0, out1, ldo,
+                      out_estride, i_store, j_store);
 
   if (!do_bias) return;
   // Column sums: the partial of feature block fb from row block sb goes to
@@ -279,22 +376,190 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(
     float sum = 0.0f;
 #pragma unroll
     for (int sb = 0; sb < BK / EPV; ++sb) sum += s_b[sb * 256 + tid];
-    float* bb;
-    int col;
-    bool ok;
-    if constexpr (MODE == 0) {
-      bb = bias0;
-      col = j;
-      ok = j < j_store;
-    } else {
-      bb = ((j >> 5) & 1) ? bias1 : bias0;
-      col = (j >> 6) * 32 + (j & 31);
-      ok = col < j_store;
+    wg_bias_add<MODE>(sum, j, e, bias0, bias1, bias_estride, j_store);
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// bf16: the operands go from HBM straight into LDS (global_load_lds, no
+// registers) in their row-major layout, and the MFMA fragments are read
+// with gfx950's transposing LDS read ds_read_b64_tr_b16.  Measured lane
+// layout of that read: within each 16-lane group, output element q of lane
+// i is element i%4 of the 8 bytes addressed by lane 4q + i/4.  So when lane
+// 4q + r addresses row k0 + q, features m0 + 4r .. m0 + 4r + 3 of a
+// [row][feature] tile, lane i receives feature m0 + i at rows k0 .. k0 + 3:
+// two such reads give the 8 consecutive k of an MFMA operand.
+//
+// LDS: a ring of 4 stages of 32 rows (P rows, then Q rows; 512-byte rows of
+// 256 features), filled 3 slabs ahead.  64-byte chunk c of row k sits at
+// chunk c ^ (k & 3), so the 4 rows one read touches fall in distinct bank
+// groups.  Rows past the expert's segment in the last slab are zeroed
+// before use.
+constexpr int kTrBK = 32;                         // rows per slab
+constexpr int kTrStages = 4;
+constexpr int kTrRowBytes = 512;                  // 256 bf16 features
+constexpr int kTrOpBytes = kTrBK * kTrRowBytes;   // 16 KB
+constexpr int kTrStageBytes = 2 * kTrOpBytes;
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4s lds_v4s;
+
+// One 1 KB direct-to-LDS load (lane l's 16 bytes land at lds + 16*l); the
+// compiler does not track it, the kernel waits with tr_wait_barrier.
+__device__ __forceinline__ void tr_dma16(const void* g, uint32_t lds) {
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(lds) : "memory");
+}
+
+// This wave's loads except the newest N have landed and its LDS accesses
+// are complete; then meet the other waves.
+template <int N>
+__device__ __forceinline__ void tr_wait_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ bf16x8 tr_frag(const char* base, int kb, int c, int moff) {
+  // rows kb .. kb+3 (first read) and kb+4 .. kb+7 (second); kb % 4 == 0
+  const int k0 = kb, k1 = kb + 4;
+  const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4s*)(base + k0 * kTrRowBytes + ((c ^ (k0 & 3)) << 6) + moff));
+  const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4s*)(base + k1 * kTrRowBytes + ((c ^ (k1 & 3)) << 6) + moff));
+  typedef short v8s __attribute__((ext_vector_type(8)));
+  const v8s r = __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
+    const bf16_t* __restrict__ P, int ldp, const bf16_t* __restrict__ Q, int ldq,
+    const int32_t* __restrict__ counts, int E, int Iy, int Jx, int gy, int gx,
+    float* __restrict__ out0, float* __restrict__ out1, int ldo, size_t out_estride, int i_store,
+    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride) {
+  __shared__ __attribute__((aligned(1024))) char smem[kTrStages * kTrStageBytes];
+  const int tid = threadIdx.x;
+  WgTile tl;
+  if (!wg_locate(counts, E, Iy, Jx, gy, gx, &tl)) return;
+  const int seg0 = tl.seg0, cnt = tl.cnt, e = tl.e;
+  const int i0 = tl.ty * kTI, j0 = tl.tx * kTJ;
+  const bool do_bias = tl.ty == 0 && bias0 != nullptr;
+  const int KT = (cnt + kTrBK - 1) / kTrBK;
+
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave), lane = lane_id();
+  // DMA role: waves 0-3 load P rows, waves 4-7 Q rows, 8 rows (4 x 1 KB) each
+  const int op = w / 4, wl = w % 4;
+  const bf16_t* src = op ? Q : P;
+  const int ld = op ? ldq : ldp;
+  const int f0 = op ? j0 : i0;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)smem;
+  const int slot = lane & 31;
+  auto dma_slab = [&](int kt) __attribute__((always_inline)) {
+    // past the last slab: repeat it (in bounds; the stage is never read)
+    const int kk = kt < KT ? kt : KT - 1;
+    const int s0 = seg0 + kk * kTrBK;
+    const uint32_t base =
+        lds0 + (uint32_t)((kt % kTrStages) * kTrStageBytes + op * kTrOpBytes + wl * 4096);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int r = wl * 8 + 2 * u + (lane >> 5);
+      const int c = (slot >> 2) ^ (r & 3);
+      const bf16_t* g = src + (size_t)(s0 + r) * ld + f0 + c * 32 + (slot & 3) * 8;
+      tr_dma16(g, base + u * 1024);
     }
-    if (ok) {
-      float* o = bb + (size_t)e * bias_estride + col;
-      *o = *o + sum;
+  };
+
+  const int wi = w / 4, wj = w % 4;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+  const int grp = lane >> 4, gl = lane & 15;
+  // this lane's part of a transposing read: row offset and byte offset
+  const int krow = 8 * (grp >> 1) + (gl >> 2);
+  const int moff = (16 * (grp & 1) + 4 * (gl & 3)) * 2;
+  constexpr int TI = 4, TJ = 2;
+  f32x16 acc[TI][TJ];
+#pragma unroll
+  for (int a = 0; a < TI; ++a)
+#pragma unroll
+    for (int b = 0; b < TJ; ++b)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[a][b][v] = 0.0f;
+  float bsum[8];
+#pragma unroll
+  for (int q = 0; q < 8; ++q) bsum[q] = 0.0f;
+
+  dma_slab(0);
+  dma_slab(1);
+  dma_slab(2);
+  for (int kt = 0; kt < KT; ++kt) {
+    tr_wait_barrier<8>();
+    const char* st = smem + (kt % kTrStages) * kTrStageBytes;
+    const int valid = cnt - kt * kTrBK;
+    if (valid < kTrBK) {
+      // last slab: rows past the segment (other experts' rows or padding)
+      // become zeros in both operands
+      char* zs = smem + (kt % kTrStages) * kTrStageBytes;
+      const int nz = (kTrBK - valid) * (kTrRowBytes / 16);   // 16-byte units per operand
+      for (int u = tid; u < 2 * nz; u += kThreads) {
+        const int o = u / nz, x = u % nz;
+        *reinterpret_cast<uint4*>(zs + o * kTrOpBytes + valid * kTrRowBytes + x * 16) =
+            make_uint4(0u, 0u, 0u, 0u);
+      }
+      __syncthreads();
     }
+    dma_slab(kt + 3);   // into the stage of slab kt-1, which every wave has finished
+    if (do_bias) {
+      const char* qs = st + kTrOpBytes;
+      const int fb = tid & 31, c = fb >> 2, sub = fb & 3;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int r = (tid >> 5) + 16 * h;
+        const uint4 v = *reinterpret_cast<const uint4*>(qs + r * kTrRowBytes +
+                                                        ((c ^ (r & 3)) << 6) + sub * 16);
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          bsum[2 * q] += __uint_as_float(wv[q] << 16);
+          bsum[2 * q + 1] += __uint_as_float(wv[q] & 0xFFFF0000u);
+        }
+      }
+    }
+    const char* ps = st;
+    const char* qs = st + kTrOpBytes;
+    bf16x8 af[2][TI], bfr[2][TJ];
+    auto frags = [&](int ks, bf16x8 (&a)[TI], bf16x8 (&b)[TJ]) __attribute__((always_inline)) {
+      const int kb = ks * 16 + krow;
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti) a[ti] = tr_frag(ps, kb, wi * 4 + ti, moff);
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj) b[tj] = tr_frag(qs, kb, wj * 2 + tj, moff);
+    };
+    frags(0, af[0], bfr[0]);
+#pragma unroll
+    for (int ks = 0; ks < kTrBK / 16; ++ks) {
+      if (ks + 1 < kTrBK / 16) frags(ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < TJ; ++tj)
+          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][ti], bfr[ks & 1][tj],
+                                                                acc[ti][tj], 0, 0, 0);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeated tail loads
+
+  wg_accumulate<MODE>(acc, i0 + wi * 128, j0 + wj * 64, lrow, lhalf, e, out0, out1, ldo,
+                      out_estride, i_store, j_store);
+  if (!do_bias) return;
+  // Column sums: thread t holds features 8*(t%32) .. +7 of row group t/32;
+  // one thread per feature then adds the 16 row groups in order.
+  __syncthreads();   // every wave is done with the ring
+  float* s_b = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int q = 0; q < 8; ++q) s_b[(tid >> 5) * 256 + (tid & 31) * 8 + q] = bsum[q];
+  __syncthreads();
+  if (tid < 256) {
+    float sum = 0.0f;
+    for (int g = 0; g < 16; ++g) sum += s_b[g * 256 + tid];
+    wg_bias_add<MODE>(sum, j0 + tid, e, bias0, bias1, bias_estride, j_store);
   }
 }
 
@@ -317,10 +582,20 @@ hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, i
       (reinterpret_cast<uintptr_t>(P) & 15) || (reinterpret_cast<uintptr_t>(Q) & 15))
     return hipErrorInvalidValue;
   if (i_store <= 0 || q_valid <= 0) return hipSuccess;
-  const dim3 grid((q_valid + kTJ - 1) / kTJ, (i_store + kTI - 1) / kTI, E);
-  hipLaunchKernelGGL((wgrad_kernel<T, MODE>), grid, dim3(kThreads), 0, stream, P, ldp, p_valid, Q,
-                     ldq, q_valid, counts, E, out0, out1, ldo, out_estride, i_store, j_store,
-                     bias0, bias1, bias_estride);
+  const int Iy = (i_store + kTI - 1) / kTI, Jx = (q_valid + kTJ - 1) / kTJ;
+  const int gx = Jx < 4 ? Jx : 4, gy = 16 / gx;
+  const int ng = ((Iy + gy - 1) / gy) * ((Jx + gx - 1) / gx);
+  const int groups = E * ng;
+  const int blocks = 16 * kNumXcd * ((groups + kNumXcd - 1) / kNumXcd);
+  if constexpr (sizeof(T) == 2) {
+    hipLaunchKernelGGL((wgrad_tr_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, stream, P, ldp,
+                       Q, ldq, counts, E, Iy, Jx, gy, gx, out0, out1, ldo, out_estride, i_store,
+                       j_store, bias0, bias1, bias_estride);
+  } else {
+    hipLaunchKernelGGL((wgrad_kernel<T, MODE>), dim3(blocks), dim3(kThreads), 0, stream, P, ldp,
+                       p_valid, Q, ldq, q_valid, counts, E, Iy, Jx, gy, gx, out0, out1, ldo,
+                       out_estride, i_store, j_store, bias0, bias1, bias_estride);
+  }
   return hipGetLastError();
 }
 

@@ -214,6 +214,16 @@ class MoELayer:
         out["forwards"] = int(ms[capi.NUM_STAGES])
         return out
 
+    def backward_stage_times(self) -> dict:
+        """Mean backward stage durations (ms) over the profiled backwards
+        since set_profiling(True), plus their count."""
+        n = capi.NUM_BWD_STAGES
+        ms = np.zeros(n + 1, dtype=np.float32)
+        capi.check(capi.lib().mgpt_moe_backward_stage_times(self._h, ms.ctypes.data, n + 1))
+        out = dict(zip(capi.BWD_STAGE_NAMES, ms[:n].tolist()))
+        out["backwards"] = int(ms[n])
+        return out
+
     def export_fp8(self, expert: int, which: int):
         rows, cols = (self.C, self.H) if which < 2 else (self.H, self.C)
         q = np.zeros((rows, cols), np.uint8)

@@ -9,6 +9,7 @@
 //   ref_driver run  <in.bin> <out.bin>
 //   ref_driver backward <in.bin> <dy.bin> <grad.bin>
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
+//   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (forward + backward)
 //
 // in.bin : "MGPTMOE1", int32 N C H E k, then float32 x[N*C] and the 2+6E
 //          parameters in MoELayer::get_parameters() order
@@ -145,10 +146,11 @@ int backward(const char* in_path, const char* dy_path, const char* out_path) {
   return 0;
 }
 
-// Times MoELayer::forward_into on one fresh layer (its CPU caches are sized
-// on first use and never resized, layers/MoELayer.cpp:42-50): 1 warmup, then
-// `reps` timed runs; prints one JSON line with every run and the median.
-int bench(int N, int C, int H, int E, int k, int reps) {
+// Times MoELayer::forward_into (train: forward_into then backward_into with
+// dout ~ N(0,1)) on one fresh layer (its CPU caches are sized on first use
+// and never resized, layers/MoELayer.cpp:42-50): 1 warmup, then `reps`
+// timed runs; prints one JSON line with every run and the median.
+int bench(int N, int C, int H, int E, int k, int reps, bool train) {
   std::mt19937 gen(20261201u);
   std::normal_distribution<float> nd(0.0f, 1.0f);
   Tensor x({1, N, C}, 0.0f, Device::CPU);
@@ -162,20 +164,27 @@ int bench(int N, int C, int H, int E, int k, int reps) {
   MoELayer layer(C, H, E, k);
   for (Tensor* p : layer.get_parameters())
     for (auto& v : p->data) v = 0.02f * nd(gen);
-  Tensor y;
-  layer.forward_into(x, y);  // warmup
+  Tensor y, dx;
+  Tensor dy({1, N, C}, 0.0f, Device::CPU);
+  for (auto& v : dy.data) v = nd(gen);
+  auto step = [&]() {
+    layer.forward_into(x, y);
+    if (train) layer.backward_into(dy, dx);
+  };
+  step();  // warmup
   std::vector<double> t;
   for (int r = 0; r < reps; ++r) {
     auto t0 = std::chrono::steady_clock::now();
-    layer.forward_into(x, y);
+    step();
     auto t1 = std::chrono::steady_clock::now();
     t.push_back(std::chrono::duration<double>(t1 - t0).count());
   }
   std::vector<double> s = t;
   std::sort(s.begin(), s.end());
   double med = s[s.size() / 2];
-  std::printf("{\"N\": %d, \"C\": %d, \"H\": %d, \"E\": %d, \"k\": %d, \"reps\": %d, "
-              "\"median_s\": %.6f, \"runs_s\": [", N, C, H, E, k, reps, med);
+  std::printf("{\"pass\": \"%s\", \"N\": %d, \"C\": %d, \"H\": %d, \"E\": %d, \"k\": %d, "
+              "\"reps\": %d, \"median_s\": %.6f, \"runs_s\": [",
+              train ? "forward+backward" : "forward", N, C, H, E, k, reps, med);
   for (size_t i = 0; i < t.size(); ++i) std::printf("%s%.6f", i ? ", " : "", t[i]);
   std::printf("], \"tokens_per_s\": %.3f, \"threads\": 1}\n", N / med);
   return 0;
@@ -186,9 +195,11 @@ int bench(int N, int C, int H, int E, int k, int reps) {
 int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
   if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
-  if (argc == 8 && std::string(argv[1]) == "bench")
+  if (argc == 8 && (std::string(argv[1]) == "bench" || std::string(argv[1]) == "bench_train"))
     return bench(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]),
-                 std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]));
-  std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | bench N C H E k reps\n");
+                 std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]),
+                 std::string(argv[1]) == "bench_train");
+  std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | "
+                       "bench[_train] N C H E k reps\n");
   return 1;
 }
