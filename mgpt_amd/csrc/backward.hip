@@ -4,11 +4,11 @@
 // branches of the tensor ops it calls (utils/Tensor.cpp):
 //   scatter_bwd   moe_scatter_backward :1410-1438: per slot,
 //                 dgo[slot] = dy[t] * p and dp[t*k+j] = <y_e[slot], dy[t]>
-//   token_bwd     scatter_indices_into :1462-1484 + the load-balance term
+//   token_dl      scatter_indices_into :1462-1484 + the load-balance term
 //                 (layers/MoELayer.cpp:193-200) + softmax_backward :885-905
-//                 on the clamped probabilities, then per token
-//                 dx = sum over its slots (ascending) of dX_e (the gather
-//                 backward :1440-1460) + dL . W_r^T (router
+//                 on the clamped probabilities
+//   token_dx      per token dx = sum over its slots (ascending) of dX_e (the
+//                 gather backward :1440-1460) + dL . W_r^T (router
 //                 LinearLayer::backward_into, layers/LinearLayer.cpp:33-80)
 //   router_wgrad  dW_r += x^T . dL, db_r += sum_t dL (same Linear backward):
 //                 per-chunk partial sums, then an in-order reduction, so the
@@ -88,52 +88,63 @@ __global__ __launch_bounds__(256) void scatter_bwd_kernel(
   if (lane == 0) dtp[flat] = dot;
 }
 
-constexpr int kTokBlock = 16;   // tokens per token_bwd block
-
-// dL and dx of kTokBlock tokens.  Phase 1 (one thread per token): dP from
-// the top-k entries and the load-balance term, s = sum_e dP*P in expert
-// order, dL = P*(dP - s), the token's slots sorted ascending.  Phase 2 (a
-// thread per 4 columns): the slot rows of dX_e summed in slot order, plus
-// dL . W_r^T with W_r read from the router's packed [G][C][RE] layout.
-template <typename ActT>
-__global__ __launch_bounds__(256) void token_bwd_kernel(
-    const ActT* __restrict__ dxe, const int32_t* __restrict__ slot_of,
-    const int32_t* __restrict__ topk_idx, const float* __restrict__ dtp,
-    const float* __restrict__ probs, const int32_t* __restrict__ counts,
-    const float* __restrict__ wr_g, int RE, int N, int C, int E, int k,
-    ActT* __restrict__ dx, float* __restrict__ dL) {
-  __shared__ float s_dl[kTokBlock][kMaxExperts];
-  __shared__ float s_lb[kMaxExperts];
-  __shared__ int s_slot[kTokBlock][kMaxTopK];
-  const int tid = threadIdx.x;
-  const int t0 = blockIdx.x * kTokBlock;
-  if (tid < E) {
-    // (alpha * E * f_e) / N with f_e = counts_e / N, alpha = 0.01
-    const float fe = (float)counts[tid] / (float)N;
-    s_lb[tid] = (0.01f * (float)E * fe) / (float)N;
+// dL of every token: a group of EP lanes per token (EP a power of two >= E,
+// <= 64, so a group never straddles a wave), lane e holding expert e:
+// dP = the top-k entry (dp of that choice, else 0) + the load-balance term
+// (alpha * E * f_e) / N with f_e = counts_e / N, alpha = 0.01;
+// s = sum_e dP*P (a fixed-order shuffle tree); dL = P*(dP - s).
+template <int EP>
+__global__ __launch_bounds__(256) void token_dl_kernel(const int32_t* __restrict__ topk_idx,
+                                                       const float* __restrict__ dtp,
+                                                       const float* __restrict__ probs,
+                                                       const int32_t* __restrict__ counts, int N,
+                                                       int E, int k, float* __restrict__ dL) {
+  const int gid = blockIdx.x * (256 / EP) + (int)threadIdx.x / EP;
+  const int e = threadIdx.x % EP;
+  const bool tok = gid < N;
+  const bool live = tok && e < E;
+  float dp = 0.0f, p = 0.0f;
+  if (live) {
+    const float fe = (float)counts[e] / (float)N;
+    const float lb = (0.01f * (float)E * fe) / (float)N;
+    float sel = 0.0f;
+    for (int j = 0; j < k; ++j)
+      if (topk_idx[(size_t)gid * k + j] == e) sel = dtp[(size_t)gid * k + j];
+    dp = sel + lb;
+    p = probs[(size_t)gid * E + e];
   }
-  __syncthreads();
-  if (tid < kTokBlock && t0 + tid < N) {
-    const int t = t0 + tid;
-    float* d = s_dl[tid];
-    for (int e = 0; e < E; ++e) d[e] = 0.0f;
-    int* sl = s_slot[tid];
-    for (int j = 0; j < k; ++j) {
-      d[topk_idx[(size_t)t * k + j]] = dtp[(size_t)t * k + j];
-      sl[j] = slot_of[(size_t)t * k + j];
-    }
-    const float* P = probs + (size_t)t * E;
-    float s = 0.0f;
-    for (int e = 0; e < E; ++e) {
-      d[e] = d[e] + s_lb[e];
-      s += d[e] * P[e];
-    }
-    for (int e = 0; e < E; ++e) {
-      const float v = P[e] * (d[e] - s);
-      d[e] = v;
-      dL[(size_t)t * E + e] = v;
-    }
-    for (int a = 1; a < k; ++a) {   // insertion sort of the slots (in LDS)
+  float sum = dp * p;
+#pragma unroll
+  for (int m = 1; m < EP; m <<= 1) sum += __shfl_xor(sum, m, kWave);
+  if (live) dL[(size_t)gid * E + e] = p * (dp - sum);
+}
+
+constexpr int kDxTokens = 8;   // tokens per token_dx wave
+
+// dx of kDxTokens tokens x 512 columns per wave (8 columns per lane):
+// the sum of the tokens' slot rows of dX_e in ascending slot order (the
+// gather backward) plus dL . W_r^T (wrt = W_r as [E][C]; experts in
+// ascending order, 4 experts' weights loaded at a time).
+template <typename ActT>
+__global__ __launch_bounds__(64) void token_dx_kernel(const ActT* __restrict__ dxe,
+                                                      const int32_t* __restrict__ slot_of,
+                                                      const float* __restrict__ dL,
+                                                      const float* __restrict__ wrt, int N, int C,
+                                                      int E, int k, ActT* __restrict__ dx) {
+  using V = Vec<ActT>;
+  __shared__ float s_dl[kDxTokens][kMaxExperts];
+  __shared__ int s_slot[kDxTokens][kMaxTopK];
+  const int lane = lane_id();
+  const int t0 = blockIdx.x * kDxTokens;
+  const int nt = min(kDxTokens, N - t0);
+  for (int p = lane; p < kDxTokens * kMaxExperts; p += kWave) {
+    const int r = p / kMaxExperts, e = p % kMaxExperts;
+    s_dl[r][e] = (r < nt && e < E) ? dL[(size_t)(t0 + r) * E + e] : 0.0f;
+  }
+  if (lane < nt) {
+    int* sl = s_slot[lane];
+    for (int j = 0; j < k; ++j) sl[j] = slot_of[(size_t)(t0 + lane) * k + j];
+    for (int a = 1; a < k; ++a) {   // insertion sort: ascending slots
       const int v = sl[a];
       int b = a;
       while (b > 0 && sl[b - 1] > v) {
@@ -144,45 +155,64 @@ __global__ __launch_bounds__(256) void token_bwd_kernel(
     }
   }
   __syncthreads();
-  const int nt = min(kTokBlock, N - t0);
-  for (int cq = tid; cq < C / 4; cq += blockDim.x) {
-    const int c = 4 * cq;
-    float acc[kTokBlock][4];
+  const int c0 = blockIdx.y * 512 + lane * 8;
+  if (c0 >= C) return;
+  float acc[kDxTokens][8];
 #pragma unroll
-    for (int r = 0; r < kTokBlock; ++r)
+  for (int r = 0; r < kDxTokens; ++r)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc[r][q] = 0.0f;
-    // router term, experts in ascending order
-    for (int e = 0; e < E; ++e) {
-      const float* wp = wr_g + ((size_t)(e / RE) * C + c) * RE + (e % RE);
-      const float w0 = wp[0], w1 = wp[RE], w2 = wp[2 * RE], w3 = wp[3 * RE];
+    for (int q = 0; q < 8; ++q) acc[r][q] = 0.0f;
+  for (int e0 = 0; e0 < E; e0 += 4) {
+    float w[4][8];
 #pragma unroll
-      for (int r = 0; r < kTokBlock; ++r) {
-        const float g = s_dl[r][e];
-        acc[r][0] += g * w0;
-        acc[r][1] += g * w1;
-        acc[r][2] += g * w2;
-        acc[r][3] += g * w3;
+    for (int u = 0; u < 4; ++u) {
+      if (e0 + u < E) {
+        const float4 a = *reinterpret_cast<const float4*>(wrt + (size_t)(e0 + u) * C + c0);
+        const float4 b = *reinterpret_cast<const float4*>(wrt + (size_t)(e0 + u) * C + c0 + 4);
+        w[u][0] = a.x; w[u][1] = a.y; w[u][2] = a.z; w[u][3] = a.w;
+        w[u][4] = b.x; w[u][5] = b.y; w[u][6] = b.z; w[u][7] = b.w;
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) w[u][q] = 0.0f;
       }
     }
 #pragma unroll
-    for (int r = 0; r < kTokBlock; ++r) {
-      if (r < nt) {
-        float gsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int j = 0; j < k; ++j) {
-          const ActT* src = dxe + (size_t)s_slot[r][j] * C + c;
+    for (int r = 0; r < kDxTokens; ++r)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) gsum[q] += to_f32(src[q]);
-        }
-        ActT* o = dx + (size_t)(t0 + r) * C + c;
+      for (int u = 0; u < 4; ++u) {
+        const float g = s_dl[r][e0 + u];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) store_act(o + q, gsum[q] + acc[r][q]);
+        for (int q = 0; q < 8; ++q) acc[r][q] += g * w[u][q];
       }
+  }
+#pragma unroll
+  for (int r = 0; r < kDxTokens; ++r) {
+    if (r >= nt) break;
+    float gs[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) gs[q] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      const ActT* src = dxe + (size_t)s_slot[r][j] * C + c0;
+#pragma unroll
+      for (int h = 0; h < 8 / V::N; ++h) {
+        float v[V::N];
+        V::unpack(*reinterpret_cast<const uint4*>(src + h * V::N), v);
+#pragma unroll
+        for (int q = 0; q < V::N; ++q) gs[h * V::N + q] += v[q];
+      }
+    }
+    ActT* o = dx + (size_t)(t0 + r) * C + c0;
+#pragma unroll
+    for (int h = 0; h < 8 / V::N; ++h) {
+      float v[V::N];
+#pragma unroll
+      for (int q = 0; q < V::N; ++q) v[q] = gs[h * V::N + q] + acc[r][h * V::N + q];
+      *reinterpret_cast<uint4*>(o + h * V::N) = V::pack(v);
     }
   }
 }
 
-constexpr int kRwChunk = 256;   // tokens per router_wgrad partial
+constexpr int kRwChunk = 64;    // tokens per router_wgrad partial
 
 // partial[chunk][c][e] = sum over the chunk's tokens of x[t][c] * dL[t][e]
 // (a thread per column, EP >= E experts in registers, dL rows read from LDS
@@ -215,15 +245,22 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
     if (blockIdx.x == 0 && tid < E)
       for (int r = 0; r < nt; ++r) bsum += sl[r * EP + tid];
     if (c < C) {
-      for (int r = 0; r < nt; ++r) {
-        const float xv = to_f32(x[(size_t)(tb + r) * C + c]);
+      // 16 tokens' loads in flight at a time (rows past nt are zero in s_dl)
+      for (int r0 = 0; r0 < nt; r0 += 16) {
+        float xv[16];
 #pragma unroll
-        for (int e4 = 0; e4 < EP / 4; ++e4) {
-          const float4 d = s_dl[r][e4];
-          acc[4 * e4 + 0] += xv * d.x;
-          acc[4 * e4 + 1] += xv * d.y;
-          acc[4 * e4 + 2] += xv * d.z;
-          acc[4 * e4 + 3] += xv * d.w;
+        for (int u = 0; u < 16; ++u)
+          xv[u] = r0 + u < nt ? to_f32(x[(size_t)(tb + r0 + u) * C + c]) : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+#pragma unroll
+          for (int e4 = 0; e4 < EP / 4; ++e4) {
+            const float4 d = s_dl[r0 + u][e4];
+            acc[4 * e4 + 0] += xv[u] * d.x;
+            acc[4 * e4 + 1] += xv[u] * d.y;
+            acc[4 * e4 + 2] += xv[u] * d.z;
+            acc[4 * e4 + 3] += xv[u] * d.w;
+          }
         }
       }
     }
@@ -237,21 +274,41 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
   if (blockIdx.x == 0 && tid < E) partial_b[(size_t)chunk * E + tid] = bsum;
 }
 
-// grad[i] += sum over chunks (in order) of partial[chunk][i], for the C*E
-// weight entries followed by the E bias entries.
+// grad[i] += sum over chunks of partial[chunk][i], for the C*E weight
+// entries followed by the E bias entries, as a fixed two-level tree (so the
+// result does not depend on scheduling): a block takes 16 entries; thread
+// (entry, g) adds the g-th of 16 consecutive chunk ranges in order, then
+// one thread per entry adds the 16 range sums in order.
 __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(
     const float* __restrict__ partial, const float* __restrict__ partial_b, int chunks, int CE,
     int E, float* __restrict__ gW, float* __restrict__ gb) {
-  const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < CE) {
-    float s = 0.0f;
-    for (int ch = 0; ch < chunks; ++ch) s += partial[(size_t)ch * CE + i];
-    gW[i] = gW[i] + s;
-  } else if (i < CE + E) {
-    const int e = i - CE;
-    float s = 0.0f;
-    for (int ch = 0; ch < chunks; ++ch) s += partial_b[(size_t)ch * E + e];
-    gb[e] = gb[e] + s;
+  __shared__ float s_part[16][16];
+  const int el = threadIdx.x % 16, g = threadIdx.x / 16;
+  const int i = blockIdx.x * 16 + el;
+  const bool live = i < CE + E;
+  const bool w = i < CE;
+  const float* src = w ? partial + i : partial_b + (i - CE);
+  const size_t stride = w ? (size_t)CE : (size_t)E;
+  const int per = (chunks + 15) / 16;
+  const int ch0 = g * per, ch1 = min(chunks, ch0 + per);
+  float s = 0.0f;
+  for (int c0 = ch0; c0 < ch1; c0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      v[u] = (live && c0 + u < ch1) ? src[(size_t)(c0 + u) * stride] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+      if (c0 + u < ch1) s += v[u];
+  }
+  s_part[g][el] = s;
+  __syncthreads();
+  if (g == 0 && live) {
+    float t = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) t += s_part[q][el];
+    float* o = w ? gW + i : gb + (i - CE);
+    *o = *o + t;
   }
 }
 
@@ -296,13 +353,21 @@ hipError_t launch_scatter_bwd(const ActT* dy, const ActT* ye, const int32_t* per
 template <typename ActT>
 hipError_t launch_token_bwd(const ActT* dxe, const int32_t* slot_of, const int32_t* topk_idx,
                             const float* dtp, const float* probs, const int32_t* counts,
-                            const float* wr_g, int RE, int N, int C, int E, int k, ActT* dx,
-                            float* dL, hipStream_t stream) {
+                            const float* wrt, int N, int C, int E, int k, ActT* dx, float* dL,
+                            hipStream_t stream) {
   if (N <= 0) return hipSuccess;
-  if (C % 4 || E > kMaxExperts || k > kMaxTopK) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(token_bwd_kernel<ActT>, dim3((N + kTokBlock - 1) / kTokBlock), dim3(256), 0,
-                     stream, dxe, slot_of, topk_idx, dtp, probs, counts, wr_g, RE, N, C, E, k, dx,
-                     dL);
+  if (E > kMaxExperts || k > kMaxTopK || C % 8) return hipErrorInvalidValue;
+  if (E <= 16)
+    hipLaunchKernelGGL(token_dl_kernel<16>, dim3((N + 15) / 16), dim3(256), 0, stream, topk_idx,
+                       dtp, probs, counts, N, E, k, dL);
+  else if (E <= 32)
+    hipLaunchKernelGGL(token_dl_kernel<32>, dim3((N + 7) / 8), dim3(256), 0, stream, topk_idx,
+                       dtp, probs, counts, N, E, k, dL);
+  else
+    hipLaunchKernelGGL(token_dl_kernel<64>, dim3((N + 3) / 4), dim3(256), 0, stream, topk_idx,
+                       dtp, probs, counts, N, E, k, dL);
+  hipLaunchKernelGGL(token_dx_kernel<ActT>, dim3((N + kDxTokens - 1) / kDxTokens, (C + 511) / 512),
+                     dim3(64), 0, stream, dxe, slot_of, dL, wrt, N, C, E, k, dx);
   return hipGetLastError();
 }
 
@@ -325,7 +390,7 @@ hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int
     hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64>), grid, dim3(256), 0, stream, x, dL, N, C,
                        E, partial, partial_b);
   const int CE = C * E;
-  hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 255) / 256), dim3(256), 0, stream,
+  hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 15) / 16), dim3(256), 0, stream,
                      partial, partial_b, chunks, CE, E, gW, gb);
   return hipGetLastError();
 }
@@ -345,7 +410,7 @@ hipError_t launch_transpose_pad(const T* src, int src_rows, int src_cols, size_t
                                             int, int, int, T*, float*, hipStream_t);           \
   template hipError_t launch_token_bwd<T>(const T*, const int32_t*, const int32_t*,            \
                                           const float*, const float*, const int32_t*,          \
-                                          const float*, int, int, int, int, int, T*, float*,   \
+                                          const float*, int, int, int, int, T*, float*,        \
                                           hipStream_t);                                        \
   template hipError_t launch_router_wgrad<T>(const T*, const float*, int, int, int, float*,    \
                                              float*, float*, float*, hipStream_t);             \

@@ -62,8 +62,8 @@ hipError_t launch_scatter_bwd(const ActT*, const ActT*, const int32_t*, const fl
                               int, ActT*, float*, hipStream_t);
 template <typename ActT>
 hipError_t launch_token_bwd(const ActT*, const int32_t*, const int32_t*, const float*,
-                            const float*, const int32_t*, const float*, int, int, int, int, int,
-                            ActT*, float*, hipStream_t);
+                            const float*, const int32_t*, const float*, int, int, int, int, ActT*,
+                            float*, hipStream_t);
 int router_wgrad_chunks(int N);
 template <typename ActT>
 hipError_t launch_router_wgrad(const ActT*, const float*, int, int, int, float*, float*, float*,
@@ -147,6 +147,7 @@ struct mgpt_moe {
   int Hq = 0;
   void* wdb = nullptr;
   void* wgub = nullptr;
+  float* wrt = nullptr;    // W_r as [E][C] (fp32)
   bool bwd_ready = false;
   float* grad = nullptr;   // gWr [C][E], gbr [E], gWg [E][C][H], gbg [E][H],
                            // gWu [E][C][H], gbu [E][H], gWd [E][H][C], gbd [E][C]
@@ -205,7 +206,7 @@ struct mgpt_moe {
       L.dgo = take((A + kRowPad) * C * act_bytes());
       L.dtp = take(A * 4);
       L.dlog = take((size_t)N * E * 4);
-      const size_t chunks = (size_t)(N + 255) / 256;
+      const size_t chunks = (size_t)router_wgrad_chunks(N);
       L.rw_part = take(chunks * C * E * 4);
       L.rw_part_b = take(chunks * E * 4);
     }
@@ -240,11 +241,11 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_g, h->wr1, h->br, h->wgu, h->wd, h->sgu, h->sd,
-                  h->bg,   h->bu,  h->bd, h->wdb, h->wgub};
+  void* ptrs[] = {h->wr_g, h->wr1, h->br,  h->wgu,  h->wd, h->sgu, h->sd,
+                  h->bg,   h->bu,  h->bd,  h->wdb, h->wgub, h->wrt};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  h->wr_g = h->wr1 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = nullptr;
+  h->wr_g = h->wr1 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = h->wrt = nullptr;
   h->wgu = h->wd = h->wdb = h->wgub = nullptr;
   h->loaded = false;
   h->bwd_ready = false;
@@ -278,6 +279,12 @@ int ensure_bwd_weights(mgpt_moe* h, hipStream_t st) {
   const size_t eb = h->act_bytes();
   if (!h->wdb) HIP_TRY(hipMalloc(&h->wdb, eb * E * h->Hq * C));
   if (!h->wgub) HIP_TRY(hipMalloc(&h->wgub, eb * E * Cp * 2 * Hp));
+  // W_r [E][C] from the router pack [G][C][RE]: per group a [C][RE] -> [RE][C]
+  // transpose (E is padded to G*RE there; the padding experts are never read)
+  const int RE = router_experts_per_wave(E), G = (E + RE - 1) / RE;
+  if (!h->wrt) HIP_TRY(hipMalloc(&h->wrt, sizeof(float) * (size_t)G * RE * C));
+  HIP_TRY(launch_transpose_pad<float>(h->wr_g, C, RE, (size_t)C * RE, h->wrt, RE, C,
+                                      (size_t)RE * C, G, st));
   if (h->act == MGPT_DTYPE_BF16) {
     HIP_TRY(launch_transpose_pad<bf16_t>((const bf16_t*)h->wd, Cp, Hp, (size_t)Cp * Hp,
                                          (bf16_t*)h->wdb, h->Hq, C, (size_t)h->Hq * C, E, st));
@@ -682,8 +689,8 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
                                  g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
                                  g + h->g_off[5], (size_t)H, st)));
   HIP_TRY(mark(5));
-  HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wr_g,
-                                 router_experts_per_wave(E), N, C, E, k, dx, dlog, st));
+  HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wrt, N, C, E, k, dx,
+                                 dlog, st));
   HIP_TRY(mark(6));
   HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
                                     (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
