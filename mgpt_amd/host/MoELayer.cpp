@@ -6,7 +6,9 @@
 //    [W_g, b_g, W_u, b_u, W_d, b_d]), which the library's
 //    mgpt_moe_load_parameters takes verbatim;
 //  * forward_into :28-128: input [B,T,C], output allocated on the input's
-//    device when empty, every element written;
+//    device when empty, every element written, the backward's caches kept;
+//  * backward_into :130-223: din [B,T,C] for dout of the last forward, and
+//    every parameter's gradient added to its Tensor::grad (add_grad);
 //  * get_expert_counts (MoELayer.h:39): float counts of the last forward.
 // The engine's tensors are fp32, so the handle is configured fp32/fp32 (the
 // path that matches the reference within 1e-5 with bit-exact routing).
@@ -117,8 +119,10 @@ void MoELayer::forward_into(const Tensor& input, Tensor& output) {
   mgpt_moe* h = get_handle();
   ensure_packed();
 
+  // The training forward: like the engine's layer, every forward keeps what
+  // a following backward needs.
   size_t ws_bytes = 0;
-  check(mgpt_moe_workspace_bytes(h, N, &ws_bytes), "workspace_bytes");
+  check(mgpt_moe_train_workspace_bytes(h, N, &ws_bytes), "train_workspace_bytes");
   void* ws;
   if (scratchpad && on_dev)
     ws = scratchpad->get_address((ws_bytes + sizeof(float) - 1) / sizeof(float));
@@ -129,21 +133,28 @@ void MoELayer::forward_into(const Tensor& input, Tensor& output) {
   if (output.size() != (size_t)N * C || output.device != input.device)
     throw std::invalid_argument("MoELayer: output must be [B, T, embed_dim] on the input's device");
 
+  // x is kept on the device for the backward (the engine's layers cache
+  // their inputs the same way): a device copy of a device input, the staged
+  // copy of a host input.
   const size_t io_bytes = (size_t)N * C * sizeof(float);
+  void* xs = device_buffer(saved_x, saved_x_bytes, io_bytes);
   if (on_dev) {
-    check(mgpt_moe_forward(h, input.get_data_ptr(), output.get_data_ptr(), N, ws, ws_bytes,
-                           nullptr),
+    if (N > 0)
+      check_hip(hipMemcpy(xs, input.get_data_ptr(), io_bytes, hipMemcpyDeviceToDevice), "copy x");
+    check(mgpt_moe_forward_train(h, xs, output.get_data_ptr(), N, ws, ws_bytes, nullptr),
           "forward");
   } else {
     // Host tensors: stage x and y through device memory (default stream,
     // synchronous copies, as the engine's own host<->device copies).
-    char* st = (char*)device_buffer(staging, staging_bytes, 2 * io_bytes + 512);
-    void* dx = st;
-    void* dy = st + ((io_bytes + 255) / 256) * 256;
-    if (N > 0) check_hip(hipMemcpy(dx, input.get_data_ptr(), io_bytes, hipMemcpyHostToDevice), "copy x");
-    check(mgpt_moe_forward(h, dx, dy, N, ws, ws_bytes, nullptr), "forward");
+    void* dy = device_buffer(staging, staging_bytes, io_bytes);
+    if (N > 0) check_hip(hipMemcpy(xs, input.get_data_ptr(), io_bytes, hipMemcpyHostToDevice), "copy x");
+    check(mgpt_moe_forward_train(h, xs, dy, N, ws, ws_bytes, nullptr), "forward");
     if (N > 0) check_hip(hipMemcpy(output.get_data_ptr(), dy, io_bytes, hipMemcpyDeviceToHost), "copy y");
   }
+  last_ws = ws;
+  last_ws_bytes = ws_bytes;
+  last_B = B;
+  last_T = T;
   counts_valid = false;
 }
 
@@ -153,8 +164,47 @@ Tensor MoELayer::backward(const Tensor& dout) {
   return din;
 }
 
-void MoELayer::backward_into(const Tensor&, Tensor&) {
-  throw std::runtime_error("MoELayer: backward is not provided by the MI355X forward path");
+void MoELayer::backward_into(const Tensor& dout, Tensor& din) {
+  if (!last_ws) throw std::runtime_error("MoELayer: backward before forward");
+  if (dout.shape != std::vector<int>({last_B, last_T, embed_dim}))
+    throw std::invalid_argument("MoELayer: dout must have the last forward's [B, T, embed_dim]");
+  const int N = last_B * last_T, C = embed_dim;
+  const bool on_dev = dout.device == Device::CUDA;
+  mgpt_moe* h = get_handle();
+  if (din.shape.empty() || din.size() != (size_t)N * C || din.device != dout.device)
+    din = Tensor({last_B, last_T, C}, 0.0f, dout.device);
+  din.shape = {last_B, last_T, C};
+
+  // The handle's gradient buffers hold this call's gradients only; they are
+  // then added to the parameters' grads.
+  check(mgpt_moe_zero_grad(h, nullptr), "zero_grad");
+  const size_t io_bytes = (size_t)N * C * sizeof(float);
+  if (on_dev) {
+    check(mgpt_moe_backward(h, saved_x.get(), dout.get_data_ptr(), din.get_data_ptr(), N, last_ws,
+                            last_ws_bytes, nullptr),
+          "backward");
+  } else {
+    char* st = (char*)device_buffer(bwd_staging, bwd_staging_bytes, 2 * io_bytes + 512);
+    void* ddy = st;
+    void* ddx = st + ((io_bytes + 255) / 256) * 256;
+    if (N > 0) check_hip(hipMemcpy(ddy, dout.get_data_ptr(), io_bytes, hipMemcpyHostToDevice), "copy dy");
+    check(mgpt_moe_backward(h, saved_x.get(), ddy, ddx, N, last_ws, last_ws_bytes, nullptr),
+          "backward");
+    if (N > 0) check_hip(hipMemcpy(din.get_data_ptr(), ddx, io_bytes, hipMemcpyDeviceToHost), "copy dx");
+  }
+
+  std::vector<Tensor*> params = get_parameters();
+  std::vector<Tensor> grads;
+  grads.reserve(params.size());
+  std::vector<float*> ptrs;
+  for (Tensor* p : params) {
+    grads.emplace_back(p->shape, 0.0f, p->device);
+    ptrs.push_back(grads.back().get_data_ptr());
+  }
+  check(mgpt_moe_get_gradients(h, ptrs.data(), (int)ptrs.size(),
+                               params.front()->device == Device::CUDA ? 1 : 0, nullptr),
+        "get_gradients");
+  for (size_t i = 0; i < params.size(); ++i) params[i]->add_grad(grads[i]);
 }
 
 std::vector<Tensor*> MoELayer::get_parameters() {
@@ -168,9 +218,10 @@ std::vector<Tensor*> MoELayer::get_parameters() {
 
 ScratchpadFootprint MoELayer::get_footprint(int B, int T) {
   size_t bytes = 0;
-  check(mgpt_moe_workspace_bytes(get_handle(), B * T, &bytes), "workspace_bytes");
-  // The workspace stays standing after forward (routing state), as the
-  // engine's routing buffers do; no per-expert temporaries.
+  check(mgpt_moe_train_workspace_bytes(get_handle(), B * T, &bytes), "train_workspace_bytes");
+  // The workspace stays standing after forward (routing state and the
+  // backward's caches), as the engine's cached tensors do; the backward
+  // works inside it.
   return {(bytes + sizeof(float) - 1) / sizeof(float), 0, 0};
 }
 

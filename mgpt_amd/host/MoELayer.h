@@ -9,14 +9,17 @@
 // experts, initialised and ordered exactly as before) and are packed into
 // the library's layouts on first use, after to(), or after refresh_weights().
 //
+// backward_into runs the library's backward on the caches the forward kept
+// and adds every parameter's gradient with the engine's own
+// Tensor::add_grad, as the engine's layer does through its Linear layers.
+//
 // Differences from the engine's layer, all deliberate:
-//  * forward only: backward()/backward_into() throw std::runtime_error (the
-//    MoE backward is not part of this path);
 //  * errors throw std::runtime_error with the library's message instead of
 //    exiting the process;
-//  * get_footprint() reports the library's workspace (routing buffers and
-//    the three activation buffers), taken from the Scratchpad when one is
-//    set and the input is on the device.
+//  * get_footprint() reports the library's training workspace (routing,
+//    gathered rows, activations, the backward's caches) as standing memory,
+//    taken from the Scratchpad when one is set and the input is on the
+//    device.
 #ifndef MGPT_AMD_MOELAYER_H
 #define MGPT_AMD_MOELAYER_H
 
@@ -45,6 +48,13 @@ class MoELayer : public Layer {
   size_t owned_workspace_bytes = 0;
   std::unique_ptr<void, DeviceDeleter> staging;           // x and y of host tensors
   size_t staging_bytes = 0;
+  std::unique_ptr<void, DeviceDeleter> saved_x;           // the forward's input (device)
+  size_t saved_x_bytes = 0;
+  std::unique_ptr<void, DeviceDeleter> bwd_staging;       // dy and dx of host tensors
+  size_t bwd_staging_bytes = 0;
+  void* last_ws = nullptr;                                // workspace of the last forward
+  size_t last_ws_bytes = 0;
+  int last_B = 0, last_T = 0;
   bool packed = false;
 
   Tensor cached_out;

@@ -5,9 +5,10 @@ Tensor.h, LinearLayer.h, SwiGLU.h under /root/reference) and keeps the
 engine's public MoELayer interface (layers/MoELayer.h:36-51).
 GPU: tests/engine/_build/dropin_main -- the engine's unmodified Tensor,
 LinearLayer and SwiGLU sources with the drop-in in place of MoELayer.cpp --
-runs the engine's MoE shape test and full forwards whose outputs are
-compared with the oracle (fp32: 1e-5) and whose expert counts must equal the
-reference fixture's.
+runs the engine's MoE shape and backward test, full forwards whose outputs
+are compared with the oracle (fp32: 1e-5) and whose expert counts must equal
+the reference fixture's, and full backwards whose din and parameter
+gradients are compared with the oracle's backward (fp32: 1e-5).
 """
 import os
 import re
@@ -86,3 +87,46 @@ def test_engine_forward_matches_reference(name):
     mx = np.abs(y - ref).max() / np.abs(ref).max()
     print(f"{name}: normwise {rel:.3e} max/max {mx:.3e}")
     assert rel <= 1e-5 and mx <= 1e-5
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.exists(BIN), reason="engine test binary not built")
+@pytest.mark.parametrize("name", ["small_f32", "ragged_k3", "cfg1"])
+def test_engine_backward_matches_reference(name):
+    """The drop-in's backward_into inside the engine: din and every
+    parameter's Tensor::grad (added with the engine's own add_grad) against
+    the oracle backward, which matches the reference's bit for bit; fp32
+    handle, tolerance 1e-5 normwise and elementwise per tensor."""
+    case = C.ALL_CASES[name]
+    inp = C.build_inputs(case)
+    dy = C.build_dy(case)
+    with tempfile.TemporaryDirectory() as d:
+        ip, dp, op = (os.path.join(d, n) for n in ("in.bin", "dy.bin", "grad.bin"))
+        write_input(ip, inp)
+        np.ascontiguousarray(dy, np.float32).tofile(dp)
+        r = _run(["backward", ip, dp, op])
+        assert r.returncode == 0, r.stdout + r.stderr
+        raw = open(op, "rb").read()
+    assert raw[:8] == b"MGPTGRD1"
+    cfg = inp.cfg
+    N, Cc, H, E = cfg.N, cfg.C, cfg.H, cfg.E
+    off = 28
+    got = []
+    for n in [N * Cc, Cc * E, E] + [Cc * H, H, Cc * H, H, H * Cc, Cc] * E:
+        got.append(np.frombuffer(raw, np.float32, n, off))
+        off += 4 * n
+    assert off == len(raw)
+    ref = O.backward(inp, dy)
+    want = [ref["dx"], ref["dWr"], ref["dbr"]]
+    for e in range(E):
+        want += [ref["dWg"][e], ref["dbg"][e], ref["dWu"][e], ref["dbu"][e], ref["dWd"][e],
+                 ref["dbd"][e]]
+    worst = 0.0
+    for g, w in zip(got, want):
+        w = np.asarray(w, np.float64).reshape(-1)
+        dd = g.astype(np.float64) - w
+        scale = max(np.abs(w).max(), 1e-30)
+        rel = np.linalg.norm(dd) / max(np.linalg.norm(w), 1e-30)
+        worst = max(worst, rel, np.abs(dd).max() / scale)
+    print(f"{name}: worst per-tensor error {worst:.3e}")
+    assert worst <= 1e-5
