@@ -41,8 +41,19 @@ CALIB_MIB = 512               # known-size elementwise copy for counter calibrat
 
 
 def stage_of(kernel_name: str):
-    """Forward stage of a kernel in a rocprofv3 trace (None: not a forward kernel)."""
+    """Stage of a kernel in a rocprofv3 trace (None: not a forward or
+    backward kernel).  The down GEMM kernel also runs the backward's dX
+    product in a training pass; the per-stage HIP-event times separate them."""
     short = kernel_name.replace("(anonymous namespace)", "").split("(")[0]
+    if "scatter_bwd_kernel" in short:
+        return "scatter_bwd"
+    if re.search(r"token_d[lx]_kernel", short):
+        return "token_bwd"
+    if "router_wgrad" in short:
+        return "router_wgrad"
+    m = re.search(r"wgrad(?:_tr)?_kernel<(?:[^,>]*, )?(\d)>", short)
+    if m:
+        return ("wgrad_down", "wgrad_gateup")[int(m.group(1))]
     if re.search(r"router_(?:topk|logits|softmax)", short):
         return "router_topk"
     if "permute_kernel" in short:
@@ -51,11 +62,11 @@ def stage_of(kernel_name: str):
         return "combine"
     m = re.search(r"gemm_(?:dma|ring5|decode|split_reduce)_kernel<(\d)[,>]", short)
     if m:
-        return ("gemm_gateup", "gemm_down")[int(m.group(1))]
+        return ("gemm_gateup", "gemm_down", "gemm_dact_swiglu_bwd")[int(m.group(1))]
     m = re.search(r"grouped_gemm_kernel<([^>]*)>", short)
     if m:
         epi = int(m.group(1).split(",")[6])
-        return ("gemm_gateup", "gemm_down")[epi]
+        return ("gemm_gateup", "gemm_down", "gemm_dact_swiglu_bwd")[epi]
     if "MulFunctor" in kernel_name:
         return "calib_copy"
     return None
@@ -146,15 +157,19 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
     with open(bench_json) as f:
         b = json.loads(f.read().strip().splitlines()[-1])
     rows = list(csv.DictReader(open(stats_csv)))
+    train = str(b.get("pass", "")).startswith("train")
+    extra = " --pass train" if train else ""
     cmd = (f"rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python bench.py "
-           f"--config {config} --steps {b['steps']} --warmup {b['warmup']} --no-cpu-baseline")
-    out = [f"# {config} MoE forward: rocprofv3 kernel statistics (MI355X)", "",
+           f"--config {config}{extra} --steps {b['steps']} --warmup {b['warmup']} --no-cpu-baseline")
+    what = "training step (forward + backward)" if train else "forward"
+    unit = "training steps" if train else "forwards"
+    out = [f"# {config} MoE {what}: rocprofv3 kernel statistics (MI355X)", "",
            "Command (repository root, on the GPU box), then "
            "`python bench.py --config %s --summarize-stats <dir>/run_kernel_stats.csv <json line>`:"
            % config, "", "```", cmd, "```", "",
-           f"Workload: {b['config']['workload']}.  {b['warmup'] + b['steps']} forwards "
-           f"({b['warmup']} warmup + {b['steps']} timed); pack/pad/quantise/copy kernels are the "
-           "one-time parameter load.", "",
+           f"Workload: {b['config']['workload']}.  {b['warmup'] + b['steps']} {unit} "
+           f"({b['warmup']} warmup + {b['steps']} timed); pack/pad/quantise/copy/transpose kernels "
+           "are the one-time parameter load and backward weight layouts.", "",
            "| Kernel | Stage | Calls | Average (us) | Share of GPU time |", "|---|---|---|---|---|"]
     for r in rows:
         name = r["Name"].replace("unsigned short", "bf16").replace("mgpt::(anonymous namespace)::", "")
@@ -166,9 +181,16 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
             "| Stage | ms |", "|---|---|"]
     out += [f"| {k} | {v} |" for k, v in b["stage_ms"].items()]
     rf = b["roofline"]
-    out += ["", f"bench.py: {b['value']:.0f} tokens/s, {b['ms_per_step']} ms/step; gate/up GEMM "
-            f"{rf['achieved']} TFLOP/s = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s dense bf16; "
-            f"both expert GEMMs {b['expert_gemm_tflops']} TFLOP/s."]
+    if train:
+        out += [f"| {k} (backward) | {v} |" for k, v in b["backward_stage_ms"].items()]
+        out += ["", f"bench.py: {b['value']:.0f} training tokens/s, {b['ms_per_step']} ms/step "
+                f"(backward {b['backward_ms']} ms); backward products (TFLOP/s): "
+                + ", ".join(f"{k} {v}" for k, v in b["backward_gemm_tflops"].items())
+                + f"; dominant: {rf['kernel']} = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s."]
+    else:
+        out += ["", f"bench.py: {b['value']:.0f} tokens/s, {b['ms_per_step']} ms/step; gate/up GEMM "
+                f"{rf['achieved']} TFLOP/s = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s dense "
+                f"bf16; both expert GEMMs {b['expert_gemm_tflops']} TFLOP/s."]
     return "\n".join(out)
 
 
