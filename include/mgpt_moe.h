@@ -95,6 +95,27 @@ int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes);
 int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* The MoE half of a transformer block, fused: out = x + MoE(RMSNorm(x) * gamma)
+ * with RMSNorm(x) = x / sqrt(mean(x^2) + eps) per token, computed as the
+ * engine's ln2 RMSNormLayer does (utils/Tensor.cpp:785-800: sequential sum of
+ * squares, r = 1/sqrt(ms/C + eps), (x*r)*gamma).  Replaces the sequence
+ * ln2.forward_into, mlp.forward_into, Tensor::add_into of
+ * TransformerBlock::forward_into (layers/TransformerBlock.cpp:42-46) without
+ * writing or re-reading the normalised rows and the MoE output: the router
+ * normalises while it reads x (routing stays bit-exact with the reference on
+ * the normalised rows), the permute gathers normalised rows and the combine
+ * adds x.  gamma: device [C] fp32; x and out: act_dtype [N,C] (out must not
+ * alias x); workspace as for mgpt_moe_forward.  Routing views and counts
+ * refer to the normalised rows, as the reference's MoE sees them. */
+int mgpt_moe_forward_block(mgpt_moe* h, const void* x, const float* gamma, float eps, void* out,
+                           int num_tokens, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* Device view of the per-token 1/rms (r above) that the last
+ * mgpt_moe_forward_block wrote into `workspace` [N] fp32 (the reference's
+ * RMSNormLayer cached_rsqrt). */
+int mgpt_moe_get_rstd(const mgpt_moe* h, int num_tokens, void* workspace, float** rstd);
+
 /* Device views of the routing produced by the last mgpt_moe_forward into
  * `workspace` (valid once that call has completed on its stream):
  *   topk_idx [N,k] int32, topk_p [N,k] fp32 (descending p; raw clamped

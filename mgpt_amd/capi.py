@@ -84,6 +84,8 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_zero_grad": [vp, vp],
         "mgpt_moe_get_gradients": [vp, ctypes.POINTER(vp), i, i, vp],
         "mgpt_moe_backward_stage_times": [vp, vp, i],
+        "mgpt_moe_forward_block": [vp, vp, vp, ctypes.c_float, vp, i, vp, sz, vp],
+        "mgpt_moe_get_rstd": [vp, i, vp, ctypes.POINTER(vp)],
     }
     for name, args in sig.items():
         f = getattr(L, name)

@@ -51,6 +51,16 @@ struct Vec16<float> {
   }
 };
 
+// Fused block: y = x1 + the MoE sum (Tensor::add_into, utils/Tensor.cpp:
+// 1579-1597, after the scatter), one rounded add per element.
+template <typename ActT>
+__device__ __forceinline__ void add_resid(const ActT* p, float (&v)[Vec16<ActT>::n]) {
+  float x[Vec16<ActT>::n];
+  Vec16<ActT>::unpack(*reinterpret_cast<const uint4*>(p), x);
+#pragma unroll
+  for (int i = 0; i < Vec16<ActT>::n; ++i) v[i] = x[i] + v[i];
+}
+
 constexpr int kWavesPerBlock = 4;
 // Tokens per wave of the k = 2 kernel.  Measured on MI355X at cfg3 shapes:
 // 1 token (20.3 us) beats 2 (20.8 us); the extra loads in flight do not pay
@@ -66,7 +76,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const ActT* __restrict__ o
                                                       const int32_t* __restrict__ topk_idx,
                                                       const float* __restrict__ topk_p,
                                                       const int32_t* __restrict__ slot_of, int N,
-                                                      int C, int k, ActT* __restrict__ y) {
+                                                      int C, int k, const ActT* __restrict__ resid,
+                                                      ActT* __restrict__ y) {
   static_assert(TPW * kMaxTopK <= kWave, "one lane per (token, choice)");
   __shared__ int s_slot[kWavesPerBlock][TPW][kMaxTopK];
   __shared__ float s_p[kWavesPerBlock][TPW][kMaxTopK];
@@ -145,7 +156,10 @@ __global__ __launch_bounds__(256) void combine_kernel(const ActT* __restrict__ o
 #pragma unroll
         for (int ch = 0; ch < CH; ++ch) {
           const int c = c0 + (ch * kWave + l) * VN;
-          if (c < C) Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc[u][ch]);
+          if (c < C) {
+            if (resid) add_resid<ActT>(resid + (size_t)(t0 + u) * C + c, acc[u][ch]);
+            Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc[u][ch]);
+          }
         }
   }
 }
@@ -159,7 +173,8 @@ template <typename ActT, int TPW, int CH>
 __global__ __launch_bounds__(256) void combine2_kernel(const ActT* __restrict__ out_rows,
                                                        const float* __restrict__ topk_p,
                                                        const int32_t* __restrict__ slot_of, int N,
-                                                       int C, ActT* __restrict__ y) {
+                                                       int C, const ActT* __restrict__ resid,
+                                                       ActT* __restrict__ y) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l = lane_id();
   const int t0 = (blockIdx.x * kWavesPerBlock + w) * TPW;
@@ -210,7 +225,10 @@ __global__ __launch_bounds__(256) void combine2_kernel(const ActT* __restrict__ 
           for (int i = 0; i < VN; ++i) acc[i] = acc[i] + v[i] * pr[u][a];
         }
         const int c = c0 + (ch * kWave + l) * VN;
-        if (c < C && u < nt) Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc);
+        if (c < C && u < nt) {
+          if (resid) add_resid<ActT>(resid + (size_t)(t0 + u) * C + c, acc);
+          Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc);
+        }
       }
   }
 }
@@ -218,21 +236,22 @@ __global__ __launch_bounds__(256) void combine2_kernel(const ActT* __restrict__ 
 template <typename ActT, int TPW, int KT>
 void launch_combine_k(int chunks, hipStream_t stream, const ActT* out_rows,
                       const int32_t* topk_idx, const float* topk_p, const int32_t* slot_of, int N,
-                      int C, int k, ActT* y) {
+                      int C, int k, const ActT* resid, ActT* y) {
   const dim3 grid((N + kWavesPerBlock * TPW - 1) / (kWavesPerBlock * TPW));
   if (chunks >= 2)
     hipLaunchKernelGGL((combine_kernel<ActT, TPW, KT, 2>), grid, dim3(256), 0, stream, out_rows,
-                       topk_idx, topk_p, slot_of, N, C, k, y);
+                       topk_idx, topk_p, slot_of, N, C, k, resid, y);
   else
     hipLaunchKernelGGL((combine_kernel<ActT, TPW, KT, 1>), grid, dim3(256), 0, stream, out_rows,
-                       topk_idx, topk_p, slot_of, N, C, k, y);
+                       topk_idx, topk_p, slot_of, N, C, k, resid, y);
 }
 
 }  // namespace
 
+// resid (nullable): the fused block's residual, y = resid + sum.
 template <typename ActT>
 hipError_t launch_combine(const ActT* out_rows, const int32_t* topk_idx, const float* topk_p,
-                          const int32_t* slot_of, int N, int C, int k, ActT* y,
+                          const int32_t* slot_of, int N, int C, int k, const ActT* resid, ActT* y,
                           hipStream_t stream) {
   if (N == 0) return hipSuccess;
   if (k < 1 || k > kMaxTopK) return hipErrorInvalidValue;
@@ -244,31 +263,33 @@ hipError_t launch_combine(const ActT* out_rows, const int32_t* topk_idx, const f
                       (kWavesPerBlock * kTokensPerWave2));
       if (chunks >= 2)
         hipLaunchKernelGGL((combine2_kernel<ActT, kTokensPerWave2, 2>), grid, dim3(256), 0,
-                           stream, out_rows, topk_p, slot_of, N, C, y);
+                           stream, out_rows, topk_p, slot_of, N, C, resid, y);
       else
         hipLaunchKernelGGL((combine2_kernel<ActT, kTokensPerWave2, 1>), grid, dim3(256), 0,
-                           stream, out_rows, topk_p, slot_of, N, C, y);
+                           stream, out_rows, topk_p, slot_of, N, C, resid, y);
       break;
     }
     // fixed k: every row chunk of a token in flight at once
     case 6:
       launch_combine_k<ActT, 1, 6>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
-                                   y);
+                                   resid, y);
       break;
     case 8:
       launch_combine_k<ActT, 1, 8>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
-                                   y);
+                                   resid, y);
       break;
     default:
       launch_combine_k<ActT, 1, 0>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
-                                   y);
+                                   resid, y);
   }
   return hipGetLastError();
 }
 
 template hipError_t launch_combine<float>(const float*, const int32_t*, const float*,
-                                          const int32_t*, int, int, int, float*, hipStream_t);
+                                          const int32_t*, int, int, int, const float*, float*,
+                                          hipStream_t);
 template hipError_t launch_combine<bf16_t>(const bf16_t*, const int32_t*, const float*,
-                                           const int32_t*, int, int, int, bf16_t*, hipStream_t);
+                                           const int32_t*, int, int, int, const bf16_t*, bf16_t*,
+                                           hipStream_t);
 
 }  // namespace mgpt

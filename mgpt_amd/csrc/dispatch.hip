@@ -62,6 +62,27 @@ struct alignas(16) V16 {
   uint32_t w[4];
 };
 
+// The row normalisation of a fused block applied to one 16-byte chunk
+// (columns c .. c + 16/sizeof(ActT) - 1): x -> (x * r) * gamma[c], two
+// rounded products as the reference's RMSNorm forms them, then rounded to
+// the activation type.
+__device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g, float) {
+  V16 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o.w[i] = __float_as_uint((__uint_as_float(v.w[i]) * r) * g[i]);
+  return o;
+}
+__device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g, bf16_t) {
+  V16 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = (__uint_as_float(v.w[i] << 16) * r) * g[2 * i];
+    const float b = (__uint_as_float(v.w[i] & 0xFFFF0000u) * r) * g[2 * i + 1];
+    o.w[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+  }
+  return o;
+}
+
 // One block per (router block of TB tokens = TB*k flat ids, column slice):
 // every slice ranks the block's ids (cheap), slice 0 writes perm/slot_of,
 // and each slice copies its share of the row bytes.  Slices only matter for
@@ -72,7 +93,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
     const ActT* __restrict__ x, const int32_t* __restrict__ topk_idx,
     const int32_t* __restrict__ hist, const int32_t* __restrict__ base, int nb, int N, int C,
     int E, int k, int32_t* __restrict__ counts, int32_t* __restrict__ perm,
-    int32_t* __restrict__ slot_of, ActT* __restrict__ xg) {
+    int32_t* __restrict__ slot_of, ActT* __restrict__ xg, const float* __restrict__ rstd,
+    const float* __restrict__ gamma) {
   __shared__ int s_base[kMaxExperts];
   __shared__ int s_pre[kMaxExperts];
   __shared__ int s_tot[kMaxExperts];
@@ -186,6 +208,14 @@ __global__ __launch_bounds__(256) void permute_kernel(
           const int r = min(r0 + R * u, ntok - 1);
           v[u] = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C)[q];
         }
+        if (gamma) {   // fused block: gather the normalised rows
+          constexpr int kPer = 16 / (int)sizeof(ActT);
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int r = min(r0 + R * u, ntok - 1);
+            v[u] = normalize16(v[u], rstd[tok0 + r], gamma + q * kPer, ActT());
+          }
+        }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int r = r0 + R * u;
@@ -203,10 +233,13 @@ __global__ __launch_bounds__(256) void permute_kernel(
 
 }  // namespace
 
+// rstd / gamma (both null, or both set): the fused block gathers
+// (x * rstd[t]) * gamma instead of x.
 template <typename ActT>
 hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t* hist,
                           int32_t* base, int N, int C, int E, int k, int32_t* counts,
-                          int32_t* perm, int32_t* slot_of, ActT* xg, hipStream_t stream) {
+                          int32_t* perm, int32_t* slot_of, ActT* xg, const float* rstd,
+                          const float* gamma, hipStream_t stream) {
   const int TB = router_tokens_per_block(E);
   const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
@@ -218,15 +251,17 @@ hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t*
   const int chunks = C * (int)sizeof(ActT) / 16;
   const int slices = max(1, min(chunks / 8, (512 + nb - 1) / nb));
   hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb, slices), dim3(256), 0, stream, x, topk_idx,
-                     hist, fold ? nullptr : base, nb, N, C, E, k, counts, perm, slot_of, xg);
+                     hist, fold ? nullptr : base, nb, N, C, E, k, counts, perm, slot_of, xg, rstd,
+                     gamma);
   return hipGetLastError();
 }
 
 template hipError_t launch_permute<float>(const float*, const int32_t*, const int32_t*, int32_t*,
                                           int, int, int, int, int32_t*, int32_t*, int32_t*,
-                                          float*, hipStream_t);
+                                          float*, const float*, const float*, hipStream_t);
 template hipError_t launch_permute<bf16_t>(const bf16_t*, const int32_t*, const int32_t*,
                                            int32_t*, int, int, int, int, int32_t*, int32_t*,
-                                           int32_t*, bf16_t*, hipStream_t);
+                                           int32_t*, bf16_t*, const float*, const float*,
+                                           hipStream_t);
 
 }  // namespace mgpt

@@ -35,14 +35,16 @@ namespace mgpt {
 // kernels (router.hip, dispatch.hip, gemm.hip, combine.hip, pack.hip)
 template <typename ActT>
 hipError_t launch_router(const ActT*, const float*, const float*, const float*, int, int, int,
-                         int, int32_t*, float*, int32_t*, float*, float*, hipStream_t);
+                         int, int32_t*, float*, int32_t*, float*, float*, const float*, float,
+                         float*, hipStream_t);
 hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
 template <typename ActT>
 hipError_t launch_permute(const ActT*, const int32_t*, const int32_t*, int32_t*, int, int, int,
-                          int, int32_t*, int32_t*, int32_t*, ActT*, hipStream_t);
+                          int, int32_t*, int32_t*, int32_t*, ActT*, const float*, const float*,
+                          hipStream_t);
 template <typename ActT>
 hipError_t launch_combine(const ActT*, const int32_t*, const float*, const int32_t*, int, int, int,
-                          ActT*, hipStream_t);
+                          const ActT*, ActT*, hipStream_t);
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT*, const WT*, const float*, const float*, const float*,
                                const int32_t*, int, int, int, int, int, OutT*, int, int, OutT*,
@@ -113,6 +115,7 @@ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 
 struct Layout {
   size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, partials;
+  size_t rstd;   // fused block: 1/rms of each token [N] f32
   // training only (after the forward regions, so those keep their offsets):
   // router probabilities [N][E] f32, gate/up pre-activations (then their
   // gradients) [A+pad][2Hp], dgo [A+pad][C], d(top-k p) [A] f32,
@@ -200,6 +203,7 @@ struct mgpt_moe {
     L.obuf = take((A + kRowPad) * C * act_bytes());
     // fp32 partial tiles of the large-M GEMMs' split last round (one per CU)
     L.partials = take(uses_gemm_dma(N) ? (size_t)num_cus * kGemmPartialBytes : 0);
+    L.rstd = take((size_t)N * 4);
     if (train) {
       L.probs = take((size_t)N * E * 4);
       L.gu = take((A + kRowPad) * 2 * Hp * act_bytes());
@@ -498,9 +502,16 @@ int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes) {
 
 namespace {
 
+// Block mode (gamma set): route and gather RMSNorm(x) * gamma and add x
+// to the output (the MoE half of TransformerBlock::forward_into).
+struct BlockArgs {
+  const float* gamma = nullptr;
+  float eps = 0.0f;
+};
+
 template <typename ActT>
 int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool train,
-                 hipStream_t st) {
+                 hipStream_t st, BlockArgs blk = BlockArgs()) {
   const Layout L = h->layout(N, train);
   const int C = h->C, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
   const size_t A = (size_t)N * k;
@@ -523,10 +534,12 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
   // training: keep the router probabilities and the gate/up pre-activations
   float* probs = train ? (float*)(ws + L.probs) : nullptr;
   ActT* gu = train ? (ActT*)(ws + L.gu) : nullptr;
+  float* rstd = blk.gamma ? (float*)(ws + L.rstd) : nullptr;
   HIP_TRY(launch_router<ActT>(x, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits,
-                              probs, st));
+                              probs, blk.gamma, blk.eps, rstd, st));
   HIP_TRY(mark(1));
-  HIP_TRY(launch_permute<ActT>(x, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg, st));
+  HIP_TRY(launch_permute<ActT>(x, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg, rstd,
+                               blk.gamma, st));
   HIP_TRY(mark(2));
   if constexpr (sizeof(ActT) == 4) {
     const int mt = (int)((A + 63) / 64) + E;
@@ -599,7 +612,7 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
     }
   }
   HIP_TRY(mark(4));
-  HIP_TRY(launch_combine<ActT>(ob, idx, topp, slot_of, N, C, k, y, st));
+  HIP_TRY(launch_combine<ActT>(ob, idx, topp, slot_of, N, C, k, blk.gamma ? x : nullptr, y, st));
   HIP_TRY(mark(5));
   if (prof) ++h->prof_count;
   HIP_TRY(hipEventRecord(h->done, st));
@@ -738,6 +751,33 @@ int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* 
                                 false, st);
   return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, false,
                              st);
+}
+
+int mgpt_moe_forward_block(mgpt_moe* h, const void* x, const float* gamma, float eps, void* out,
+                           int num_tokens, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  if (int rc = check_forward_args(h, x, out, num_tokens, workspace, workspace_bytes, false))
+    return rc;
+  if (num_tokens == 0) return MGPT_OK;
+  if (!gamma) return fail(MGPT_ERR_INVALID_ARGUMENT, "null gamma");
+  if (!(eps >= 0.0f)) return fail(MGPT_ERR_INVALID_ARGUMENT, "eps must be >= 0");
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  BlockArgs blk;
+  blk.gamma = gamma;
+  blk.eps = eps;
+  if (h->act == MGPT_DTYPE_BF16)
+    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)out, num_tokens, (char*)workspace,
+                                false, st, blk);
+  return forward_impl<float>(h, (const float*)x, (float*)out, num_tokens, (char*)workspace, false,
+                             st, blk);
+}
+
+int mgpt_moe_get_rstd(const mgpt_moe* h, int num_tokens, void* workspace, float** rstd) {
+  if (!h || !workspace || !rstd || num_tokens < 0)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "null argument or negative num_tokens");
+  *rstd = (float*)((char*)workspace + h->layout(num_tokens).rstd);
+  return MGPT_OK;
 }
 
 int mgpt_moe_train_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes) {

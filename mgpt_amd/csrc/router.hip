@@ -185,10 +185,38 @@ __device__ __forceinline__ int chunk_cols(int nw, int RE) {
 // reads).  Each logit accumulates c = 0, 1, ... in order, one rounded
 // product and one rounded add per term (built with -ffp-contract=off); the
 // caller adds the bias.
+// Row normalisation fused into the router (the engine's ln2 RMSNormLayer,
+// utils/Tensor.cpp:785-800): with gamma set, a first pass over the staged
+// chunks sums x^2 of the lane's row in column order, r = 1/sqrt(ms/C + eps)
+// with IEEE division and square root, and the logits then use
+// (x * r) * gamma[c], two rounded products as the reference forms them.
+struct RowNorm {
+  const float* gamma;   // null: no normalisation
+  float eps;
+};
+
+// Correctly rounded square root of a positive normal y.  The hardware
+// v_sqrt_f32 is within an ulp but not always the nearest float, so the
+// estimate s is corrected by the sign of the exact residuals y - s_-*s and
+// y - s_+*s of its neighbours (one fused multiply-add each; the classic
+// residual test for a one-ulp-accurate square root, Muller et al.,
+// Handbook of Floating-Point Arithmetic, ch. 5): residuals are multiples
+// of ulp(s)^2, so their signs decide the rounding exactly.
+__device__ __forceinline__ float sqrt_rn(float y) {
+  const float s = __builtin_amdgcn_sqrtf(y);
+  if (!(y >= 0x1p-100f && y <= 0x1p100f)) return s;   // outside the normalisation's range
+  const float sd = __uint_as_float(__float_as_uint(s) - 1u);
+  const float su = __uint_as_float(__float_as_uint(s) + 1u);
+  if (__builtin_fmaf(-sd, s, y) <= 0.0f) return sd;
+  if (__builtin_fmaf(-su, s, y) > 0.0f) return su;
+  return s;
+}
+
 template <typename ActT, int RE>
 __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int n_rows,
                                              const float* __restrict__ wsrc, int g_valid, int nw,
-                                             int g, int C, char* smem, float (&acc)[RE]) {
+                                             int g, int C, char* smem, float (&acc)[RE],
+                                             RowNorm nrm, float* r_out) {
   constexpr int kPer = 16 / (int)sizeof(ActT);   // columns per 16-byte unit
   const int CB = chunk_cols<ActT>(nw, RE);
   const int xrow_bytes = CB * (int)sizeof(ActT);   // LDS bytes per token row
@@ -234,6 +262,31 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
   for (int j = 0; j < RE; ++j) acc[j] = 0.0f;
   constexpr int kWU = kPer * RE / 4;   // float4 of weights per unit
   int b = 0;
+  float r = 1.0f;
+  if (nrm.gamma) {
+    // pass 1: the row's sum of squares, columns in order
+    float ms = 0.0f;
+    chunk_dma(0, min(CB, C), 0);
+    for (int c0 = 0; c0 < C; c0 += CB) {
+      const int cnum = min(CB, C - c0);
+      drain_barrier();
+      if (c0 + CB < C) chunk_dma(c0 + CB, min(CB, C - c0 - CB), b ^ 1);
+      const char* xr = smem + b * stage_bytes + lane * xrow_bytes;
+      for (int u = 0; u < cnum / kPer; ++u) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const float v = widen<ActT>(xv, i);
+          ms = ms + v * v;
+        }
+      }
+      b ^= 1;
+    }
+    r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ms, (float)C) + nrm.eps));
+    if (r_out) *r_out = r;
+    drain_barrier();   // every wave done with the stages before they are refilled
+    b = 0;
+  }
   chunk_dma(0, min(CB, C), 0);
   for (int c0 = 0; c0 < C; c0 += CB) {
     const int cnum = min(CB, C - c0);
@@ -243,31 +296,59 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
     const char* xr = st + lane * xrow_bytes;
     const float* wq = reinterpret_cast<const float*>(st + x_bytes + g * wgb);
     const int units = cnum / kPer;
-    // operands of unit u+1 are read while unit u is multiplied
-    uint4 x0, x1;
-    float4 w0[kWU], w1[kWU];
-    auto rd = [&](int u, uint4& xv, float4 (&wv)[kWU]) __attribute__((always_inline)) {
-      xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
+    if (!nrm.gamma) {
+      // operands of unit u+1 are read while unit u is multiplied
+      uint4 x0, x1;
+      float4 w0[kWU], w1[kWU];
+      auto rd = [&](int u, uint4& xv, float4 (&wv)[kWU]) __attribute__((always_inline)) {
+        xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
 #pragma unroll
-      for (int v = 0; v < kWU; ++v) wv[v] = reinterpret_cast<const float4*>(wq + u * kPer * RE)[v];
-    };
-    auto mul_add = [&](const uint4& xv, const float4 (&wv)[kWU]) __attribute__((always_inline)) {
+        for (int v = 0; v < kWU; ++v)
+          wv[v] = reinterpret_cast<const float4*>(wq + u * kPer * RE)[v];
+      };
+      auto mul_add = [&](const uint4& xv, const float4 (&wv)[kWU]) __attribute__((always_inline)) {
 #pragma unroll
-      for (int v = 0; v < kWU; ++v) {
-        const float w4[4] = {wv[v].x, wv[v].y, wv[v].z, wv[v].w};
+        for (int v = 0; v < kWU; ++v) {
+          const float w4[4] = {wv[v].x, wv[v].y, wv[v].z, wv[v].w};
 #pragma unroll
-        for (int e4 = 0; e4 < 4; ++e4) {
-          const int idx = 4 * v + e4;   // = column * RE + expert
-          acc[idx % RE] = acc[idx % RE] + widen<ActT>(xv, idx / RE) * w4[e4];
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int idx = 4 * v + e4;   // = column * RE + expert
+            acc[idx % RE] = acc[idx % RE] + widen<ActT>(xv, idx / RE) * w4[e4];
+          }
+        }
+      };
+      rd(0, x0, w0);
+      for (int u = 0; u < units; u += 2) {   // units is even (cnum % 64 == 0)
+        rd(u + 1, x1, w1);
+        mul_add(x0, w0);
+        if (u + 2 < units) rd(u + 2, x0, w0);
+        mul_add(x1, w1);
+      }
+    } else {
+      // normalised: x -> (x * r) * gamma[c] before each product (gamma is
+      // the same for every lane: wave-uniform loads)
+      for (int u = 0; u < units; ++u) {
+        const uint4 xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
+        float4 wv[kWU];
+#pragma unroll
+        for (int v = 0; v < kWU; ++v)
+          wv[v] = reinterpret_cast<const float4*>(wq + u * kPer * RE)[v];
+        float xn[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) {
+          const float gm = nrm.gamma[c0 + u * kPer + i];
+          xn[i] = (widen<ActT>(xv, i) * r) * gm;
+        }
+#pragma unroll
+        for (int v = 0; v < kWU; ++v) {
+          const float w4[4] = {wv[v].x, wv[v].y, wv[v].z, wv[v].w};
+#pragma unroll
+          for (int e4 = 0; e4 < 4; ++e4) {
+            const int idx = 4 * v + e4;
+            acc[idx % RE] = acc[idx % RE] + xn[idx / RE] * w4[e4];
+          }
         }
       }
-    };
-    rd(0, x0, w0);
-    for (int u = 0; u < units; u += 2) {   // units is even (cnum % 64 == 0)
-      rd(u + 1, x1, w1);
-      mul_add(x0, w0);
-      if (u + 2 < units) rd(u + 2, x0, w0);
-      mul_add(x1, w1);
     }
     b ^= 1;
   }
@@ -355,7 +436,8 @@ template <typename ActT, int RE>
 __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
     int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
-    int32_t* __restrict__ hist, int num_blocks, float* __restrict__ probs) {
+    int32_t* __restrict__ hist, int num_blocks, float* __restrict__ probs, RowNorm nrm,
+    float* __restrict__ rstd) {
   __shared__ float s_l[kRT][kMaxExperts + 1];
   __shared__ float s_m[kRT];
   __shared__ int s_hist[kMaxExperts];
@@ -367,7 +449,9 @@ __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
   const int tok0 = blockIdx.x * kRT;
   if (tid < kMaxExperts) s_hist[tid] = 0;
   float acc[RE];
-  logit_chains<ActT, RE>(x + (size_t)tok0 * C, N - tok0, wr_g, nw, nw, g, C, smem, acc);
+  float r = 1.0f;
+  logit_chains<ActT, RE>(x + (size_t)tok0 * C, N - tok0, wr_g, nw, nw, g, C, smem, acc, nrm, &r);
+  if (nrm.gamma && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
 #pragma unroll
   for (int j = 0; j < RE; ++j) {
     const int e = g * RE + j;
@@ -387,15 +471,17 @@ constexpr int kSplitExperts = 4;
 template <typename ActT>
 __global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr1, const float* __restrict__ br,
-    int N, int C, int E, float* __restrict__ logits) {
+    int N, int C, int E, float* __restrict__ logits, RowNorm nrm, float* __restrict__ rstd) {
   __shared__ __attribute__((aligned(1024))) char smem[kRouterLds];
   const int lane = lane_id();
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
   const int e0 = blockIdx.y * kSplitExperts;
   const int tok0 = blockIdx.x * kRT;
   float acc[1];
+  float r = 1.0f;
   logit_chains<ActT, 1>(x + (size_t)tok0 * C, N - tok0, wr1 + (size_t)e0 * C,
-                        min(kSplitExperts, E - e0), kSplitExperts, g, C, smem, acc);
+                        min(kSplitExperts, E - e0), kSplitExperts, g, C, smem, acc, nrm, &r);
+  if (nrm.gamma && blockIdx.y == 0 && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
   const int e = e0 + g;
   if (e < E && tok0 + lane < N) logits[(size_t)(tok0 + lane) * E + e] = acc[0] + br[e];
 }
@@ -426,16 +512,21 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
 // logits == nullptr: the fused kernel.  Otherwise (E > 16, few tokens) the
 // split path through logits [N][E] (wr1 = W_r as [E][C]).  probs (nullable)
 // receives the clamped softmax [N][E] (the reference's cached_router_probs).
+// gamma (nullable): route on RMSNorm(x) * gamma instead of x, writing each
+// token's 1/rms to rstd [N].
 template <typename ActT>
 hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, const float* br,
                          int N, int C, int E, int k, int32_t* topk_idx, float* topk_p,
-                         int32_t* hist, float* logits, float* probs, hipStream_t stream) {
+                         int32_t* hist, float* logits, float* probs, const float* gamma,
+                         float eps, float* rstd, hipStream_t stream) {
+  const RowNorm nrm{gamma, eps};
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
   if (logits) {
     hipLaunchKernelGGL(router_logits_kernel<ActT>,
                        dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
-                       dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits);
+                       dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits, nrm,
+                       rstd);
     hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(1024), 0, stream, logits, N, E, k,
                        topk_idx, topk_p, hist, nb, probs);
     return hipGetLastError();
@@ -446,25 +537,26 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
   switch (RE) {
     case 1:
       hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 1>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb, probs);
+                         C, E, k, topk_idx, topk_p, hist, nb, probs, nrm, rstd);
       break;
     case 2:
       hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 2>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb, probs);
+                         C, E, k, topk_idx, topk_p, hist, nb, probs, nrm, rstd);
       break;
     default:
       hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 4>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb, probs);
+                         C, E, k, topk_idx, topk_p, hist, nb, probs, nrm, rstd);
   }
   return hipGetLastError();
 }
 
 template hipError_t launch_router<float>(const float*, const float*, const float*, const float*,
                                          int, int, int, int, int32_t*, float*, int32_t*, float*,
-                                         float*, hipStream_t);
+                                         float*, const float*, float, float*, hipStream_t);
 template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*,
                                           const float*, int, int, int, int, int32_t*, float*,
-                                          int32_t*, float*, float*, hipStream_t);
+                                          int32_t*, float*, float*, const float*, float, float*,
+                                          hipStream_t);
 
 // Device expf over a buffer (tests compare it with the host's glibc expf).
 __global__ void expf_probe_kernel(const float* __restrict__ in, float* __restrict__ out, int n) {

@@ -124,6 +124,34 @@ class MoELayer:
         self.forward_into(x, out, train)
         return out
 
+    def forward_block(self, x: torch.Tensor, gamma: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+        """out = x + MoE(RMSNorm(x) * gamma): the MoE half of a transformer
+        block (ln2, mlp and the residual add of
+        layers/TransformerBlock.cpp:42-46) in one fused pass."""
+        if not x.is_cuda or x.dtype != self.dtype or x.shape[-1] != self.C or not x.is_contiguous():
+            raise ValueError("x must be a contiguous device tensor [..., C] of the layer's dtype")
+        g = gamma.detach().to(device=x.device, dtype=torch.float32).contiguous()
+        if g.numel() != self.C:
+            raise ValueError("gamma must have C elements")
+        out = torch.empty_like(x)
+        n = x.numel() // self.C
+        ws = self._workspace(n, x.device)
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        capi.check(capi.lib().mgpt_moe_forward_block(self._h, x.data_ptr(), g.data_ptr(),
+                                                     float(eps), out.data_ptr(), n,
+                                                     ws.data_ptr(), ws.numel(), stream))
+        self._last_n = n
+        self._train_x = None
+        return out
+
+    def rstd(self) -> torch.Tensor:
+        """Device view [N] of the per-token 1/rms of the last forward_block."""
+        n = self._last_n
+        p = ctypes.c_void_p()
+        capi.check(capi.lib().mgpt_moe_get_rstd(self._h, n, self._ws.data_ptr(), ctypes.byref(p)))
+        off = p.value - self._ws.data_ptr()
+        return self._ws[off:off + 4 * n].view(torch.float32)
+
     # -------------------------------------------------------------- backward
     def backward_into(self, dout: torch.Tensor, din: torch.Tensor) -> None:
         """din = dL/dx for upstream gradient dout after forward(x, train=True);

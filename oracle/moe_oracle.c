@@ -440,3 +440,42 @@ void oracle_rmsnorm(int N, int C, float eps, const float* x, float* out) {
     for (int c = 0; c < C; ++c) out[(size_t)i * C + c] = (xr[c] * r) * 1.0f;
   }
 }
+
+/* utils/Tensor.cpp:785-800 (rms_norm_into, CPU branch), as called by
+ * RMSNormLayer::forward_into (layers/RMSNormLayer.cpp:14-22):
+ * ms = sum x^2 sequential; r = 1/sqrt(ms/C + eps); out = (x*r)*scale. */
+void oracle_rmsnorm_scaled(int N, int C, float eps, const float* x, const float* scale,
+                           float* out, float* rstd) {
+  for (int i = 0; i < N; ++i) {
+    const float* xr = x + (size_t)i * C;
+    float ms = 0.0f;
+    for (int c = 0; c < C; ++c) ms += xr[c] * xr[c];
+    const float r = 1.0f / sqrtf(ms / C + eps);
+    if (rstd) rstd[i] = r;
+    for (int c = 0; c < C; ++c) {
+      const float norm = xr[c] * r;
+      out[(size_t)i * C + c] = norm * scale[c];
+    }
+  }
+}
+
+/* layers/TransformerBlock.cpp:42-46: ln2.forward_into(x1, xn),
+ * mlp.forward_into(xn, y), Tensor::add_into(x1, y, out) (utils/Tensor.cpp:
+ * 1579-1597: out = x1 + y elementwise). */
+int oracle_moe_block(int N, int C, int H, int E, int k, float eps, const float* x1,
+                     const float* gamma, const float* Wr, const float* br, const float* Wg,
+                     const float* bg, const float* Wu, const float* bu, const float* Wd,
+                     const float* bd, float* out, float* xn, float* rstd, int32_t* idx,
+                     float* topp, int32_t* counts, int32_t* perm) {
+  if (N < 0 || C <= 0) return 1;
+  float* XN = xn ? xn : (float*)malloc(sizeof(float) * ((size_t)N * C + 1));
+  float* Y = (float*)malloc(sizeof(float) * ((size_t)N * C + 1));
+  oracle_rmsnorm_scaled(N, C, eps, x1, gamma, XN, rstd);
+  int rc = oracle_moe_forward(N, C, H, E, k, XN, Wr, br, Wg, bg, Wu, bu, Wd, bd, Y, NULL, NULL,
+                              idx, topp, counts, NULL, perm);
+  if (rc == 0)
+    for (size_t i = 0; i < (size_t)N * C; ++i) out[i] = x1[i] + Y[i];
+  if (!xn) free(XN);
+  free(Y);
+  return rc;
+}

@@ -76,6 +76,21 @@ int oracle_moe_backward(int N, int C, int H, int E, int k, const float* x,
                         float* dbg, float* dWu, float* dbu, float* dWd,
                         float* dbd);
 
+/* out[N,C] = RMSNorm(x) * scale and rstd[N] = 1/rms, the engine's
+ * RMSNormLayer (eps) forward; rstd may be NULL. */
+void oracle_rmsnorm_scaled(int N, int C, float eps, const float* x, const float* scale,
+                           float* out, float* rstd);
+
+/* The MoE half of a transformer block: xn = RMSNorm(x1) * gamma, y = MoE(xn),
+ * out = x1 + y.  xn (may be NULL) receives the normalised rows, rstd (may
+ * be NULL) the per-token 1/rms; the routing outputs follow
+ * oracle_moe_forward (any may be NULL). */
+int oracle_moe_block(int N, int C, int H, int E, int k, float eps, const float* x1,
+                     const float* gamma, const float* Wr, const float* br, const float* Wg,
+                     const float* bg, const float* Wu, const float* bu, const float* Wd,
+                     const float* bd, float* out, float* xn, float* rstd, int32_t* idx,
+                     float* topp, int32_t* counts, int32_t* perm);
+
 /* x_hat[N,C] = RMSNorm(x) with gamma = 1 (input preparation, a1). */
 void oracle_rmsnorm(int N, int C, float eps, const float* x, float* out);
 

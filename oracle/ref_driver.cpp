@@ -8,6 +8,7 @@
 //
 //   ref_driver run  <in.bin> <out.bin>
 //   ref_driver backward <in.bin> <dy.bin> <grad.bin>
+//   ref_driver block <in.bin> <gamma.bin> <out.bin>
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
 //   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (forward + backward)
 //
@@ -19,6 +20,11 @@
 //          float32 topp[N*k], int32 counts[E], int32 offsets[E],
 //          int32 perm[N*k], float32 logits[N*E], float32 probs[N*E].
 // dy.bin : float32 dy[N*C] (the upstream gradient).
+// block  : x of in.bin is the residual stream x1, gamma.bin float32 [C] the
+//          ln2 scale; out.bin: "MGPTBLK1", int32 N C E k, float32 out[N*C]
+//          (x1 + MoE(ln2(x1)), layers/TransformerBlock.cpp:42-46), float32
+//          xn[N*C] (ln2's output), float32 rstd[N] (its cached_rsqrt),
+//          int32 idx[N*k], float32 topp[N*k], int32 counts[E], int32 perm[N*k].
 // grad.bin: "MGPTGRD1", int32 N C H E k, float32 dx[N*C], then the .grad of
 //          every parameter in get_parameters() order (sizes as in in.bin),
 //          after one forward_into and one backward_into
@@ -45,6 +51,7 @@
 // headers see the redefinition.
 #define private public
 #include "MoELayer.h"
+#include "RMSNormLayer.h"
 #undef private
 
 namespace {
@@ -146,6 +153,45 @@ int backward(const char* in_path, const char* dy_path, const char* out_path) {
   return 0;
 }
 
+int block(const char* in_path, const char* g_path, const char* out_path) {
+  int32_t dims[5];
+  Tensor x1;
+  std::unique_ptr<MoELayer> owner;
+  if (int rc = load(in_path, dims, x1, owner)) return rc;
+  MoELayer& layer = *owner;
+  const int N = dims[0], C = dims[1], E = dims[3], k = dims[4];
+  RMSNormLayer ln2(C);   // eps = 1e-5, layers/RMSNormLayer.h:23
+  FILE* f = std::fopen(g_path, "rb");
+  if (!f) { std::perror(g_path); return 2; }
+  if (!read_exact(f, ln2.get_parameters()[0]->data.data(), sizeof(float) * C)) return 3;
+  std::fclose(f);
+
+  Tensor xn, y, out;
+  ln2.forward_into(x1, xn);
+  layer.forward_into(xn, y);
+  Tensor::add_into(x1, y, out);
+
+  const size_t A = (size_t)N * k;
+  std::vector<int32_t> idx(A), perm(A), counts(E);
+  for (size_t i = 0; i < A; ++i) idx[i] = (int32_t)layer.cached_top_indices.data[i];
+  for (size_t i = 0; i < A; ++i) perm[i] = (int32_t)layer.cached_sorted_token_ids.data[i];
+  for (int e = 0; e < E; ++e) counts[e] = (int32_t)layer.cached_cpu_counts[e];
+  FILE* o = std::fopen(out_path, "wb");
+  if (!o) { std::perror(out_path); return 2; }
+  const int32_t odims[4] = {N, C, E, k};
+  std::fwrite("MGPTBLK1", 1, 8, o);
+  std::fwrite(odims, sizeof(int32_t), 4, o);
+  std::fwrite(out.data.data(), sizeof(float), (size_t)N * C, o);
+  std::fwrite(xn.data.data(), sizeof(float), (size_t)N * C, o);
+  std::fwrite(ln2.cached_rsqrt.data.data(), sizeof(float), (size_t)N, o);
+  std::fwrite(idx.data(), sizeof(int32_t), A, o);
+  std::fwrite(layer.cached_top_probs.data.data(), sizeof(float), A, o);
+  std::fwrite(counts.data(), sizeof(int32_t), E, o);
+  std::fwrite(perm.data(), sizeof(int32_t), A, o);
+  std::fclose(o);
+  return 0;
+}
+
 // Times MoELayer::forward_into (train: forward_into then backward_into with
 // dout ~ N(0,1)) on one fresh layer (its CPU caches are sized on first use
 // and never resized, layers/MoELayer.cpp:42-50): 1 warmup, then `reps`
@@ -195,11 +241,12 @@ int bench(int N, int C, int H, int E, int k, int reps, bool train) {
 int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
   if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
+  if (argc == 5 && std::string(argv[1]) == "block") return block(argv[2], argv[3], argv[4]);
   if (argc == 8 && (std::string(argv[1]) == "bench" || std::string(argv[1]) == "bench_train"))
     return bench(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]),
                  std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]),
                  std::string(argv[1]) == "bench_train");
   std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | "
-                       "bench[_train] N C H E k reps\n");
+                       "block <in> <gamma> <out> | bench[_train] N C H E k reps\n");
   return 1;
 }

@@ -109,6 +109,30 @@ def build_dy(case: Case) -> np.ndarray:
     return dy
 
 
+# Cases of the fused block (tests/golden/block/): out = x1 + MoE(RMSNorm(x1)*gamma).
+BLOCK_CASES = ["small_f32", "ragged_k3", "k8_bf16", "bf16_large_m", "fp8_small", "cfg1", "cfg3",
+               "cfg5"]
+BLOCK_EPS = 1e-5   # the engine's RMSNormLayer default (layers/RMSNormLayer.h:23)
+
+
+def build_block_inputs(case: Case):
+    """(x1, gamma) of a fused-block case: the case's unit-RMS rows scaled per
+    token by 2^(t%5 - 2) * (1 + (t%3)/4), i.e. 0.25 .. 6 (so the
+    normalisation matters), plus a small offset, and gamma = 1 + 0.2 N(0,1)
+    from the portable generator.  Only float32 arithmetic on exactly
+    generated values, so every host builds the same bits (no libm)."""
+    inp = build_inputs(case)
+    N, Cc = inp.x.shape
+    t = np.arange(N)
+    scale = (np.exp2((t % 5 - 2).astype(np.float32)) *
+             (np.float32(1.0) + (t % 3).astype(np.float32) / np.float32(4.0)))
+    x1 = (inp.x * scale[:, None].astype(np.float32) + np.float32(0.05)).astype(np.float32)
+    gamma = (np.float32(1.0) + wl.normal_f32(SEED, 4013, Cc, std=0.2)).astype(np.float32)
+    if case.cfg.act == "bf16":
+        x1 = wl.bf16_round(x1)
+    return inp, x1, gamma
+
+
 def sample_flat(n: int, m: int = 256) -> np.ndarray:
     """Deterministic sample of flat indices of an n-element gradient."""
     if n <= m:

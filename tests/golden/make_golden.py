@@ -23,7 +23,13 @@ tests/golden/backward/<case>.npz with
   dx and every gradient in full                  cases with full_arrays and
                                                  at most 1e5 gradient values
 
-Usage: python tests/golden/make_golden.py [--backward] [case ...]
+With --block it runs the reference's ln2 RMSNormLayer, MoELayer and
+Tensor::add_into (ref_driver block) on cases.BLOCK_CASES with
+(x1, gamma) = cases.build_block_inputs(case), and stores
+tests/golden/block/<case>.npz with sha256 digests of out, xn, rstd, idx,
+topp, perm, the counts, sampled rows of out and xn, and rstd in full.
+
+Usage: python tests/golden/make_golden.py [--backward | --block] [case ...]
 (default: all cases)
 """
 from __future__ import annotations
@@ -98,10 +104,13 @@ GRAD_NAMES = ("dWr", "dbr", "dWg", "dbg", "dWu", "dbu", "dWd", "dbd")
 
 
 def canonical_digest(a: np.ndarray) -> str:
-    """Digest with every NaN replaced by one quiet NaN (payload bits of NaNs
-    are not part of the contract)."""
-    a = np.array(a, dtype=np.float32, copy=True)
-    a[np.isnan(a)] = np.float32("nan")
+    """Digest with every NaN of a float array replaced by one quiet NaN
+    (payload bits of NaNs are not part of the contract); integer arrays as
+    they are."""
+    a = np.array(a, copy=True)
+    if a.dtype.kind == "f":
+        a = a.astype(np.float32)
+        a[np.isnan(a)] = np.float32("nan")
     return wl.digest(a)
 
 
@@ -163,6 +172,47 @@ def make_backward(case: C.Case) -> None:
           flush=True)
 
 
+def make_block(case: C.Case) -> None:
+    t0 = time.time()
+    inp, x1, gamma = C.build_block_inputs(case)
+    cfg = inp.cfg
+    N, Cc, E, k = cfg.N, cfg.C, cfg.E, cfg.k
+    blk_inp = wl.MoEInputs(cfg, x1, inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu, inp.Wd,
+                           inp.bd, inp.raw)
+    with tempfile.TemporaryDirectory() as d:
+        ip, gp, op = (os.path.join(d, n) for n in ("in.bin", "gamma.bin", "out.bin"))
+        write_input(ip, blk_inp)
+        np.ascontiguousarray(gamma, np.float32).tofile(gp)
+        subprocess.run([REF, "block", ip, gp, op], check=True)
+        raw = open(op, "rb").read()
+    assert raw[:8] == b"MGPTBLK1", "bad reference block output"
+    off = 8 + 16
+
+    def take(dtype, n):
+        nonlocal off
+        a = np.frombuffer(raw, dtype=dtype, count=n, offset=off).copy()
+        off += 4 * n
+        return a
+
+    A = N * k
+    ref = {"out": take(np.float32, N * Cc).reshape(N, Cc),
+           "xn": take(np.float32, N * Cc).reshape(N, Cc), "rstd": take(np.float32, N),
+           "idx": take(np.int32, A).reshape(N, k), "topp": take(np.float32, A).reshape(N, k),
+           "counts": take(np.int32, E), "perm": take(np.int32, A)}
+    assert off == len(raw)
+    rows = C.sample_rows(N)
+    fx = {"rows": rows, "out_rows": ref["out"][rows], "xn_rows": ref["xn"][rows],
+          "rstd": ref["rstd"], "counts": ref["counts"]}
+    for n in ("out", "xn", "rstd", "idx", "topp", "perm"):
+        fx["sha_" + n] = np.array(canonical_digest(ref[n]))
+    if case.full_arrays:
+        for n in ("idx", "topp", "perm"):
+            fx[n] = ref[n]
+    os.makedirs(os.path.join(HERE, "block"), exist_ok=True)
+    np.savez_compressed(os.path.join(HERE, "block", case.name + ".npz"), **fx)
+    print(f"{case.name} block ({time.time() - t0:.1f}s)", flush=True)
+
+
 def make_case(case: C.Case) -> None:
     t0 = time.time()
     inp = C.build_inputs(case)
@@ -190,6 +240,10 @@ def main(argv):
     if argv and argv[0] == "--backward":
         for n in argv[1:] or C.BACKWARD_CASES:
             make_backward(C.ALL_CASES[n])
+        return
+    if argv and argv[0] == "--block":
+        for n in argv[1:] or C.BLOCK_CASES:
+            make_block(C.ALL_CASES[n])
         return
     names = argv or list(C.ALL_CASES)
     for n in names:

@@ -41,6 +41,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_rmsnorm.argtypes = [i, i, ctypes.c_float, vp, vp]
         L.oracle_moe_backward.argtypes = [i] * 5 + [vp] * 19
         L.oracle_moe_backward.restype = i
+        L.oracle_rmsnorm_scaled.argtypes = [i, i, ctypes.c_float, vp, vp, vp, vp]
+        L.oracle_moe_block.argtypes = [i] * 5 + [ctypes.c_float] + [vp] * 17
+        L.oracle_moe_block.restype = i
         _LIB = L
     return _LIB
 
@@ -156,6 +159,32 @@ def backward(inp, dy, library=None) -> dict:
         out[name] = np.zeros(a.shape, np.float32)
     rc = (library or lib()).oracle_moe_backward(N, C, H, E, k, *[_p(a) for a in arrs], _p(dy),
                                    _p(out["dx"]), *[_p(out[n]) for n in GRAD_NAMES])
+    assert rc == 0
+    return out
+
+
+def rmsnorm_scaled(x, gamma, eps=1e-5):
+    """(RMSNorm(x) * gamma, rstd) as the engine's RMSNormLayer computes them."""
+    x, gamma = _f32(x), _f32(gamma)
+    out = np.empty_like(x)
+    rstd = np.empty(x.shape[0], np.float32)
+    lib().oracle_rmsnorm_scaled(x.shape[0], x.shape[1], eps, _p(x), _p(gamma), _p(out), _p(rstd))
+    return out, rstd
+
+
+def block(inp, x1, gamma, eps=1e-5) -> dict:
+    """The fused block out = x1 + MoE(RMSNorm(x1) * gamma) with its routing."""
+    cfg = inp.cfg
+    N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
+    x1, gamma = _f32(x1), _f32(gamma)
+    arrs = [_f32(a) for a in (inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu, inp.Wd, inp.bd)]
+    out = {"out": np.empty((N, C), np.float32), "xn": np.empty((N, C), np.float32),
+           "rstd": np.empty(N, np.float32), "idx": np.empty((N, k), np.int32),
+           "topp": np.empty((N, k), np.float32), "counts": np.empty(E, np.int32),
+           "perm": np.empty(N * k, np.int32)}
+    rc = lib().oracle_moe_block(N, C, H, E, k, eps, _p(x1), _p(gamma), *[_p(a) for a in arrs],
+                                *[_p(out[n]) for n in ("out", "xn", "rstd", "idx", "topp",
+                                                       "counts", "perm")])
     assert rc == 0
     return out
 
