@@ -16,7 +16,13 @@ bounded sample of the same workload on this host.
 also keeps the backward's caches, then the backward with dy ~ N(0,1)):
 tokens/s of forward + backward, the forward and backward stage times, the
 roofline of the backward's dominant GEMM, and the reference's CPU forward +
-backward on a sample.  The driver's headline line is the default forward.
+backward on a sample.
+
+--pass block measures the fused MoE half of a transformer block,
+out = x + MoE(RMSNorm(x) * gamma) (mgpt_moe_forward_block), beside the same
+computation unfused (torch RMSNorm, the layer forward, torch add) on the
+same inputs, and the reference's CPU RMSNormLayer + MoELayer + add.  The
+driver's headline line is the default forward.
 """
 from __future__ import annotations
 
@@ -36,6 +42,8 @@ PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
 METRIC_TRAIN = ("MoE layer training tokens/s, forward + backward "
+                "(N=16384,C=1024,E=16,k=2)")
+METRIC_BLOCK = ("MoE block tokens/s, out = x + MoE(RMSNorm(x) * gamma) "
                 "(N=16384,C=1024,E=16,k=2)")
 CALIB_MIB = 512               # known-size elementwise copy for counter calibration
 
@@ -119,15 +127,20 @@ def summarize_traffic(fetch_dir: str, write_dir: str, workload: str, commands) -
             "kernels": kern, "commands": commands}
 
 
-def cpu_baseline(cfg, sample_tokens: int, reps: int, train: bool = False):
-    """The reference's own CPU MoE forward (train: forward + backward)
+def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
+    """The reference's own CPU MoE forward (train: forward + backward; block:
+    ln2 RMSNormLayer + forward + residual add)
     (oracle/_ref/ref_driver, built from the unmodified reference sources),
     single-threaded as the reference is, on `sample_tokens` tokens of the
     workload's shape."""
     drv = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
     if not os.path.exists(drv):
         return None
-    cmd = [drv, "bench_train" if train else "bench", str(sample_tokens), str(cfg.C), str(cfg.H),
+    sub = {"forward": "bench", "train": "bench_train", "block": "bench_block"}[mode]
+    what = {"forward": "MoELayer::forward_into",
+            "train": "MoELayer::forward_into + backward_into",
+            "block": "RMSNormLayer::forward_into + MoELayer::forward_into + Tensor::add_into"}[mode]
+    cmd = [drv, sub, str(sample_tokens), str(cfg.C), str(cfg.H),
            str(cfg.E), str(cfg.k), str(reps)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     if r.returncode != 0:
@@ -143,7 +156,7 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int, train: bool = False):
         "kind": "reference",
         "sample": (f"{sample_tokens} of {cfg.N} tokens at the workload's shape "
                    f"(C={cfg.C}, E={cfg.E}, k={cfg.k}, H={cfg.H}), fp32 reference CPU path "
-                   f"({'MoELayer::forward_into + backward_into' if train else 'MoELayer::forward_into'}), "
+                   f"({what}), "
                    f"1 warmup + median of {reps}; "
                    f"1 thread of {os.cpu_count()} visible cores, {model}"),
         "median_s": res["median_s"],
@@ -224,8 +237,10 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pass", dest="mode", choices=["forward", "train"], default="forward",
-                    help="forward (default, the headline) or train (forward + backward)")
+    ap.add_argument("--pass", dest="mode", choices=["forward", "train", "block"],
+                    default="forward",
+                    help="forward (default, the headline), train (forward + backward) or "
+                         "block (RMSNorm + MoE + residual, fused)")
     ap.add_argument("--calib-copy", action="store_true",
                     help=f"after the timed run, copy {CALIB_MIB} MiB with an elementwise kernel 3 "
                          "times (known-size traffic for calibrating FETCH_SIZE/WRITE_SIZE)")
@@ -271,16 +286,34 @@ def main() -> int:
     y = torch.empty_like(x)
     del inp
     train = args.mode == "train"
+    block = args.mode == "block"
     if train:
         g = torch.Generator(device="cpu").manual_seed(7)
         dy = torch.randn(x.shape, generator=g).to(dev).to(dt)
         dx = torch.empty_like(x)
+    if block:
+        # x1: the workload's rows scaled per token by 0.25 .. 4; gamma ~ 1 + 0.2 N(0,1)
+        g = torch.Generator(device="cpu").manual_seed(13)
+        scale = torch.exp2(torch.randint(-2, 3, (x.shape[0], 1), generator=g).float())
+        x = (x.float() * scale.to(dev)).to(dt)
+        gamma = (1.0 + 0.2 * torch.randn(cfg.C, generator=g)).to(dev)
+        eps = 1e-5
     print(f"setup {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
     def step():
+        if block:
+            layer.forward_block_into(x, gamma, eps, y)
+            return
         layer.forward_into(x, y, train)
         if train:
             layer.backward_into(dy, dx)
+
+    def unfused_step():
+        # the same block unfused: torch RMSNorm in fp32, the layer, torch add
+        xf = x.float()
+        xn = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * gamma).to(dt)
+        layer.forward_into(xn, y)
+        y.add_(x)
 
     for _ in range(args.warmup):
         step()
@@ -387,7 +420,24 @@ def main() -> int:
                 "peak": peak_mm, "unit": "TFLOP/s", "frac": round(rates[dom] / peak_mm, 4),
                 "traffic": None},
         })
-    traffic = None if train else load_traffic(cfg)
+    if block:
+        for _ in range(args.warmup):
+            unfused_step()
+        torch.cuda.synchronize()
+        start.record()
+        for _ in range(args.steps):
+            unfused_step()
+        stop.record()
+        torch.cuda.synchronize()
+        ms_unfused = start.elapsed_time(stop) / args.steps
+        result.update({
+            "metric": METRIC_BLOCK,
+            "pass": "block (mgpt_moe_forward_block: RMSNorm in the router, residual in combine)",
+            "value": round(N / (ms_per_step * 1e-3), 1),
+            "unfused_ms_per_step": round(ms_unfused, 4),
+            "unfused": "torch fp32 RMSNorm -> bf16, mgpt_moe_forward, torch add (same inputs)",
+        })
+    traffic = None if (train or block) else load_traffic(cfg)
     if traffic:
         gu = traffic["kernels"].get("gemm_gateup")
         result["roofline"]["traffic"] = gu["hbm_bytes"] if gu else None
@@ -407,7 +457,7 @@ def main() -> int:
     if not args.no_cpu_baseline:
         print("cpu baseline ...", file=sys.stderr, flush=True)
         tokens = min(args.cpu_tokens // 4 if train else args.cpu_tokens, N)
-        result["cpu_baseline"] = cpu_baseline(cfg, tokens, args.cpu_reps, train)
+        result["cpu_baseline"] = cpu_baseline(cfg, tokens, args.cpu_reps, args.mode)
     print(json.dumps(result))
     return 0
 

@@ -223,6 +223,55 @@ int mgpt_moe_export_fp8(const mgpt_moe* h, int expert, int which,
  * so tests can compare it bit for bit with the host expf. */
 int mgpt_moe_device_expf(const float* d_in, float* d_out, int n, void* stream);
 
+/* ---- GPT checkpoint (.bin) weight path --------------------------------
+ * The engine's checkpoint is GPT::save_weights_bin's file (nn/GPT.cpp:128-155):
+ * int32 vocab_size, max_seq_len, embed_dim, num_layers, completed_steps,
+ * then every parameter as float32 in GPT::get_parameters() order
+ * (nn/GPT.cpp:115-126): tok_emb [V,C]; per block (TransformerBlock.cpp:105-112)
+ * ln1 scale [C], attention W_QKV [C,3C], b_QKV [3C], W_O [C,C], b_O [C]
+ * (MultiHeadAttentionLayer.cpp:178-189), ln2 scale [C], then the block's
+ * 2 + 6E MoE parameters (as in mgpt_moe_load_parameters); ln_f scale and
+ * shift [C]; lm_head W [C,V], b [V].  Older files have no completed_steps:
+ * as GPT::load_weights_bin (nn/GPT.cpp:157-206) decides, the fifth integer
+ * is read only when the file holds at least 5 ints plus every parameter. */
+typedef struct mgpt_gpt_bin_info {
+  int32_t vocab_size, max_seq_len, embed_dim, num_layers;
+  int32_t completed_steps;    /* 0 for a 4-int header */
+  int32_t header_ints;        /* 4 or 5 */
+  int64_t file_bytes;
+  int64_t param_floats;       /* every parameter of the model, in floats */
+  int64_t block_floats;       /* one transformer block's parameters */
+  int64_t moe_floats;         /* one block's 2 + 6E MoE parameters */
+} mgpt_gpt_bin_info;
+
+/* Reads a checkpoint's header and checks that its size fits a GPT with
+ * num_experts experts of hidden size hidden_dim (> 0, or -1 for 4*C as
+ * GPTConfig::default_hidden_scale gives, nn/GPT.cpp:9-10); these two are not
+ * in the file.  The file must hold exactly 4 or 5 ints plus every
+ * parameter, else MGPT_ERR_INVALID_ARGUMENT (the reference reads a short file
+ * short and ignores trailing bytes without a word; exact sizes also catch a
+ * wrong E or H).  Host only: no device call. */
+int mgpt_gpt_bin_inspect(const char* path, int num_experts, int hidden_dim,
+                         mgpt_gpt_bin_info* info);
+
+/* Copies block `layer`'s ln2 scale (ln2_gamma: C floats, may be NULL) and
+ * its 2 + 6E MoE parameters (moe_params: info.moe_floats floats, in
+ * get_parameters() order and reference layouts, back to back as
+ * mgpt_moe_load_parameters' pointers would address them) from the
+ * checkpoint into host memory, reading only that block's bytes.  Replaces,
+ * for this block, the parameter reads of GPT::load_weights_bin
+ * (nn/GPT.cpp:194-203).  Host only. */
+int mgpt_gpt_bin_read_block(const char* path, int num_experts, int hidden_dim, int layer,
+                            float* ln2_gamma, float* moe_params, size_t moe_floats);
+
+/* Loads block `layer`'s MoE parameters from the checkpoint into the handle
+ * (its C, H, E; the file's embed_dim must equal C) and packs / quantises
+ * them once, as mgpt_moe_load_parameters does; ln2_gamma (host, C floats,
+ * may be NULL) receives the block's ln2 scale for mgpt_moe_forward_block.
+ * Synchronous with respect to `stream`'s prior work. */
+int mgpt_moe_load_gpt_bin(mgpt_moe* h, const char* path, int layer, float* ln2_gamma,
+                          void* stream);
+
 /* Description of the last error on this host thread ("" if none). */
 const char* mgpt_moe_last_error(void);
 

@@ -20,7 +20,7 @@ LIB = os.path.join(HERE, "lib")
 OBJ = os.path.join(HERE, "_build")
 
 HIP_SOURCES = ["router.hip", "dispatch.hip", "gemm.hip", "gemm_dma.hip", "gemm_decode.hip", "combine.hip",
-               "pack.hip", "backward.hip", "wgrad.hip", "moe_capi.hip"]
+               "pack.hip", "backward.hip", "wgrad.hip", "moe_capi.hip", "checkpoint.cpp"]
 ARCH = os.environ.get("MGPT_OFFLOAD_ARCH", "gfx950")
 
 # -ffp-contract=off: the router must round every product and sum separately
@@ -52,7 +52,7 @@ def build_hip(verbose: bool = False) -> str:
     objs = []
     cmds = []
     for src in HIP_SOURCES:
-        obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+        obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
         objs.append(obj)
         cmds.append([hipcc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     with cf.ThreadPoolExecutor(max_workers=min(8, len(cmds))) as ex:

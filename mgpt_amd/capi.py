@@ -42,6 +42,14 @@ class Routing(ctypes.Structure):
                 ("slot_of", ctypes.c_void_p)]
 
 
+class GptBinInfo(ctypes.Structure):
+    _fields_ = [("vocab_size", ctypes.c_int32), ("max_seq_len", ctypes.c_int32),
+                ("embed_dim", ctypes.c_int32), ("num_layers", ctypes.c_int32),
+                ("completed_steps", ctypes.c_int32), ("header_ints", ctypes.c_int32),
+                ("file_bytes", ctypes.c_int64), ("param_floats", ctypes.c_int64),
+                ("block_floats", ctypes.c_int64), ("moe_floats", ctypes.c_int64)]
+
+
 class MoEError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(f"mgpt_moe status {status}: {message}")
@@ -86,6 +94,9 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_backward_stage_times": [vp, vp, i],
         "mgpt_moe_forward_block": [vp, vp, vp, ctypes.c_float, vp, i, vp, sz, vp],
         "mgpt_moe_get_rstd": [vp, i, vp, ctypes.POINTER(vp)],
+        "mgpt_gpt_bin_inspect": [ctypes.c_char_p, i, i, ctypes.POINTER(GptBinInfo)],
+        "mgpt_gpt_bin_read_block": [ctypes.c_char_p, i, i, i, vp, vp, sz],
+        "mgpt_moe_load_gpt_bin": [vp, ctypes.c_char_p, i, vp, vp],
     }
     for name, args in sig.items():
         f = getattr(L, name)

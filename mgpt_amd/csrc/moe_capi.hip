@@ -29,6 +29,7 @@
 #include <vector>
 
 #include "../../include/mgpt_moe.h"
+#include "capi_internal.hpp"
 #include "common.hpp"
 
 namespace mgpt {
@@ -82,9 +83,7 @@ hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const f
                               int, hipStream_t);
 }  // namespace mgpt
 
-using namespace mgpt;
-
-namespace {
+namespace mgpt {
 
 thread_local std::string g_last_error;
 
@@ -97,6 +96,12 @@ int fail(int code, const char* fmt, ...) {
   g_last_error = buf;
   return code;
 }
+
+}  // namespace mgpt
+
+using namespace mgpt;
+
+namespace {
 
 #define HIP_TRY(expr)                                                                  \
   do {                                                                                 \
@@ -489,6 +494,44 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   }
   h->loaded = true;
   return MGPT_OK;
+}
+
+int mgpt_moe_load_gpt_bin(mgpt_moe* h, const char* path, int layer, float* ln2_gamma,
+                          void* stream) {
+  if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  mgpt_gpt_bin_info info;
+  if (int rc = mgpt_gpt_bin_inspect(path, h->E, h->H, &info)) return rc;
+  if (info.embed_dim != h->C)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "%s: embed_dim %d, the handle has C = %d", path,
+                info.embed_dim, h->C);
+  std::vector<float> buf;
+  try {
+    buf.resize((size_t)info.moe_floats);
+  } catch (const std::bad_alloc&) {
+    return fail(MGPT_ERR_OUT_OF_MEMORY, "host buffer of %lld floats", (long long)info.moe_floats);
+  }
+  if (int rc = mgpt_gpt_bin_read_block(path, h->E, h->H, layer, ln2_gamma, buf.data(),
+                                       buf.size()))
+    return rc;
+  // pointers into the block's parameters, get_parameters() order
+  const size_t C = h->C, H = h->H, E = h->E;
+  std::vector<const float*> ptr;
+  const float* p = buf.data();
+  auto take = [&](size_t n) {
+    ptr.push_back(p);
+    p += n;
+  };
+  take(C * E);
+  take(E);
+  for (size_t e = 0; e < E; ++e) {
+    take(C * H);
+    take(H);
+    take(C * H);
+    take(H);
+    take(H * C);
+    take(C);
+  }
+  return mgpt_moe_load_parameters(h, ptr.data(), (int)ptr.size(), 0, stream);
 }
 
 int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes) {

@@ -13,6 +13,7 @@ libmgpt_moe.so.  There is no CPU path: a CPU tensor is rejected.
 from __future__ import annotations
 
 import ctypes
+import os
 
 import numpy as np
 import torch
@@ -77,6 +78,18 @@ class MoELayer:
                                                         int(bool(on_device)), stream))
         self._loaded = True
 
+    def load_gpt_bin(self, path: str, layer: int) -> torch.Tensor:
+        """Loads block `layer`'s MoE parameters from a GPT checkpoint written
+        by GPT::save_weights_bin (nn/GPT.cpp:128-155), reading only that
+        block's bytes, and packs them as load_parameters does.  Returns the
+        block's ln2 scale (float32 [C], host) for forward_block."""
+        gamma = np.empty(self.C, np.float32)
+        stream = torch.cuda.current_stream().cuda_stream
+        capi.check(capi.lib().mgpt_moe_load_gpt_bin(self._h, os.fsencode(path), int(layer),
+                                                     gamma.ctypes.data, stream))
+        self._loaded = True
+        return torch.from_numpy(gamma)
+
     # --------------------------------------------------------------- forward
     def workspace_bytes(self, num_tokens: int) -> int:
         n = ctypes.c_size_t()
@@ -128,12 +141,21 @@ class MoELayer:
         """out = x + MoE(RMSNorm(x) * gamma): the MoE half of a transformer
         block (ln2, mlp and the residual add of
         layers/TransformerBlock.cpp:42-46) in one fused pass."""
+        out = torch.empty_like(x)
+        self.forward_block_into(x, gamma, eps, out)
+        return out
+
+    def forward_block_into(self, x: torch.Tensor, gamma: torch.Tensor, eps: float,
+                           out: torch.Tensor) -> None:
+        """forward_block writing into a caller-provided `out` (same shape and
+        dtype as x); gamma is a float32 device tensor of C elements."""
         if not x.is_cuda or x.dtype != self.dtype or x.shape[-1] != self.C or not x.is_contiguous():
             raise ValueError("x must be a contiguous device tensor [..., C] of the layer's dtype")
+        if not out.is_cuda or out.dtype != self.dtype or out.shape != x.shape or not out.is_contiguous():
+            raise ValueError("out must be a contiguous device tensor shaped like x")
         g = gamma.detach().to(device=x.device, dtype=torch.float32).contiguous()
         if g.numel() != self.C:
             raise ValueError("gamma must have C elements")
-        out = torch.empty_like(x)
         n = x.numel() // self.C
         ws = self._workspace(n, x.device)
         stream = torch.cuda.current_stream(x.device).cuda_stream
@@ -142,7 +164,6 @@ class MoELayer:
                                                      ws.data_ptr(), ws.numel(), stream))
         self._last_n = n
         self._train_x = None
-        return out
 
     def rstd(self) -> torch.Tensor:
         """Device view [N] of the per-token 1/rms of the last forward_block."""

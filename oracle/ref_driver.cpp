@@ -11,6 +11,8 @@
 //   ref_driver block <in.bin> <gamma.bin> <out.bin>
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
 //   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (forward + backward)
+//   ref_driver bench_block <N> <C> <H> <E> <k> <reps>   (ln2 + MoE + residual)
+//   ref_driver gptbin <out.bin> <side.bin> V S C L heads E k H steps seed
 //
 // in.bin : "MGPTMOE1", int32 N C H E k, then float32 x[N*C] and the 2+6E
 //          parameters in MoELayer::get_parameters() order
@@ -29,7 +31,16 @@
 //          every parameter in get_parameters() order (sizes as in in.bin),
 //          after one forward_into and one backward_into
 //          (layers/MoELayer.cpp:130-223) on a fresh layer.
+// gptbin : a GPT checkpoint written by the reference's own
+//          GPT::save_weights_bin (nn/GPT.cpp:128-155) for GPTConfig{V, S, C,
+//          L, heads, hidden_dim H, E, k}, every parameter a seeded normal
+//          (std 0.3; RMSNorm scales 1 + 0.2 N(0,1)) rounded to a multiple of
+//          1/64; side.bin: "MGPTGBS1",
+//          int32 V S C L E k H steps, then per block its ln2 scale [C] and
+//          its MoE parameters in get_parameters() order, read from the live
+//          layers (not from file offsets).
 #include <algorithm>
+#include <fstream>
 #include <chrono>
 #include <cmath>
 #include <cstddef>
@@ -53,6 +64,7 @@
 #include "MoELayer.h"
 #include "RMSNormLayer.h"
 #undef private
+#include "GPT.h"
 
 namespace {
 
@@ -193,10 +205,15 @@ int block(const char* in_path, const char* g_path, const char* out_path) {
 }
 
 // Times MoELayer::forward_into (train: forward_into then backward_into with
-// dout ~ N(0,1)) on one fresh layer (its CPU caches are sized on first use
-// and never resized, layers/MoELayer.cpp:42-50): 1 warmup, then `reps`
-// timed runs; prints one JSON line with every run and the median.
-int bench(int N, int C, int H, int E, int k, int reps, bool train) {
+// dout ~ N(0,1); block: ln2 RMSNormLayer, MoELayer and the residual
+// Tensor::add_into of layers/TransformerBlock.cpp:42-46) on one fresh layer
+// (its CPU caches are sized on first use and never resized,
+// layers/MoELayer.cpp:42-50): 1 warmup, then `reps` timed runs; prints one
+// JSON line with every run and the median.
+enum BenchPass { kBenchForward, kBenchTrain, kBenchBlock };
+
+int bench(int N, int C, int H, int E, int k, int reps, BenchPass pass) {
+  const bool train = pass == kBenchTrain;
   std::mt19937 gen(20261201u);
   std::normal_distribution<float> nd(0.0f, 1.0f);
   Tensor x({1, N, C}, 0.0f, Device::CPU);
@@ -210,10 +227,18 @@ int bench(int N, int C, int H, int E, int k, int reps, bool train) {
   MoELayer layer(C, H, E, k);
   for (Tensor* p : layer.get_parameters())
     for (auto& v : p->data) v = 0.02f * nd(gen);
-  Tensor y, dx;
+  Tensor y, dx, xn, out;
   Tensor dy({1, N, C}, 0.0f, Device::CPU);
   for (auto& v : dy.data) v = nd(gen);
+  RMSNormLayer ln2(C);
+  for (auto& v : ln2.get_parameters()[0]->data) v = 1.0f + 0.2f * nd(gen);
   auto step = [&]() {
+    if (pass == kBenchBlock) {
+      ln2.forward_into(x, xn);
+      layer.forward_into(xn, y);
+      Tensor::add_into(x, y, out);
+      return;
+    }
     layer.forward_into(x, y);
     if (train) layer.backward_into(dy, dx);
   };
@@ -230,9 +255,48 @@ int bench(int N, int C, int H, int E, int k, int reps, bool train) {
   double med = s[s.size() / 2];
   std::printf("{\"pass\": \"%s\", \"N\": %d, \"C\": %d, \"H\": %d, \"E\": %d, \"k\": %d, "
               "\"reps\": %d, \"median_s\": %.6f, \"runs_s\": [",
-              train ? "forward+backward" : "forward", N, C, H, E, k, reps, med);
+              train ? "forward+backward" : pass == kBenchBlock ? "block" : "forward", N, C, H,
+              E, k, reps, med);
   for (size_t i = 0; i < t.size(); ++i) std::printf("%s%.6f", i ? ", " : "", t[i]);
   std::printf("], \"tokens_per_s\": %.3f, \"threads\": 1}\n", N / med);
+  return 0;
+}
+
+int gptbin(const char* bin_path, const char* side_path, int V, int S, int C, int L, int heads,
+           int E, int k, int H, int steps, unsigned seed) {
+  GPTConfig cfg;
+  cfg.vocab_size = V;
+  cfg.max_seq_len = S;
+  cfg.embed_dim = C;
+  cfg.num_layers = L;
+  cfg.num_heads = heads;
+  cfg.hidden_dim = H;
+  cfg.num_experts = E;
+  cfg.top_k = k;
+  GPT gpt(cfg);
+  std::mt19937 gen(seed);
+  std::normal_distribution<float> nd(0.0f, 1.0f);
+  // values on a 1/64 grid, so the committed checkpoint compresses well
+  auto grid = [](float v) { return std::round(v * 64.0f) / 64.0f; };
+  for (Tensor* p : gpt.get_parameters())
+    for (auto& v : p->data) v = grid(0.3f * nd(gen));
+  for (auto& b : gpt.blocks) {
+    for (auto& v : b->ln1.get_parameters()[0]->data) v = 1.0f + grid(0.2f * nd(gen));
+    for (auto& v : b->ln2.get_parameters()[0]->data) v = 1.0f + grid(0.2f * nd(gen));
+  }
+  gpt.save_weights_bin(bin_path, steps);
+  FILE* o = std::fopen(side_path, "wb");
+  if (!o) { std::perror(side_path); return 2; }
+  const int32_t dims[8] = {V, S, C, L, E, k, H, steps};
+  std::fwrite("MGPTGBS1", 1, 8, o);
+  std::fwrite(dims, sizeof(int32_t), 8, o);
+  for (auto& b : gpt.blocks) {
+    const Tensor* g = b->ln2.get_parameters()[0];
+    std::fwrite(g->data.data(), sizeof(float), g->data.size(), o);
+    for (Tensor* p : b->mlp.get_parameters())
+      std::fwrite(p->data.data(), sizeof(float), p->data.size(), o);
+  }
+  std::fclose(o);
   return 0;
 }
 
@@ -242,11 +306,19 @@ int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
   if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
   if (argc == 5 && std::string(argv[1]) == "block") return block(argv[2], argv[3], argv[4]);
-  if (argc == 8 && (std::string(argv[1]) == "bench" || std::string(argv[1]) == "bench_train"))
+  if (argc == 14 && std::string(argv[1]) == "gptbin")
+    return gptbin(argv[2], argv[3], std::atoi(argv[4]), std::atoi(argv[5]), std::atoi(argv[6]),
+                  std::atoi(argv[7]), std::atoi(argv[8]), std::atoi(argv[9]), std::atoi(argv[10]),
+                  std::atoi(argv[11]), std::atoi(argv[12]), (unsigned)std::atol(argv[13]));
+  if (argc == 8 && (std::string(argv[1]) == "bench" || std::string(argv[1]) == "bench_train" ||
+                    std::string(argv[1]) == "bench_block"))
     return bench(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]),
                  std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]),
-                 std::string(argv[1]) == "bench_train");
+                 std::string(argv[1]) == "bench_train"   ? kBenchTrain
+                 : std::string(argv[1]) == "bench_block" ? kBenchBlock
+                                                         : kBenchForward);
   std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | "
-                       "block <in> <gamma> <out> | bench[_train] N C H E k reps\n");
+                       "block <in> <gamma> <out> | bench[_train|_block] N C H E k reps | "
+                       "gptbin <out> <side> V S C L heads E k H steps seed\n");
   return 1;
 }

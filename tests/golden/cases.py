@@ -145,3 +145,11 @@ def sample_rows(N: int, n: int = 32) -> np.ndarray:
     if N <= n:
         return np.arange(N, dtype=np.int32)
     return np.unique(np.linspace(0, N - 1, n).round().astype(np.int32))
+
+
+# A small MoE GPT checkpoint written by the reference's GPT::save_weights_bin
+# (tests/golden/gptbin/small.npz): vocab V, max_seq_len S, embed_dim C,
+# L blocks, heads, E experts, top-k, hidden H, completed_steps, seed.
+GPTBIN = {"V": 16, "S": 32, "C": 64, "L": 2, "heads": 2, "E": 4, "k": 2, "H": 64,
+          "steps": 7, "seed": 20261202}
+

@@ -29,7 +29,13 @@ Tensor::add_into (ref_driver block) on cases.BLOCK_CASES with
 tests/golden/block/<case>.npz with sha256 digests of out, xn, rstd, idx,
 topp, perm, the counts, sampled rows of out and xn, and rstd in full.
 
-Usage: python tests/golden/make_golden.py [--backward | --block] [case ...]
+With --gptbin it has the reference write a small MoE GPT checkpoint with its
+own GPT::save_weights_bin (ref_driver gptbin; cases.GPTBIN's dimensions,
+seeded parameters) and stores tests/golden/gptbin/small.npz with the file's
+bytes and, per block, sha256 digests of its ln2 scale and of its 2 + 6E MoE
+parameters as the live layers held them (not located by file offsets).
+
+Usage: python tests/golden/make_golden.py [--backward | --block | --gptbin] [case ...]
 (default: all cases)
 """
 from __future__ import annotations
@@ -213,6 +219,34 @@ def make_block(case: C.Case) -> None:
     print(f"{case.name} block ({time.time() - t0:.1f}s)", flush=True)
 
 
+def make_gptbin() -> None:
+    g = C.GPTBIN
+    with tempfile.TemporaryDirectory() as d:
+        bp, sp = os.path.join(d, "model.bin"), os.path.join(d, "side.bin")
+        subprocess.run([REF, "gptbin", bp, sp] + [str(g[n]) for n in
+                        ("V", "S", "C", "L", "heads", "E", "k", "H", "steps", "seed")],
+                       check=True, stdout=subprocess.DEVNULL)
+        blob = open(bp, "rb").read()
+        side = open(sp, "rb").read()
+    assert side[:8] == b"MGPTGBS1"
+    dims = np.frombuffer(side, np.int32, 8, 8)
+    Cc, L, E, H = g["C"], g["L"], g["E"], g["H"]
+    moe = Cc * E + E + E * (2 * (Cc * H + H) + H * Cc + Cc)
+    fx = {"bin": np.frombuffer(blob, np.uint8), "dims": dims}
+    off = 40
+    for layer in range(L):
+        ln2 = np.frombuffer(side, np.float32, Cc, off)
+        off += 4 * Cc
+        params = np.frombuffer(side, np.float32, moe, off)
+        off += 4 * moe
+        fx[f"sha_ln2_{layer}"] = np.array(wl.digest(ln2))
+        fx[f"sha_moe_{layer}"] = np.array(wl.digest(params))
+    assert off == len(side)
+    os.makedirs(os.path.join(HERE, "gptbin"), exist_ok=True)
+    np.savez_compressed(os.path.join(HERE, "gptbin", "small.npz"), **fx)
+    print(f"gptbin: {len(blob)} bytes, dims {dims.tolist()}", flush=True)
+
+
 def make_case(case: C.Case) -> None:
     t0 = time.time()
     inp = C.build_inputs(case)
@@ -240,6 +274,9 @@ def main(argv):
     if argv and argv[0] == "--backward":
         for n in argv[1:] or C.BACKWARD_CASES:
             make_backward(C.ALL_CASES[n])
+        return
+    if argv and argv[0] == "--gptbin":
+        make_gptbin()
         return
     if argv and argv[0] == "--block":
         for n in argv[1:] or C.BLOCK_CASES:
