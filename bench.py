@@ -21,8 +21,15 @@ backward on a sample.
 --pass block measures the fused MoE half of a transformer block,
 out = x + MoE(RMSNorm(x) * gamma) (mgpt_moe_forward_block), beside the same
 computation unfused (torch RMSNorm, the layer forward, torch add) on the
-same inputs, and the reference's CPU RMSNormLayer + MoELayer + add.  The
-driver's headline line is the default forward.
+same inputs, and the reference's CPU RMSNormLayer + MoELayer + add.
+
+--pass decode (default config cfg5) measures the layer inside the engine's
+sampling loop (pipeline/Generator.cpp:13-36: B = 1, no KV cache, the whole
+context re-run every step, cropped to max_seq_len S = cfg.N): the growing
+phase N = 1 .. S enqueued without any host synchronisation, then
+steady-state steps at N = S, eager and replayed from one captured HIP
+graph.  value = steady-state steps/s (graph replay).  The driver's headline
+line is the default forward.
 """
 from __future__ import annotations
 
@@ -43,6 +50,8 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
 METRIC_TRAIN = ("MoE layer training tokens/s, forward + backward "
                 "(N=16384,C=1024,E=16,k=2)")
+METRIC_DECODE = ("MoE decode steps/s in the sampling loop (Generator B=1, no KV cache, "
+                 "context S=64, C=2048, E=64, k=8, H=1408, fp8 weights)")
 METRIC_BLOCK = ("MoE block tokens/s, out = x + MoE(RMSNorm(x) * gamma) "
                 "(N=16384,C=1024,E=16,k=2)")
 CALIB_MIB = 512               # known-size elementwise copy for counter calibration
@@ -237,10 +246,11 @@ def main() -> int:
     ap.add_argument("--cpu-tokens", type=int, default=4096)
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pass", dest="mode", choices=["forward", "train", "block"],
+    ap.add_argument("--pass", dest="mode", choices=["forward", "train", "block", "decode"],
                     default="forward",
-                    help="forward (default, the headline), train (forward + backward) or "
-                         "block (RMSNorm + MoE + residual, fused)")
+                    help="forward (default, the headline), train (forward + backward), "
+                         "block (RMSNorm + MoE + residual, fused) or decode (the sampling "
+                         "loop at cfg5's shape)")
     ap.add_argument("--calib-copy", action="store_true",
                     help=f"after the timed run, copy {CALIB_MIB} MiB with an elementwise kernel 3 "
                          "times (known-size traffic for calibrating FETCH_SIZE/WRITE_SIZE)")
@@ -275,6 +285,8 @@ def main() -> int:
     from mgpt_amd import workload as wl
     from mgpt_amd.moe import MoELayer
 
+    if args.mode == "decode":
+        return decode_main(args)
     cfg = wl.CONFIGS[args.config]
     dev = torch.device("cuda", 0)
     t0 = time.time()
@@ -458,6 +470,128 @@ def main() -> int:
         print("cpu baseline ...", file=sys.stderr, flush=True)
         tokens = min(args.cpu_tokens // 4 if train else args.cpu_tokens, N)
         result["cpu_baseline"] = cpu_baseline(cfg, tokens, args.cpu_reps, args.mode)
+    print(json.dumps(result))
+    return 0
+
+
+def decode_main(args) -> int:
+    """The sampling-loop measurement (--pass decode)."""
+    import torch
+
+    from mgpt_amd import workload as wl
+    from mgpt_amd.moe import MoELayer
+
+    cfg = wl.CONFIGS["cfg5" if args.config == "cfg3" else args.config]
+    S, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
+    dev = torch.device("cuda", 0)
+    inp = wl.make_inputs(cfg, seed=20261201)
+    layer = MoELayer(C, H, E, k, act=cfg.act, weights=cfg.weights)
+    layer.load_parameters(inp.params(raw=True))
+    dt = torch.float32 if cfg.act == "f32" else torch.bfloat16
+    x = torch.from_numpy(inp.x).to(dev).to(dt)
+    y = torch.empty_like(x)
+    layer.reserve(S)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def grow():
+        for n in range(1, S + 1):
+            layer.forward_into(x[:n], y[:n])
+
+    for _ in range(max(1, args.warmup)):
+        grow()
+    torch.cuda.synchronize()
+    # growing context: N = 1 .. S, the host never waits
+    t0 = time.perf_counter()
+    start.record()
+    grow()
+    stop.record()
+    host_enqueue_s = time.perf_counter() - t0
+    torch.cuda.synchronize()
+    grow_ms = start.elapsed_time(stop)
+
+    # steady state, eager (also the per-stage timing)
+    K = args.steps
+    start.record()
+    for _ in range(K):
+        layer.forward_into(x, y)
+    stop.record()
+    torch.cuda.synchronize()
+    eager_ms = start.elapsed_time(stop) / K
+    layer.set_profiling(True)
+    for _ in range(K):
+        layer.forward_into(x, y)
+    torch.cuda.synchronize()
+    stages = layer.stage_times()
+    stages.pop("forwards")
+    layer.set_profiling(False)
+    counts = layer.get_expert_counts()
+
+    # steady state, one captured HIP graph replayed
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        layer.forward_into(x, y)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        layer.forward_into(x, y)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    start.record()
+    for _ in range(K):
+        g.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    graph_ms = start.elapsed_time(stop) / K
+
+    used = sum(1 for c_ in counts if c_ > 0)
+    w = {"bf16": 2, "fp8": 1, "f32": 4}[cfg.weights]
+    gu_bytes = used * (2.0 * H * C * w + 2 * H * 4)
+    dn_bytes = used * (1.0 * H * C * w + C * 4)
+    t_gu = stages["gemm_gateup"] * 1e-3
+    result = {
+        "metric": METRIC_DECODE,
+        "value": round(1e3 / graph_ms, 1),
+        "unit": "steps/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(graph_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if cfg.act == "bf16" else "f32",
+        "data": "synthetic (seeded; mgpt_amd.workload)",
+        "pass": "decode (sampling loop: growing context, then steady state)",
+        "config": {"workload": workload_name(cfg) + f"; sampling loop, max_seq_len S={S}, B=1",
+                   "N": S, "C": C, "E": E, "k": k, "H": H, "parallelism": "single GPU"},
+        "steady_eager_ms_per_step": round(eager_ms, 4),
+        "steady_graph_ms_per_step": round(graph_ms, 4),
+        "growing_phase_ms": round(grow_ms, 4),
+        "growing_phase_steps": S,
+        "growing_phase_host_enqueue_ms": round(host_enqueue_s * 1e3, 3),
+        "stage_ms": {kk: round(v, 4) for kk, v in stages.items()},
+        "experts_used": used,
+        "weight_bytes_per_step": gu_bytes + dn_bytes,
+        "weight_stream_GBs": round((gu_bytes + dn_bytes) / (graph_ms * 1e-3) / 1e9, 1),
+        "roofline": {
+            "kernel": "gate/up fp8 weight-streaming GEMM + SwiGLU epilogue (steady-state step)",
+            "bound": "hbm", "achieved": round(gu_bytes / t_gu / 1e9, 1), "peak": PEAK_HBM_GBS,
+            "unit": "GB/s", "frac": round(gu_bytes / t_gu / 1e9 / PEAK_HBM_GBS, 4),
+            "traffic": None},
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        print("cpu baseline ...", file=sys.stderr, flush=True)
+        cb = cpu_baseline(cfg, S, args.cpu_reps, "forward")
+        if cb and "value" in cb:
+            cb = dict(cb, value=round(cb["value"] / S, 4), unit="steps/s",
+                      sample=cb["sample"] + f"; one steady-state step = {S} tokens")
+        result["cpu_baseline"] = cb
     print(json.dumps(result))
     return 0
 

@@ -91,7 +91,12 @@ int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes);
  * act_dtype, row-major, device memory; y must not alias x.  The workspace
  * (>= mgpt_moe_workspace_bytes) holds the routing of this call until the
  * next call that uses it.  num_tokens = 0 is a no-op.  Replaces
- * MoELayer::forward_into (layers/MoELayer.cpp:28-128) on the device. */
+ * MoELayer::forward_into (layers/MoELayer.cpp:28-128) on the device.
+ * No allocation, copy, memset or host synchronisation happens inside, so
+ * the call may be captured into a HIP graph (stream capture) and replayed,
+ * e.g. the fixed-length decode step of a sampling loop; under capture it
+ * records no events (no stage timing; mgpt_moe_expert_counts then reports
+ * MGPT_ERR_NOT_READY until the next eager forward). */
 int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens,
                      void* workspace, size_t workspace_bytes, void* stream);
 

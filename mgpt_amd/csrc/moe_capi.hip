@@ -568,7 +568,13 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
   ActT* xg = (ActT*)(ws + L.xg);
   ActT* hb = (ActT*)(ws + L.hbuf);
   ActT* ob = (ActT*)(ws + L.obuf);
-  const bool prof = h->profiling;
+  // Under stream capture (a HIP graph of the forward, e.g. a fixed-length
+  // decode step) the forward records no events: stage timing is off and
+  // mgpt_moe_expert_counts reports NOT_READY until an eager forward.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(st, &cap));
+  const bool capturing = cap != hipStreamCaptureStatusNone;
+  const bool prof = h->profiling && !capturing;
   hipEvent_t* evs = h->ev[h->prof_count % mgpt_moe::kProfSlots];
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
@@ -658,8 +664,12 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
   HIP_TRY(launch_combine<ActT>(ob, idx, topp, slot_of, N, C, k, blk.gamma ? x : nullptr, y, st));
   HIP_TRY(mark(5));
   if (prof) ++h->prof_count;
-  HIP_TRY(hipEventRecord(h->done, st));
-  h->done_valid = true;
+  if (capturing) {
+    h->done_valid = false;
+  } else {
+    HIP_TRY(hipEventRecord(h->done, st));
+    h->done_valid = true;
+  }
   h->last_counts = counts;
   return MGPT_OK;
 }

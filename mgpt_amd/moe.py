@@ -107,6 +107,15 @@ class MoELayer:
                                                              ctypes.byref(n)))
         return n.value
 
+    def reserve(self, max_tokens: int, train: bool = False, device=None) -> None:
+        """Allocates the workspace for up to max_tokens tokens now, so that
+        forwards of any N <= max_tokens allocate nothing: a sampling loop
+        whose context grows to max_seq_len (pipeline/Generator.cpp:13-36
+        re-runs the whole cropped context every step), or a decode step
+        captured into a HIP graph."""
+        dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+        self._workspace(max_tokens, dev, train)
+
     def _workspace(self, n: int, device, train: bool = False) -> torch.Tensor:
         need = self.train_workspace_bytes(n) if train else self.workspace_bytes(n)
         if self._ws is None or self._ws.numel() < need or self._ws.device != device:
