@@ -179,25 +179,41 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
     with open(bench_json) as f:
         b = json.loads(f.read().strip().splitlines()[-1])
     rows = list(csv.DictReader(open(stats_csv)))
-    train = str(b.get("pass", "")).startswith("train")
-    extra = " --pass train" if train else ""
+    mode = str(b.get("pass", "forward")).split(" ")[0]
+    train = mode == "train"
+    extra = "" if mode == "forward" else f" --pass {mode}"
+    cfg_arg = "" if mode == "decode" else f"--config {config} "
     cmd = (f"rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python bench.py "
-           f"--config {config}{extra} --steps {b['steps']} --warmup {b['warmup']} --no-cpu-baseline")
-    what = "training step (forward + backward)" if train else "forward"
-    unit = "training steps" if train else "forwards"
-    out = [f"# {config} MoE {what}: rocprofv3 kernel statistics (MI355X)", "",
+           f"{cfg_arg}{extra.strip()} --steps {b['steps']} --warmup {b['warmup']} "
+           "--no-cpu-baseline").replace("  ", " ")
+    what = {"train": "training step (forward + backward)",
+            "block": "fused block (RMSNorm + MoE + residual)",
+            "decode": "decode steps in the sampling loop"}.get(mode, "forward")
+    runs = {"train": f"{b['warmup'] + b['steps']} training steps ({b['warmup']} warmup + "
+                     f"{b['steps']} timed)",
+            "block": f"{b['warmup'] + b['steps']} fused block forwards and as many unfused "
+                     f"({b['warmup']} warmup + {b['steps']} timed each)",
+            "decode": f"{b['warmup'] + 1} growing loops of {b.get('growing_phase_steps')} steps "
+                      f"(N = 1 .. {b['config']['N']}), then {b['steps']} eager, {b['steps']} "
+                      f"profiled, 1 + {b['warmup'] + b['steps']} graph-replayed steady-state "
+                      "steps (kernel averages mix every N)"}.get(
+        mode, f"{b['warmup'] + b['steps']} forwards ({b['warmup']} warmup + {b['steps']} timed)")
+    out = [f"# {b['config']['workload'].split(':')[0]} MoE {what}: rocprofv3 kernel statistics "
+           "(MI355X)", "",
            "Command (repository root, on the GPU box), then "
-           "`python bench.py --config %s --summarize-stats <dir>/run_kernel_stats.csv <json line>`:"
-           % config, "", "```", cmd, "```", "",
-           f"Workload: {b['config']['workload']}.  {b['warmup'] + b['steps']} {unit} "
-           f"({b['warmup']} warmup + {b['steps']} timed); pack/pad/quantise/copy/transpose kernels "
-           "are the one-time parameter load and backward weight layouts.", "",
+           "`python bench.py --summarize-stats <dir>/run_kernel_stats.csv <json line>`:", "",
+           "```", cmd, "```", "",
+           f"Workload: {b['config']['workload']}.  {runs}; pack/pad/quantise/copy/transpose "
+           "kernels are the one-time parameter load and backward weight layouts.", "",
            "| Kernel | Stage | Calls | Average (us) | Share of GPU time |", "|---|---|---|---|---|"]
     for r in rows:
         name = r["Name"].replace("unsigned short", "bf16").replace("mgpt::(anonymous namespace)::", "")
         if len(name) > 110:
             name = name[:107] + "..."
-        out.append(f"| `{name}` | {stage_of(r['Name']) or '-'} | {r['Calls']} | "
+        st = stage_of(r["Name"]) or "-"
+        if mode == "block" and r["Name"].startswith(("void at::native", "at::native")):
+            st = "unfused (torch)"   # the unfused comparison's torch kernels
+        out.append(f"| `{name}` | {st} | {r['Calls']} | "
                    f"{float(r['AverageNs']) / 1e3:.1f} | {float(r['Percentage']):.2f}% |")
     out += ["", "HIP-event stage means measured by bench.py in the same run (ms):", "",
             "| Stage | ms |", "|---|---|"]
@@ -209,10 +225,20 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
                 f"(backward {b['backward_ms']} ms); backward products (TFLOP/s): "
                 + ", ".join(f"{k} {v}" for k, v in b["backward_gemm_tflops"].items())
                 + f"; dominant: {rf['kernel']} = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s."]
+    elif mode == "decode":
+        out += ["", f"bench.py: {b['value']:.0f} steady-state steps/s ({b['ms_per_step']} ms/step "
+                f"replayed from a HIP graph, {b['steady_eager_ms_per_step']} ms eager); growing "
+                f"loop of {b['growing_phase_steps']} steps {b['growing_phase_ms']} ms on the "
+                f"device, enqueued by the host in {b['growing_phase_host_enqueue_ms']} ms; "
+                f"{rf['kernel']}: {rf['achieved']} GB/s = {100 * rf['frac']:.1f}% of "
+                f"{rf['peak']} GB/s."]
     else:
         out += ["", f"bench.py: {b['value']:.0f} tokens/s, {b['ms_per_step']} ms/step; gate/up GEMM "
                 f"{rf['achieved']} TFLOP/s = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s dense "
                 f"bf16; both expert GEMMs {b['expert_gemm_tflops']} TFLOP/s."]
+        if mode == "block":
+            out += [f"Unfused (torch RMSNorm, the layer forward, torch add) on the same inputs: "
+                    f"{b['unfused_ms_per_step']} ms/step."]
     return "\n".join(out)
 
 

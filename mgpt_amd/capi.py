@@ -11,7 +11,9 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libmgpt_moe.so")
+# MGPT_MOE_LIB: another build of the same library (e.g. one compiled with
+# different tile constants, for measurement)
+LIB_PATH = os.environ.get("MGPT_MOE_LIB") or os.path.join(HERE, "lib", "libmgpt_moe.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "mgpt_moe.h")
 
 MGPT_OK = 0

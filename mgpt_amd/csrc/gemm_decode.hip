@@ -29,7 +29,10 @@ constexpr int kDThreads = 256;
 constexpr int kDBM = 32;                     // token rows per item
 constexpr int kDBN = 256;                    // features per item
 constexpr int kDBK = 128;                    // columns per stage
-constexpr int kDStages = 3;
+#ifndef MGPT_DECODE_STAGES
+#define MGPT_DECODE_STAGES 3
+#endif
+constexpr int kDStages = MGPT_DECODE_STAGES;   // ring depth (LDS: 40 KB a stage)
 constexpr int kWBytes = kDBN * kDBK;         // 32 KB of fp8 weights
 constexpr int kABytes = kDBM * kDBK * 2;     // 8 KB of bf16 activations
 constexpr int kDStage = kWBytes + kABytes;   // 40 KB

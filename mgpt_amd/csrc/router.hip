@@ -154,16 +154,22 @@ __device__ __forceinline__ void drain_barrier() {
 
 // LDS budget of the logit stage: two buffers of (x chunk + weight chunk).
 constexpr int kRouterLds = 96 * 1024;
+// The split path (few tokens, E > 16) has no softmax stage in its kernel and
+// spends the whole budget on the logit stage's buffers.
+#ifndef MGPT_ROUTER_SPLIT_LDS_KB
+#define MGPT_ROUTER_SPLIT_LDS_KB 96
+#endif
+constexpr int kRouterSplitLds = MGPT_ROUTER_SPLIT_LDS_KB * 1024;
 
 // LDS bytes of one group's weight chunk: whole 1 KB DMA blocks.
 __device__ __forceinline__ int wgroup_bytes(int CB, int RE) { return max(CB * RE * 4, 1024); }
 
 // Columns per chunk: the largest power of two >= 64 whose two stages fit.
 template <typename ActT>
-__device__ __forceinline__ int chunk_cols(int nw, int RE) {
+__device__ __forceinline__ int chunk_cols(int nw, int RE, int lds_bytes) {
   auto stage = [&](int cb) { return kRT * cb * (int)sizeof(ActT) + nw * wgroup_bytes(cb, RE); };
   int CB = 64;
-  while (2 * stage(2 * CB) <= kRouterLds) CB *= 2;
+  while (2 * stage(2 * CB) <= lds_bytes) CB *= 2;
   return CB;
 }
 
@@ -216,9 +222,10 @@ template <typename ActT, int RE>
 __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int n_rows,
                                              const float* __restrict__ wsrc, int g_valid, int nw,
                                              int g, int C, char* smem, float (&acc)[RE],
-                                             RowNorm nrm, float* r_out) {
+                                             RowNorm nrm, float* r_out,
+                                             int lds_bytes = kRouterLds) {
   constexpr int kPer = 16 / (int)sizeof(ActT);   // columns per 16-byte unit
-  const int CB = chunk_cols<ActT>(nw, RE);
+  const int CB = chunk_cols<ActT>(nw, RE, lds_bytes);
   const int xrow_bytes = CB * (int)sizeof(ActT);   // LDS bytes per token row
   const int x_bytes = kRT * xrow_bytes;
   const int wgb = wgroup_bytes(CB, RE);
@@ -472,7 +479,7 @@ template <typename ActT>
 __global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr1, const float* __restrict__ br,
     int N, int C, int E, float* __restrict__ logits, RowNorm nrm, float* __restrict__ rstd) {
-  __shared__ __attribute__((aligned(1024))) char smem[kRouterLds];
+  __shared__ __attribute__((aligned(1024))) char smem[kRouterSplitLds];
   const int lane = lane_id();
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
   const int e0 = blockIdx.y * kSplitExperts;
@@ -480,7 +487,8 @@ __global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
   float acc[1];
   float r = 1.0f;
   logit_chains<ActT, 1>(x + (size_t)tok0 * C, N - tok0, wr1 + (size_t)e0 * C,
-                        min(kSplitExperts, E - e0), kSplitExperts, g, C, smem, acc, nrm, &r);
+                        min(kSplitExperts, E - e0), kSplitExperts, g, C, smem, acc, nrm, &r,
+                        kRouterSplitLds);
   if (nrm.gamma && blockIdx.y == 0 && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
   const int e = e0 + g;
   if (e < E && tok0 + lane < N) logits[(size_t)(tok0 + lane) * E + e] = acc[0] + br[e];
