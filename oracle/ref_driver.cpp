@@ -13,6 +13,7 @@
 //   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (forward + backward)
 //   ref_driver bench_block <N> <C> <H> <E> <k> <reps>   (ln2 + MoE + residual)
 //   ref_driver gptbin <out.bin> <side.bin> V S C L heads E k H steps seed
+//   ref_driver gptlogits <model.bin> <heads> <E> <k> <H> <ids.bin> <out.bin>
 //
 // in.bin : "MGPTMOE1", int32 N C H E k, then float32 x[N*C] and the 2+6E
 //          parameters in MoELayer::get_parameters() order
@@ -39,6 +40,9 @@
 //          int32 V S C L E k H steps, then per block its ln2 scale [C] and
 //          its MoE parameters in get_parameters() order, read from the live
 //          layers (not from file offsets).
+// gptlogits: GPT::load_weights_bin of model.bin into the GPT its header and
+//          the given heads / E / k / H describe, then GPT::forward on the
+//          int32 token ids of ids.bin; writes the logits [T*V] float32.
 #include <algorithm>
 #include <fstream>
 #include <chrono>
@@ -300,12 +304,50 @@ int gptbin(const char* bin_path, const char* side_path, int V, int S, int C, int
   return 0;
 }
 
+int gptlogits(const char* bin, int heads, int E, int k, int H, const char* ids_path,
+              const char* out_path) {
+  int32_t hdr[4];
+  FILE* f = std::fopen(bin, "rb");
+  if (!f || std::fread(hdr, sizeof(int32_t), 4, f) != 4) { std::perror(bin); return 2; }
+  std::fclose(f);
+  GPTConfig cfg;
+  cfg.vocab_size = hdr[0];
+  cfg.max_seq_len = hdr[1];
+  cfg.embed_dim = hdr[2];
+  cfg.num_layers = hdr[3];
+  cfg.num_heads = heads;
+  cfg.num_experts = E;
+  cfg.top_k = k;
+  cfg.hidden_dim = H;
+  cfg.use_flash_attention = false;
+  GPT gpt(cfg);
+  gpt.load_weights_bin(bin);
+  FILE* fi = std::fopen(ids_path, "rb");
+  if (!fi) { std::perror(ids_path); return 2; }
+  std::vector<int32_t> ids;
+  int32_t v;
+  while (std::fread(&v, sizeof(int32_t), 1, fi) == 1) ids.push_back(v);
+  std::fclose(fi);
+  const int T = (int)ids.size();
+  Tensor in({1, T}, 0.0f, Device::CPU);
+  for (int t = 0; t < T; ++t) in.data[t] = (float)ids[t];
+  Tensor out = gpt.forward(in);
+  FILE* o = std::fopen(out_path, "wb");
+  if (!o) { std::perror(out_path); return 2; }
+  std::fwrite(out.data.data(), sizeof(float), out.data.size(), o);
+  std::fclose(o);
+  return 0;
+}
+
 }  // namespace
 
 int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
   if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
   if (argc == 5 && std::string(argv[1]) == "block") return block(argv[2], argv[3], argv[4]);
+  if (argc == 9 && std::string(argv[1]) == "gptlogits")
+    return gptlogits(argv[2], std::atoi(argv[3]), std::atoi(argv[4]), std::atoi(argv[5]),
+                     std::atoi(argv[6]), argv[7], argv[8]);
   if (argc == 14 && std::string(argv[1]) == "gptbin")
     return gptbin(argv[2], argv[3], std::atoi(argv[4]), std::atoi(argv[5]), std::atoi(argv[6]),
                   std::atoi(argv[7]), std::atoi(argv[8]), std::atoi(argv[9]), std::atoi(argv[10]),
@@ -319,6 +361,7 @@ int main(int argc, char** argv) {
                                                          : kBenchForward);
   std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | "
                        "block <in> <gamma> <out> | bench[_train|_block] N C H E k reps | "
-                       "gptbin <out> <side> V S C L heads E k H steps seed\n");
+                       "gptbin <out> <side> V S C L heads E k H steps seed | "
+                       "gptlogits <bin> heads E k H <ids> <out>\n");
   return 1;
 }

@@ -153,3 +153,8 @@ def sample_rows(N: int, n: int = 32) -> np.ndarray:
 GPTBIN = {"V": 16, "S": 32, "C": 64, "L": 2, "heads": 2, "E": 4, "k": 2, "H": 64,
           "steps": 7, "seed": 20261202}
 
+
+def gptbin_ids() -> np.ndarray:
+    """Token ids of the checkpoint's GPT forward: 24 tokens < V."""
+    return ((7 * np.arange(24) + 3) % GPTBIN["V"]).astype(np.int32)
+

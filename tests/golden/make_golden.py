@@ -32,8 +32,10 @@ topp, perm, the counts, sampled rows of out and xn, and rstd in full.
 With --gptbin it has the reference write a small MoE GPT checkpoint with its
 own GPT::save_weights_bin (ref_driver gptbin; cases.GPTBIN's dimensions,
 seeded parameters) and stores tests/golden/gptbin/small.npz with the file's
-bytes and, per block, sha256 digests of its ln2 scale and of its 2 + 6E MoE
-parameters as the live layers held them (not located by file offsets).
+bytes, per block sha256 digests of its ln2 scale and of its 2 + 6E MoE
+parameters as the live layers held them (not located by file offsets), and
+the logits of the reference's whole GPT::forward (after its own
+GPT::load_weights_bin of that file) on cases.gptbin_ids().
 
 Usage: python tests/golden/make_golden.py [--backward | --block | --gptbin] [case ...]
 (default: all cases)
@@ -226,13 +228,19 @@ def make_gptbin() -> None:
         subprocess.run([REF, "gptbin", bp, sp] + [str(g[n]) for n in
                         ("V", "S", "C", "L", "heads", "E", "k", "H", "steps", "seed")],
                        check=True, stdout=subprocess.DEVNULL)
+        ids = C.gptbin_ids()
+        ip, lp = os.path.join(d, "ids.bin"), os.path.join(d, "logits.bin")
+        ids.tofile(ip)
+        subprocess.run([REF, "gptlogits", bp] + [str(g[n]) for n in ("heads", "E", "k", "H")]
+                       + [ip, lp], check=True, stdout=subprocess.DEVNULL)
+        logits = np.fromfile(lp, np.float32).reshape(len(ids), g["V"])
         blob = open(bp, "rb").read()
         side = open(sp, "rb").read()
     assert side[:8] == b"MGPTGBS1"
     dims = np.frombuffer(side, np.int32, 8, 8)
     Cc, L, E, H = g["C"], g["L"], g["E"], g["H"]
     moe = Cc * E + E + E * (2 * (Cc * H + H) + H * Cc + Cc)
-    fx = {"bin": np.frombuffer(blob, np.uint8), "dims": dims}
+    fx = {"bin": np.frombuffer(blob, np.uint8), "dims": dims, "logits": logits}
     off = 40
     for layer in range(L):
         ln2 = np.frombuffer(side, np.float32, Cc, off)

@@ -9,6 +9,9 @@ runs the engine's MoE shape and backward test, full forwards whose outputs
 are compared with the oracle (fp32: 1e-5) and whose expert counts must equal
 the reference fixture's, and full backwards whose din and parameter
 gradients are compared with the oracle's backward (fp32: 1e-5).
+tests/engine/_build/gpt_main -- the engine's whole GPT with the drop-in as
+every block's MoE -- loads a reference-written checkpoint with the engine's
+own GPT::load_weights_bin and must reproduce the reference GPT's logits.
 """
 import os
 import re
@@ -130,3 +133,34 @@ def test_engine_backward_matches_reference(name):
         worst = max(worst, rel, np.abs(dd).max() / scale)
     print(f"{name}: worst per-tensor error {worst:.3e}")
     assert worst <= 1e-5
+
+
+GPT_BIN = os.path.join(HERE, "engine", "_build", "gpt_main")
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.exists(GPT_BIN), reason="engine GPT test binary not built")
+def test_engine_gpt_loads_checkpoint_and_matches_reference_logits(tmp_path):
+    """The engine's whole GPT (its own sources: embedding, attention, norms,
+    LM head) with the drop-in as every block's MoE: GPT::load_weights_bin
+    fills the drop-in's tensors from a checkpoint the reference wrote, and
+    GPT::forward gives the reference's logits (its own GPT with its own
+    MoELayer on the same file and tokens, tests/golden/gptbin/small.npz)
+    to 1e-5 normwise and elementwise (fp32 handles)."""
+    import gptbin_case as G
+    g = C.GPTBIN
+    fx = G.fixture()
+    path = G.write_bin(tmp_path)
+    ids = os.path.join(str(tmp_path), "ids.bin")
+    out = os.path.join(str(tmp_path), "logits.bin")
+    C.gptbin_ids().tofile(ids)
+    print("gpt_main logits", flush=True)
+    r = subprocess.run([GPT_BIN, "logits", path] + [str(g[n]) for n in ("heads", "E", "k", "H")]
+                       + [ids, out], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0, r.stdout + r.stderr
+    got = np.fromfile(out, np.float32).reshape(fx["logits"].shape)
+    ref = fx["logits"]
+    rel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    mx = np.abs(got - ref).max() / np.abs(ref).max()
+    print(f"GPT logits: normwise {rel:.3e} max/max {mx:.3e}")
+    assert rel <= 1e-5 and mx <= 1e-5
