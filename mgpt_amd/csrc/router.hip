@@ -154,6 +154,9 @@ __device__ __forceinline__ void drain_barrier() {
 
 // LDS budget of the logit stage: two buffers of (x chunk + weight chunk).
 constexpr int kRouterLds = 96 * 1024;
+#ifndef MGPT_SOFTMAX_THREADS
+#define MGPT_SOFTMAX_THREADS 1024   // threads of the split path's softmax block
+#endif
 // The split path (few tokens, E > 16) has no softmax stage in its kernel and
 // spends the whole budget on the logit stage's buffers.
 #ifndef MGPT_ROUTER_SPLIT_LDS_KB
@@ -535,7 +538,8 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
                        dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
                        dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits, nrm,
                        rstd);
-    hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(1024), 0, stream, logits, N, E, k,
+    hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(MGPT_SOFTMAX_THREADS), 0, stream,
+                       logits, N, E, k,
                        topk_idx, topk_p, hist, nb, probs);
     return hipGetLastError();
   }
