@@ -632,7 +632,8 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
       const int mt = (int)((A + 255) / 256) + E;
       float* part = (float*)(ws + L.partials);
       // The gate/up GEMM has ~12x more tiles than CUs at prefill shapes, so a
-      // partial last round costs little; only the down GEMM splits it.
+      // partial last round costs little; only the down GEMM splits it
+      // (splitting gate/up's last round too measured within noise at cfg2-cfg4).
       HIP_TRY(launch_gemm_dma<kEpiGateUp>(xg, (const bf16_t*)h->wgu, h->bg, h->bu, counts, E, C,
                                           2 * Hp, 2 * Hp, Hp, hb, Hp, mt, nullptr, h->num_cus,
                                           (bf16_t*)gu, 2 * Hp, st));
