@@ -113,3 +113,38 @@ def test_block_routes_like_the_unfused_composition(name):
         assert np.array_equal(r["perm"], r2["perm"])
         rel, mx = errors(out, x1 + y.float().cpu().numpy())
         assert rel <= 1e-6
+
+
+def test_block_edge_cases_and_errors():
+    """Empty input is a no-op; a null gamma, a negative eps and an output
+    that overlaps x are rejected with a status (nothing runs)."""
+    import ctypes
+    from mgpt_amd import capi
+    case = C.ALL_CASES["small_f32"]
+    inp, x1, gamma = C.build_block_inputs(case)
+    from mgpt_amd.moe import MoELayer
+    cfg = inp.cfg
+    layer = MoELayer(cfg.C, cfg.H, cfg.E, cfg.k, act="f32")
+    layer.load_parameters(inp.params(raw=True))
+    x = torch.from_numpy(x1).to("cuda")
+    g = torch.from_numpy(gamma).to("cuda")
+    empty = layer.forward_block(x[:0], g, C.BLOCK_EPS)
+    assert empty.shape == (0, cfg.C)
+    layer.reserve(cfg.N)
+    ws = layer._ws
+    out = torch.empty_like(x)
+    stream = torch.cuda.current_stream().cuda_stream
+    L = capi.lib()
+
+    def call(gp, eps, o):
+        return L.mgpt_moe_forward_block(layer._h, x.data_ptr(), gp, ctypes.c_float(eps), o,
+                                        cfg.N, ws.data_ptr(), ws.numel(), stream)
+
+    assert call(None, 1e-5, out.data_ptr()) == capi.MGPT_ERR_INVALID_ARGUMENT
+    assert call(g.data_ptr(), -1.0, out.data_ptr()) == capi.MGPT_ERR_INVALID_ARGUMENT
+    assert call(g.data_ptr(), 1e-5, x.data_ptr()) == capi.MGPT_ERR_INVALID_ARGUMENT
+    assert call(g.data_ptr(), 1e-5, out.data_ptr()) == capi.MGPT_OK
+    torch.cuda.synchronize()
+    ref = O.block(inp, x1, gamma, C.BLOCK_EPS)
+    rel, mx = errors(out.cpu().numpy(), ref["out"])
+    assert rel <= 1e-5 and mx <= 1e-5
