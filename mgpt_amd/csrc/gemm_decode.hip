@@ -18,7 +18,8 @@
 //    ks (element e) in both operands, so a lane's weights for the stage are
 //    64 contiguous bytes of its row (four 16-byte LDS reads).
 // Same contract as gemm.hip's grouped_gemm_kernel (A = expert-contiguous
-// activations [rows][K], B = packed weights [E][Npad][K] fp8 with scales
+// activations [rows][K], B = fp8 weights in stage tiles
+// [E][Npad/256][K/128][256][128] (pack.hip: tile_fp8_kernel) with scales
 // [E][Npad], SwiGLU or bias epilogue).
 #include "common.hpp"
 
@@ -149,7 +150,9 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
   // 8w .. 8w+7 in 2 blocks of 4 rows; lane l covers row 4i + l/16, slot
   // l%16 = chunk ^ (row & 15).  Activation rows past the item's last token
   // re-read that token (in bounds, never stored).
-  const size_t wrow_g = (size_t)K;          // fp8 bytes per weight row
+  // Weights are in the tiled layout [E][Npad/256][K/128][256][128]: a
+  // stage is one contiguous 32 KB block, rows 128 bytes apart.
+  const size_t wrow_g = (size_t)kDBK;       // fp8 bytes between weight rows of a stage
   const size_t arow_g = (size_t)K * 2;      // bf16 bytes per activation row
   uint32_t woff[2];
 #pragma unroll
@@ -160,7 +163,8 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
   auto dma_stage = [&](const DItem& it, int kt, int stage) __attribute__((always_inline)) {
     const uint32_t st = lds0 + (uint32_t)(stage * kDStage);
     const char* wg = reinterpret_cast<const char*>(B) +
-                     ((size_t)it.expert * Npad + it.n0 + 64 * w) * wrow_g + (size_t)kt * kDBK;
+                     (((size_t)it.expert * nbx + it.n0 / kDBN) * KT + kt) * (size_t)kWBytes +
+                     (size_t)(64 * w) * wrow_g;
 #pragma unroll
     for (int i = 0; i < kDmaW; ++i)
       dma16(wg + (size_t)(8 * i) * wrow_g + woff[i & 1], st + (uint32_t)((w * kDmaW + i) * 1024));

@@ -77,6 +77,7 @@ hipError_t launch_transpose_pad(const T*, int, int, size_t, T*, int, int, size_t
 template <typename T, int MODE>
 hipError_t launch_wgrad(const T*, int, int, const T*, int, int, const int32_t*, int, float*,
                         float*, int, size_t, int, int, float*, float*, size_t, hipStream_t);
+hipError_t launch_tile_fp8(const uint8_t*, int, int, int, uint8_t*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
                               const float*, const int32_t*, int, int, int, int, int, bf16_t*, int,
@@ -142,6 +143,10 @@ struct mgpt_moe {
   float* br = nullptr;     // [E]
   void* wgu = nullptr;     // [E][2Hp][C] of bf16 / fp8 / f32
   void* wd = nullptr;      // [E][Cp][Hp]
+  // fp8 only: wgu and wd again in the decode stream's tiles
+  // [E][Npad/256][K/128][256][128] (null when the shape does not tile)
+  void* wgu_t = nullptr;
+  void* wd_t = nullptr;
   float* sgu = nullptr;    // fp8 scales [E][2Hp] (packed-row order)
   float* sd = nullptr;     // fp8 scales [E][Cp]
   float* bg = nullptr;     // [E][Hp]
@@ -250,12 +255,12 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_g, h->wr1, h->br,  h->wgu,  h->wd, h->sgu, h->sd,
-                  h->bg,   h->bu,  h->bd,  h->wdb, h->wgub, h->wrt};
+  void* ptrs[] = {h->wr_g, h->wr1, h->br,  h->wgu,  h->wd,   h->sgu,  h->sd, h->bg,
+                  h->bu,   h->bd,  h->wdb, h->wgub, h->wrt, h->wgu_t, h->wd_t};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   h->wr_g = h->wr1 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = h->wrt = nullptr;
-  h->wgu = h->wd = h->wdb = h->wgub = nullptr;
+  h->wgu = h->wd = h->wdb = h->wgub = h->wgu_t = h->wd_t = nullptr;
   h->loaded = false;
   h->bwd_ready = false;
 }
@@ -482,6 +487,13 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
       // Host sources are staged through one buffer: finish before reuse.
       if (!params_on_device) HIP_TRY(hipStreamSynchronize(st));
     }
+    if (rc == MGPT_OK && fp8 && C % 128 == 0 && Hp % 128 == 0 && Cp % 256 == 0) {
+      // the decode stream's contiguous 32 KB stage tiles (a second copy)
+      HIP_TRY(hipMalloc(&h->wgu_t, (size_t)E * 2 * Hp * C));
+      HIP_TRY(hipMalloc(&h->wd_t, (size_t)E * Cp * Hp));
+      HIP_TRY(launch_tile_fp8((const uint8_t*)h->wgu, E, 2 * Hp, C, (uint8_t*)h->wgu_t, st));
+      HIP_TRY(launch_tile_fp8((const uint8_t*)h->wd, E, Cp, Hp, (uint8_t*)h->wd_t, st));
+    }
   } while (0);
   hipError_t se = hipStreamSynchronize(st);
   if (rc) {
@@ -603,12 +615,13 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
     const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
     if (small_m(h, N)) {
       const int mt = (int)((A + 31) / 32) + E;
-      if (fp8 && C % 128 == 0 && (2 * Hp) % 256 == 0) {
-        // weight streaming: the persistent direct-to-LDS decode kernel
-        HIP_TRY(launch_gemm_decode<kEpiGateUp>(xg, (const fp8_t*)h->wgu, h->sgu, h->bg, h->bu,
+      if (fp8 && h->wgu_t) {
+        // weight streaming: the persistent direct-to-LDS decode kernel on the
+        // tiled copies
+        HIP_TRY(launch_gemm_decode<kEpiGateUp>(xg, (const fp8_t*)h->wgu_t, h->sgu, h->bg, h->bu,
                                                counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt, st));
         HIP_TRY(mark(3));
-        HIP_TRY(launch_gemm_decode<kEpiDown>(hb, (const fp8_t*)h->wd, h->sd, h->bd, nullptr,
+        HIP_TRY(launch_gemm_decode<kEpiDown>(hb, (const fp8_t*)h->wd_t, h->sd, h->bd, nullptr,
                                              counts, E, Hp, Cp, C, Cp, ob, C, mt, st));
       } else if (fp8) {
         HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, fp8_t, kEpiGateUp, bf16_t>(

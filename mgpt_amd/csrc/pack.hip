@@ -98,7 +98,35 @@ __global__ void pack_router_kernel(const float* __restrict__ wr, int C, int E, i
   out[i] = e < E ? wr[(size_t)c * E + e] : 0.0f;
 }
 
+// fp8 weights [E][Npad][K] -> the decode stream's tiles
+// [E][Npad/256][K/128][256][128]: every 256-row x 128-column stage the decode
+// GEMM loads is one contiguous 32 KB block.  One thread per 16-byte chunk.
+__global__ __launch_bounds__(256) void tile_fp8_kernel(const uint4* __restrict__ src, int Npad,
+                                                       int K, size_t chunks,
+                                                       uint4* __restrict__ dst) {
+  const size_t q = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= chunks) return;
+  const size_t row_chunks = (size_t)K / 16;
+  const size_t row = q / row_chunks;               // e * Npad + n
+  const int c16 = (int)(q % row_chunks);
+  const size_t e = row / Npad;
+  const int n = (int)(row % Npad);
+  const int KT = K / 128;
+  const size_t tile = (e * (size_t)(Npad / 256) + n / 256) * KT + c16 / 8;
+  dst[(tile * 256 + n % 256) * 8 + c16 % 8] = src[q];
+}
+
 }  // namespace
+
+hipError_t launch_tile_fp8(const uint8_t* src, int E, int Npad, int K, uint8_t* dst,
+                           hipStream_t stream) {
+  if (Npad % 256 != 0 || K % 128 != 0) return hipErrorInvalidValue;
+  const size_t chunks = (size_t)E * Npad * (K / 16);
+  hipLaunchKernelGGL(tile_fp8_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, stream,
+                     reinterpret_cast<const uint4*>(src), Npad, K, chunks,
+                     reinterpret_cast<uint4*>(dst));
+  return hipGetLastError();
+}
 
 // RE experts per wave group; the fused router uses router_experts_per_wave(E),
 // the split decode path RE = 1 (W_r transposed).
