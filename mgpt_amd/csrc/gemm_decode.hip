@@ -329,8 +329,12 @@ hipError_t launch_gemm_decode(const bf16_t* A, const fp8_t* B, const float* wsca
     if (e == hipSuccess) e = hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess || num_cus <= 0) num_cus = 256;
   }
+#ifndef MGPT_DECODE_BLOCKS_PER_CU
+#define MGPT_DECODE_BLOCKS_PER_CU 1
+#endif
   const int items = max_mtiles * (Npad / kDBN);
-  const int grid = items < num_cus ? items : num_cus;
+  const int slots = MGPT_DECODE_BLOCKS_PER_CU * num_cus;
+  const int grid = items < slots ? items : slots;
   hipLaunchKernelGGL((gemm_decode_kernel<EPI>), dim3(grid), dim3(kDThreads), 0, stream, A, B,
                      wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo);
   return hipGetLastError();
