@@ -51,14 +51,44 @@ struct Vec16<float> {
   }
 };
 
+// VN consecutive values of the output or residual type (VN = the values of
+// one 16-byte chunk of expert rows: 8 for bf16 rows, 4 for fp32 rows).
+template <typename T, int VN>
+struct OutVec;
+template <int VN>
+struct OutVec<bf16_t, VN> {
+  static_assert(VN == 8, "bf16 outputs come from bf16 rows");
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[VN]) {
+    Vec16<bf16_t>::unpack(*reinterpret_cast<const uint4*>(p), v);
+  }
+  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[VN]) {
+    Vec16<bf16_t>::store(p, v);
+  }
+};
+template <int VN>
+struct OutVec<float, VN> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[VN]) {
+#pragma unroll
+    for (int i = 0; i < VN; i += 4) {
+      const float4 f = *reinterpret_cast<const float4*>(p + i);
+      v[i] = f.x; v[i + 1] = f.y; v[i + 2] = f.z; v[i + 3] = f.w;
+    }
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[VN]) {
+#pragma unroll
+    for (int i = 0; i < VN; i += 4)
+      *reinterpret_cast<float4*>(p + i) = make_float4(v[i], v[i + 1], v[i + 2], v[i + 3]);
+  }
+};
+
 // Fused block: y = x1 + the MoE sum (Tensor::add_into, utils/Tensor.cpp:
 // 1579-1597, after the scatter), one rounded add per element.
-template <typename ActT>
-__device__ __forceinline__ void add_resid(const ActT* p, float (&v)[Vec16<ActT>::n]) {
-  float x[Vec16<ActT>::n];
-  Vec16<ActT>::unpack(*reinterpret_cast<const uint4*>(p), x);
+template <typename T, int VN>
+__device__ __forceinline__ void add_resid(const T* p, float (&v)[VN]) {
+  float x[VN];
+  OutVec<T, VN>::load(p, x);
 #pragma unroll
-  for (int i = 0; i < Vec16<ActT>::n; ++i) v[i] = x[i] + v[i];
+  for (int i = 0; i < VN; ++i) v[i] = x[i] + v[i];
 }
 
 constexpr int kWavesPerBlock = 4;
@@ -71,13 +101,13 @@ constexpr int kTokensPerWave2 = 1;
 // runtime k, one row at a time) and CH 16-byte chunks per lane and row.
 // With KT fixed, all TPW * KT * CH chunk loads of a wave are issued before
 // any is used, so each wave keeps them all in flight.
-template <typename ActT, int TPW, int KT, int CH>
+template <typename ActT, typename OutT, int TPW, int KT, int CH>
 __global__ __launch_bounds__(256) void combine_kernel(const ActT* __restrict__ out_rows,
                                                       const int32_t* __restrict__ topk_idx,
                                                       const float* __restrict__ topk_p,
                                                       const int32_t* __restrict__ slot_of, int N,
-                                                      int C, int k, const ActT* __restrict__ resid,
-                                                      ActT* __restrict__ y) {
+                                                      int C, int k, const OutT* __restrict__ resid,
+                                                      OutT* __restrict__ y) {
   static_assert(TPW * kMaxTopK <= kWave, "one lane per (token, choice)");
   __shared__ int s_slot[kWavesPerBlock][TPW][kMaxTopK];
   __shared__ float s_p[kWavesPerBlock][TPW][kMaxTopK];
@@ -157,8 +187,8 @@ __global__ __launch_bounds__(256) void combine_kernel(const ActT* __restrict__ o
         for (int ch = 0; ch < CH; ++ch) {
           const int c = c0 + (ch * kWave + l) * VN;
           if (c < C) {
-            if (resid) add_resid<ActT>(resid + (size_t)(t0 + u) * C + c, acc[u][ch]);
-            Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc[u][ch]);
+            if (resid) add_resid<OutT, VN>(resid + (size_t)(t0 + u) * C + c, acc[u][ch]);
+            OutVec<OutT, VN>::store(y + (size_t)(t0 + u) * C + c, acc[u][ch]);
           }
         }
   }
@@ -169,12 +199,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const ActT* __restrict__ o
 // rows are added in ascending slot order, which is ascending expert id:
 // slots are expert-major and a token's choices are distinct experts.  All
 // TPW * 2 * CH chunk loads are issued before any is used.
-template <typename ActT, int TPW, int CH>
+template <typename ActT, typename OutT, int TPW, int CH>
 __global__ __launch_bounds__(256) void combine2_kernel(const ActT* __restrict__ out_rows,
                                                        const float* __restrict__ topk_p,
                                                        const int32_t* __restrict__ slot_of, int N,
-                                                       int C, const ActT* __restrict__ resid,
-                                                       ActT* __restrict__ y) {
+                                                       int C, const OutT* __restrict__ resid,
+                                                       OutT* __restrict__ y) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int l = lane_id();
   const int t0 = (blockIdx.x * kWavesPerBlock + w) * TPW;
@@ -226,32 +256,34 @@ __global__ __launch_bounds__(256) void combine2_kernel(const ActT* __restrict__ 
         }
         const int c = c0 + (ch * kWave + l) * VN;
         if (c < C && u < nt) {
-          if (resid) add_resid<ActT>(resid + (size_t)(t0 + u) * C + c, acc);
-          Vec16<ActT>::store(y + (size_t)(t0 + u) * C + c, acc);
+          if (resid) add_resid<OutT, VN>(resid + (size_t)(t0 + u) * C + c, acc);
+          OutVec<OutT, VN>::store(y + (size_t)(t0 + u) * C + c, acc);
         }
       }
   }
 }
 
-template <typename ActT, int TPW, int KT>
+template <typename ActT, typename OutT, int TPW, int KT>
 void launch_combine_k(int chunks, hipStream_t stream, const ActT* out_rows,
                       const int32_t* topk_idx, const float* topk_p, const int32_t* slot_of, int N,
-                      int C, int k, const ActT* resid, ActT* y) {
+                      int C, int k, const OutT* resid, OutT* y) {
   const dim3 grid((N + kWavesPerBlock * TPW - 1) / (kWavesPerBlock * TPW));
   if (chunks >= 2)
-    hipLaunchKernelGGL((combine_kernel<ActT, TPW, KT, 2>), grid, dim3(256), 0, stream, out_rows,
-                       topk_idx, topk_p, slot_of, N, C, k, resid, y);
+    hipLaunchKernelGGL((combine_kernel<ActT, OutT, TPW, KT, 2>), grid, dim3(256), 0, stream,
+                       out_rows, topk_idx, topk_p, slot_of, N, C, k, resid, y);
   else
-    hipLaunchKernelGGL((combine_kernel<ActT, TPW, KT, 1>), grid, dim3(256), 0, stream, out_rows,
-                       topk_idx, topk_p, slot_of, N, C, k, resid, y);
+    hipLaunchKernelGGL((combine_kernel<ActT, OutT, TPW, KT, 1>), grid, dim3(256), 0, stream,
+                       out_rows, topk_idx, topk_p, slot_of, N, C, k, resid, y);
 }
 
 }  // namespace
 
-// resid (nullable): the fused block's residual, y = resid + sum.
-template <typename ActT>
+// resid (nullable): the fused block's residual, y = resid + sum.  ActT: the
+// expert rows; OutT: y and resid (fp32 outputs of bf16 rows keep the fp32
+// sum unrounded).
+template <typename ActT, typename OutT>
 hipError_t launch_combine(const ActT* out_rows, const int32_t* topk_idx, const float* topk_p,
-                          const int32_t* slot_of, int N, int C, int k, const ActT* resid, ActT* y,
+                          const int32_t* slot_of, int N, int C, int k, const OutT* resid, OutT* y,
                           hipStream_t stream) {
   if (N == 0) return hipSuccess;
   if (k < 1 || k > kMaxTopK) return hipErrorInvalidValue;
@@ -262,34 +294,37 @@ hipError_t launch_combine(const ActT* out_rows, const int32_t* topk_idx, const f
       const dim3 grid((N + kWavesPerBlock * kTokensPerWave2 - 1) /
                       (kWavesPerBlock * kTokensPerWave2));
       if (chunks >= 2)
-        hipLaunchKernelGGL((combine2_kernel<ActT, kTokensPerWave2, 2>), grid, dim3(256), 0,
+        hipLaunchKernelGGL((combine2_kernel<ActT, OutT, kTokensPerWave2, 2>), grid, dim3(256), 0,
                            stream, out_rows, topk_p, slot_of, N, C, resid, y);
       else
-        hipLaunchKernelGGL((combine2_kernel<ActT, kTokensPerWave2, 1>), grid, dim3(256), 0,
+        hipLaunchKernelGGL((combine2_kernel<ActT, OutT, kTokensPerWave2, 1>), grid, dim3(256), 0,
                            stream, out_rows, topk_p, slot_of, N, C, resid, y);
       break;
     }
     // fixed k: every row chunk of a token in flight at once
     case 6:
-      launch_combine_k<ActT, 1, 6>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
-                                   resid, y);
+      launch_combine_k<ActT, OutT, 1, 6>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N,
+                                         C, k, resid, y);
       break;
     case 8:
-      launch_combine_k<ActT, 1, 8>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
-                                   resid, y);
+      launch_combine_k<ActT, OutT, 1, 8>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N,
+                                         C, k, resid, y);
       break;
     default:
-      launch_combine_k<ActT, 1, 0>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N, C, k,
-                                   resid, y);
+      launch_combine_k<ActT, OutT, 1, 0>(chunks, stream, out_rows, topk_idx, topk_p, slot_of, N,
+                                         C, k, resid, y);
   }
   return hipGetLastError();
 }
 
-template hipError_t launch_combine<float>(const float*, const int32_t*, const float*,
-                                          const int32_t*, int, int, int, const float*, float*,
-                                          hipStream_t);
-template hipError_t launch_combine<bf16_t>(const bf16_t*, const int32_t*, const float*,
-                                           const int32_t*, int, int, int, const bf16_t*, bf16_t*,
-                                           hipStream_t);
+template hipError_t launch_combine<float, float>(const float*, const int32_t*, const float*,
+                                                 const int32_t*, int, int, int, const float*,
+                                                 float*, hipStream_t);
+template hipError_t launch_combine<bf16_t, bf16_t>(const bf16_t*, const int32_t*, const float*,
+                                                   const int32_t*, int, int, int, const bf16_t*,
+                                                   bf16_t*, hipStream_t);
+template hipError_t launch_combine<bf16_t, float>(const bf16_t*, const int32_t*, const float*,
+                                                  const int32_t*, int, int, int, const float*,
+                                                  float*, hipStream_t);
 
 }  // namespace mgpt

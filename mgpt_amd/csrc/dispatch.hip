@@ -83,14 +83,49 @@ __device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g
   return o;
 }
 
+// One 16-byte chunk of a gathered row (OutT) and the input bytes it comes
+// from: the same 16 bytes when the caller's rows have the gather's type, or
+// 32 bytes of fp32 rounded to 8 bf16 (RNE) when a fp32 caller feeds bf16
+// expert products.  With gamma set (fused block) the fp32 values are
+// normalised, (x * r) * gamma[c], before that rounding.
+template <typename InT, typename OutT>
+struct RowChunk {
+  static_assert(sizeof(InT) >= sizeof(OutT), "the gather only narrows");
+  static constexpr int kIn = (int)(sizeof(InT) / sizeof(OutT));   // input V16 per output V16
+  static constexpr int kPer = 16 / (int)sizeof(OutT);              // columns per chunk
+  V16 raw[kIn];
+  __device__ __forceinline__ void load(const InT* row, int q) {
+#pragma unroll
+    for (int i = 0; i < kIn; ++i) raw[i] = reinterpret_cast<const V16*>(row)[q * kIn + i];
+  }
+  __device__ __forceinline__ V16 out(float r, const float* g) const {
+    if constexpr (kIn == 1) {
+      return g ? normalize16(raw[0], r, g, OutT()) : raw[0];
+    } else {
+      V16 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float a = __uint_as_float(raw[i / 2].w[(2 * i) % 4]);
+        float b = __uint_as_float(raw[i / 2].w[(2 * i) % 4 + 1]);
+        if (g) {
+          a = (a * r) * g[2 * i];
+          b = (b * r) * g[2 * i + 1];
+        }
+        o.w[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+      }
+      return o;
+    }
+  }
+};
+
 // One block per (router block of TB tokens = TB*k flat ids, column slice):
 // every slice ranks the block's ids (cheap), slice 0 writes perm/slot_of,
 // and each slice copies its share of the row bytes.  Slices only matter for
 // few tokens (decode shapes), where one block per 64 tokens would leave the
 // GPU idle.
-template <typename ActT>
+template <typename InT, typename ActT>
 __global__ __launch_bounds__(256) void permute_kernel(
-    const ActT* __restrict__ x, const int32_t* __restrict__ topk_idx,
+    const InT* __restrict__ x, const int32_t* __restrict__ topk_idx,
     const int32_t* __restrict__ hist, const int32_t* __restrict__ base, int nb, int N, int C,
     int E, int k, int32_t* __restrict__ counts, int32_t* __restrict__ perm,
     int32_t* __restrict__ slot_of, ActT* __restrict__ xg, const float* __restrict__ rstd,
@@ -202,19 +237,20 @@ __global__ __launch_bounds__(256) void permute_kernel(
   if (rr < R) {
     for (int q = q0 + tid % W; q < q1; q += W) {
       for (int r0 = rr; r0 < ntok; r0 += R * U) {
-        V16 v[U];
+        using Chunk = RowChunk<InT, ActT>;
+        Chunk in[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
           const int r = min(r0 + R * u, ntok - 1);
-          v[u] = reinterpret_cast<const V16*>(x + (size_t)(tok0 + r) * C)[q];
+          in[u].load(x + (size_t)(tok0 + r) * C, q);
         }
-        if (gamma) {   // fused block: gather the normalised rows
-          constexpr int kPer = 16 / (int)sizeof(ActT);
+        V16 v[U];
 #pragma unroll
-          for (int u = 0; u < U; ++u) {
-            const int r = min(r0 + R * u, ntok - 1);
-            v[u] = normalize16(v[u], rstd[tok0 + r], gamma + q * kPer, ActT());
-          }
+        for (int u = 0; u < U; ++u) {
+          // fused block: gather the normalised rows
+          const int r = min(r0 + R * u, ntok - 1);
+          v[u] = gamma ? in[u].out(rstd[tok0 + r], gamma + q * Chunk::kPer)
+                       : in[u].out(1.0f, nullptr);
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -234,9 +270,10 @@ __global__ __launch_bounds__(256) void permute_kernel(
 }  // namespace
 
 // rstd / gamma (both null, or both set): the fused block gathers
-// (x * rstd[t]) * gamma instead of x.
-template <typename ActT>
-hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t* hist,
+// (x * rstd[t]) * gamma instead of x.  InT: the caller's rows (fp32 rows may
+// feed a bf16 gather); ActT: the gathered rows.
+template <typename InT, typename ActT>
+hipError_t launch_permute(const InT* x, const int32_t* topk_idx, const int32_t* hist,
                           int32_t* base, int N, int C, int E, int k, int32_t* counts,
                           int32_t* perm, int32_t* slot_of, ActT* xg, const float* rstd,
                           const float* gamma, hipStream_t stream) {
@@ -250,18 +287,23 @@ hipError_t launch_permute(const ActT* x, const int32_t* topk_idx, const int32_t*
   // (128 bytes of a row).
   const int chunks = C * (int)sizeof(ActT) / 16;
   const int slices = max(1, min(chunks / 8, (512 + nb - 1) / nb));
-  hipLaunchKernelGGL(permute_kernel<ActT>, dim3(nb, slices), dim3(256), 0, stream, x, topk_idx,
+  hipLaunchKernelGGL((permute_kernel<InT, ActT>), dim3(nb, slices), dim3(256), 0, stream, x, topk_idx,
                      hist, fold ? nullptr : base, nb, N, C, E, k, counts, perm, slot_of, xg, rstd,
                      gamma);
   return hipGetLastError();
 }
 
-template hipError_t launch_permute<float>(const float*, const int32_t*, const int32_t*, int32_t*,
-                                          int, int, int, int, int32_t*, int32_t*, int32_t*,
-                                          float*, const float*, const float*, hipStream_t);
-template hipError_t launch_permute<bf16_t>(const bf16_t*, const int32_t*, const int32_t*,
-                                           int32_t*, int, int, int, int, int32_t*, int32_t*,
-                                           int32_t*, bf16_t*, const float*, const float*,
-                                           hipStream_t);
+template hipError_t launch_permute<float, float>(const float*, const int32_t*, const int32_t*,
+                                                 int32_t*, int, int, int, int, int32_t*,
+                                                 int32_t*, int32_t*, float*, const float*,
+                                                 const float*, hipStream_t);
+template hipError_t launch_permute<bf16_t, bf16_t>(const bf16_t*, const int32_t*, const int32_t*,
+                                                   int32_t*, int, int, int, int, int32_t*,
+                                                   int32_t*, int32_t*, bf16_t*, const float*,
+                                                   const float*, hipStream_t);
+template hipError_t launch_permute<float, bf16_t>(const float*, const int32_t*, const int32_t*,
+                                                  int32_t*, int, int, int, int, int32_t*,
+                                                  int32_t*, int32_t*, bf16_t*, const float*,
+                                                  const float*, hipStream_t);
 
 }  // namespace mgpt

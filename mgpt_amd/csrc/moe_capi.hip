@@ -36,16 +36,18 @@ namespace mgpt {
 // kernels (router.hip, dispatch.hip, gemm.hip, combine.hip, pack.hip)
 template <typename ActT>
 hipError_t launch_router(const ActT*, const float*, const float*, const float*, int, int, int,
-                         int, int32_t*, float*, int32_t*, float*, float*, const float*, float,
+                         int, int32_t*, float*, int32_t*, float*, float*, const float*, float, int,
                          float*, hipStream_t);
 hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
-template <typename ActT>
-hipError_t launch_permute(const ActT*, const int32_t*, const int32_t*, int32_t*, int, int, int,
+template <typename InT, typename ActT>
+hipError_t launch_permute(const InT*, const int32_t*, const int32_t*, int32_t*, int, int, int,
                           int, int32_t*, int32_t*, int32_t*, ActT*, const float*, const float*,
                           hipStream_t);
-template <typename ActT>
+template <typename ActT, typename OutT>
 hipError_t launch_combine(const ActT*, const int32_t*, const float*, const int32_t*, int, int, int,
-                          const ActT*, ActT*, hipStream_t);
+                          const OutT*, OutT*, hipStream_t);
+template <typename T>
+hipError_t launch_copy_cols(const T*, int, T*, int, int, int, int, hipStream_t);
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT*, const WT*, const float*, const float*, const float*,
                                const int32_t*, int, int, int, int, int, OutT*, int, int, OutT*,
@@ -54,7 +56,7 @@ template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
-hipError_t launch_pack_router(const float*, int, int, int, float*, hipStream_t);
+hipError_t launch_pack_router(const float*, int, int, int, int, float*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
                            const int32_t*, int, int, int, int, int, bf16_t*, int, int, float*, int,
@@ -122,19 +124,30 @@ int round_up(int v, int m) { return (v + m - 1) / m * m; }
 struct Layout {
   size_t topk_idx, topk_p, slot_of, perm, hist, base, counts, logits, xg, hbuf, obuf, partials;
   size_t rstd;   // fused block: 1/rms of each token [N] f32
+  // a caller width Cx that is not a multiple of 64: x and y at the padded
+  // width C (boundary dtype), and the fused block's gamma [C] f32
+  size_t xpad, ypad, gpad;
   // training only (after the forward regions, so those keep their offsets):
   // router probabilities [N][E] f32, gate/up pre-activations (then their
   // gradients) [A+pad][2Hp], dgo [A+pad][C], d(top-k p) [A] f32,
   // d(logits) [N][E] f32, router weight-gradient partials
   size_t probs, gu, dgo, dtp, dlog, rw_part, rw_part_b;
+  size_t dypad, dxpad;   // padded width: dy and dx at width C
   size_t total;
 };
 
 }  // namespace
 
 struct mgpt_moe {
+  // C: the width every kernel works at, the caller's embed_dim Cx rounded up
+  // to a multiple of 64 (zero columns: weights, padded rows and gradients
+  // carry zeros there, so routing and outputs are those of width Cx).
   int C, H, E, k, Hp, Cp;
-  int act, wdt;
+  int Cx;
+  // io: dtype of the caller's x, y, dx, dy; act: dtype of the gathered rows,
+  // h and the expert outputs (bf16 whenever the weights are bf16 or fp8);
+  // wdt: the packed expert weights.
+  int io, act, wdt;
   int device;
   int num_cus = 0;         // compute units of the device (persistent grids)
   int gemm_tile = 256;     // block tile of the large-M bf16 GEMMs (256 or 128)
@@ -179,6 +192,8 @@ struct mgpt_moe {
   const int32_t* last_counts = nullptr;
 
   size_t act_bytes() const { return act == MGPT_DTYPE_BF16 ? 2 : 4; }
+  size_t io_bytes() const { return io == MGPT_DTYPE_BF16 ? 2 : 4; }
+  bool padded() const { return Cx != C; }
   // Few tokens and many experts: the router's logits are spread over more
   // blocks (one expert per wave) instead of one block per 64 tokens.
   bool router_split(int N) const { return E > 16 && N < 4096; }
@@ -207,13 +222,19 @@ struct mgpt_moe {
     L.hist = take(nb * E * 4);
     L.base = take(nb * E * 4);
     L.counts = take((size_t)E * 4);
-    L.logits = take(router_split(N) ? (size_t)N * E * 4 : 0);
+    // Sized for min(N, 4095) tokens whenever E > 16, so that the workspace
+    // never shrinks as N grows past the split router's range.
+    L.logits = take(E > 16 ? (size_t)std::min(N, 4095) * E * 4 : 0);
     L.xg = take((A + kRowPad) * C * act_bytes());
     L.hbuf = take((A + kRowPad) * Hp * act_bytes());
     L.obuf = take((A + kRowPad) * C * act_bytes());
     // fp32 partial tiles of the large-M GEMMs' split last round (one per CU)
     L.partials = take(uses_gemm_dma(N) ? (size_t)num_cus * kGemmPartialBytes : 0);
     L.rstd = take((size_t)N * 4);
+    const size_t pad_rows = padded() ? (size_t)N * C * io_bytes() : 0;
+    L.xpad = take(pad_rows);
+    L.ypad = take(pad_rows);
+    L.gpad = take(padded() ? (size_t)C * 4 : 0);
     if (train) {
       L.probs = take((size_t)N * E * 4);
       L.gu = take((A + kRowPad) * 2 * Hp * act_bytes());
@@ -223,6 +244,8 @@ struct mgpt_moe {
       const size_t chunks = (size_t)router_wgrad_chunks(N);
       L.rw_part = take(chunks * C * E * 4);
       L.rw_part_b = take(chunks * E * 4);
+      L.dypad = take(pad_rows);
+      L.dxpad = take(pad_rows);
     }
     L.total = off;
     return L;
@@ -239,15 +262,15 @@ int check_config(const mgpt_moe_config* c) {
     return fail(MGPT_ERR_INVALID_ARGUMENT,
                 "invalid shape: embed_dim=%d hidden_dim=%d num_experts=%d top_k=%d",
                 c->embed_dim, c->hidden_dim, c->num_experts, c->top_k);
-  if (c->embed_dim % 64 != 0)
-    return fail(MGPT_ERR_UNSUPPORTED, "embed_dim %d is not a multiple of 64", c->embed_dim);
   if (c->num_experts > kMaxExperts)
     return fail(MGPT_ERR_UNSUPPORTED, "num_experts %d > %d", c->num_experts, kMaxExperts);
   if (c->top_k > kMaxTopK)
     return fail(MGPT_ERR_UNSUPPORTED, "top_k %d > %d", c->top_k, kMaxTopK);
+  // fp32 activations with bf16 / fp8 weights: the caller's tensors stay
+  // fp32 (routing on the fp32 rows), the expert products run in bf16.
   const bool f32 = c->act_dtype == MGPT_DTYPE_F32 && c->weight_dtype == MGPT_DTYPE_F32;
-  const bool bf = c->act_dtype == MGPT_DTYPE_BF16 &&
-                  (c->weight_dtype == MGPT_DTYPE_BF16 || c->weight_dtype == MGPT_DTYPE_FP8_E4M3);
+  const bool lowp_w = c->weight_dtype == MGPT_DTYPE_BF16 || c->weight_dtype == MGPT_DTYPE_FP8_E4M3;
+  const bool bf = (c->act_dtype == MGPT_DTYPE_BF16 || c->act_dtype == MGPT_DTYPE_F32) && lowp_w;
   if (!f32 && !bf)
     return fail(MGPT_ERR_UNSUPPORTED, "unsupported dtype pair act=%d weight=%d", c->act_dtype,
                 c->weight_dtype);
@@ -266,8 +289,9 @@ void free_weights(mgpt_moe* h) {
 }
 
 // Training is built for bf16 x bf16 and fp32 x fp32 handles (fp8 weights
-// are an inference format here).
-bool trainable(const mgpt_moe* h) { return h->wdt == h->act; }
+// are an inference format here, and fp32 tensors over bf16 products an
+// inference option).
+bool trainable(const mgpt_moe* h) { return h->wdt == h->act && h->io == h->act; }
 
 // Allocates and zeroes the gradient buffer on first use (stream-ordered).
 int ensure_grad(mgpt_moe* h, hipStream_t st) {
@@ -332,12 +356,14 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
   if (rc) return rc;
   mgpt_moe* h = new (std::nothrow) mgpt_moe();
   if (!h) return fail(MGPT_ERR_OUT_OF_MEMORY, "host allocation failed");
-  h->C = cfg->embed_dim;
+  h->Cx = cfg->embed_dim;
+  h->C = round_up(h->Cx, 64);
   h->H = cfg->hidden_dim == -1 ? 4 * cfg->embed_dim : cfg->hidden_dim;
   h->E = cfg->num_experts;
   h->k = cfg->top_k;
-  h->act = cfg->act_dtype;
+  h->io = cfg->act_dtype;
   h->wdt = cfg->weight_dtype;
+  h->act = h->wdt == MGPT_DTYPE_F32 ? MGPT_DTYPE_F32 : MGPT_DTYPE_BF16;
   h->Hp = round_up(h->H, 128);
   h->Cp = round_up(h->C, 256);
   // Tuning override for the large-M tile (default 256x256).
@@ -389,7 +415,7 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   hipStream_t st = (hipStream_t)stream_ptr;
   HIP_TRY(hipSetDevice(h->device));
   free_weights(h);
-  const int C = h->C, H = h->H, E = h->E, Hp = h->Hp, Cp = h->Cp;
+  const int C = h->C, Cx = h->Cx, H = h->H, E = h->E, Hp = h->Hp, Cp = h->Cp;
   const size_t wb = h->w_bytes();
   const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
   const bool bf = h->wdt == MGPT_DTYPE_BF16;
@@ -416,7 +442,7 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
       if (p) (void)hipFree(p);
     }
   } stage_buf, tmp_buf;
-  const size_t max_elems = std::max<size_t>((size_t)C * std::max(H, E), (size_t)H * C);
+  const size_t max_elems = std::max<size_t>((size_t)Cx * std::max(H, E), (size_t)H * Cx);
   HIP_TRY(hipMalloc(&stage_buf.p, sizeof(float) * max_elems));
   if (fp8)
     HIP_TRY(hipMalloc(&tmp_buf.p,
@@ -442,10 +468,10 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
     if (e != hipSuccess) rc = fail(MGPT_ERR_HIP, "pack failed: %s", hipGetErrorString(e));
   };
   do {
-    const float* s = src(0, (size_t)C * E);
+    const float* s = src(0, (size_t)Cx * E);
     if (!s) break;
-    if (launch_pack_router(s, C, E, RE, h->wr_g, st) != hipSuccess ||
-        (h->wr1 && launch_pack_router(s, C, E, 1, h->wr1, st) != hipSuccess)) {
+    if (launch_pack_router(s, Cx, C, E, RE, h->wr_g, st) != hipSuccess ||
+        (h->wr1 && launch_pack_router(s, Cx, C, E, 1, h->wr1, st) != hipSuccess)) {
       rc = fail(MGPT_ERR_HIP, "router pack failed");
       break;
     }
@@ -458,12 +484,13 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
       const size_t d_off = (size_t)e * Cp * Hp;
       if (fp8) HIP_TRY(hipMemsetAsync(fp32tmp, 0, sizeof(float) * 2 * Hp * C, st));
       for (int which = 0; which < 2 && rc == MGPT_OK; ++which) {   // gate, up
-        if (!(s = src(p + 2 * which, (size_t)C * H))) break;
+        // [Cx][H] -> rows of the packed [2Hp][C]: columns past Cx stay zero
+        if (!(s = src(p + 2 * which, (size_t)Cx * H))) break;
         if (fp8) {
-          if (launch_pack_transpose<float>(s, C, H, fp32tmp, C, 1, 32 * which, st) != hipSuccess)
+          if (launch_pack_transpose<float>(s, Cx, H, fp32tmp, C, 1, 32 * which, st) != hipSuccess)
             rc = fail(MGPT_ERR_HIP, "pack failed");
         } else {
-          pack(s, C, H, (char*)h->wgu + gu_off * h->w_bytes(), C, 1, 32 * which);
+          pack(s, Cx, H, (char*)h->wgu + gu_off * h->w_bytes(), C, 1, 32 * which);
         }
         if (!(s = src(p + 2 * which + 1, H))) break;
         HIP_TRY(launch_pad_row(s, H, (which ? h->bu : h->bg) + (size_t)e * Hp, Hp, st));
@@ -472,18 +499,19 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
       if (fp8)
         HIP_TRY(launch_quantize_rows(fp32tmp, 2 * Hp, C, (uint8_t*)h->wgu + gu_off,
                                      h->sgu + (size_t)e * 2 * Hp, st));
-      if (!(s = src(p + 4, (size_t)H * C))) break;
+      // [H][Cx] -> rows 0..Cx of the packed [Cp][Hp]; the rest stay zero
+      if (!(s = src(p + 4, (size_t)H * Cx))) break;
       if (fp8) {
         HIP_TRY(hipMemsetAsync(fp32tmp, 0, sizeof(float) * Cp * Hp, st));
-        if (launch_pack_transpose<float>(s, H, C, fp32tmp, Hp, 0, 0, st) != hipSuccess)
+        if (launch_pack_transpose<float>(s, H, Cx, fp32tmp, Hp, 0, 0, st) != hipSuccess)
           rc = fail(MGPT_ERR_HIP, "pack failed");
         HIP_TRY(launch_quantize_rows(fp32tmp, Cp, Hp, (uint8_t*)h->wd + d_off,
                                      h->sd + (size_t)e * Cp, st));
       } else {
-        pack(s, H, C, (char*)h->wd + d_off * h->w_bytes(), Hp, 0, 0);
+        pack(s, H, Cx, (char*)h->wd + d_off * h->w_bytes(), Hp, 0, 0);
       }
-      if (!(s = src(p + 5, C))) break;
-      HIP_TRY(launch_pad_row(s, C, h->bd + (size_t)e * Cp, Cp, st));
+      if (!(s = src(p + 5, Cx))) break;
+      HIP_TRY(launch_pad_row(s, Cx, h->bd + (size_t)e * Cp, Cp, st));
       // Host sources are staged through one buffer: finish before reuse.
       if (!params_on_device) HIP_TRY(hipStreamSynchronize(st));
     }
@@ -513,9 +541,9 @@ int mgpt_moe_load_gpt_bin(mgpt_moe* h, const char* path, int layer, float* ln2_g
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   mgpt_gpt_bin_info info;
   if (int rc = mgpt_gpt_bin_inspect(path, h->E, h->H, &info)) return rc;
-  if (info.embed_dim != h->C)
+  if (info.embed_dim != h->Cx)
     return fail(MGPT_ERR_INVALID_ARGUMENT, "%s: embed_dim %d, the handle has C = %d", path,
-                info.embed_dim, h->C);
+                info.embed_dim, h->Cx);
   std::vector<float> buf;
   try {
     buf.resize((size_t)info.moe_floats);
@@ -526,7 +554,7 @@ int mgpt_moe_load_gpt_bin(mgpt_moe* h, const char* path, int layer, float* ln2_g
                                        buf.size()))
     return rc;
   // pointers into the block's parameters, get_parameters() order
-  const size_t C = h->C, H = h->H, E = h->E;
+  const size_t C = h->Cx, H = h->H, E = h->E;
   std::vector<const float*> ptr;
   const float* p = buf.data();
   auto take = [&](size_t n) {
@@ -564,11 +592,12 @@ struct BlockArgs {
   float eps = 0.0f;
 };
 
-template <typename ActT>
-int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool train,
+// IoT: the caller's x and y; ActT: the gathered rows, h and expert outputs.
+template <typename IoT, typename ActT>
+int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
                  hipStream_t st, BlockArgs blk = BlockArgs()) {
   const Layout L = h->layout(N, train);
-  const int C = h->C, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
+  const int C = h->C, Cx = h->Cx, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
   const size_t A = (size_t)N * k;
   int32_t* idx = (int32_t*)(ws + L.topk_idx);
   float* topp = (float*)(ws + L.topk_p);
@@ -591,16 +620,33 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
   HIP_TRY(mark(0));
+  // A caller width that is not a multiple of 64: the rows (and gamma) are
+  // copied into zero-padded ones of width C; the output comes back the same
+  // way.  Padding adds +0 terms only, so routing and outputs are unchanged.
+  const IoT* xi = x;
+  IoT* yi = y;
+  const float* gamma = blk.gamma;
+  if (h->padded()) {
+    IoT* xp = (IoT*)(ws + L.xpad);
+    HIP_TRY(launch_copy_cols<IoT>(x, Cx, xp, C, N, Cx, C, st));
+    xi = xp;
+    yi = (IoT*)(ws + L.ypad);
+    if (gamma) {
+      float* gp = (float*)(ws + L.gpad);
+      HIP_TRY(launch_copy_cols<float>(gamma, Cx, gp, C, 1, Cx, C, st));
+      gamma = gp;
+    }
+  }
   float* logits = h->router_split(N) ? (float*)(ws + L.logits) : nullptr;
   // training: keep the router probabilities and the gate/up pre-activations
   float* probs = train ? (float*)(ws + L.probs) : nullptr;
   ActT* gu = train ? (ActT*)(ws + L.gu) : nullptr;
-  float* rstd = blk.gamma ? (float*)(ws + L.rstd) : nullptr;
-  HIP_TRY(launch_router<ActT>(x, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits,
-                              probs, blk.gamma, blk.eps, rstd, st));
+  float* rstd = gamma ? (float*)(ws + L.rstd) : nullptr;
+  HIP_TRY(launch_router<IoT>(xi, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits,
+                             probs, gamma, blk.eps, Cx, rstd, st));
   HIP_TRY(mark(1));
-  HIP_TRY(launch_permute<ActT>(x, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg, rstd,
-                               blk.gamma, st));
+  HIP_TRY((launch_permute<IoT, ActT>(xi, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg,
+                                     rstd, gamma, st)));
   HIP_TRY(mark(2));
   if constexpr (sizeof(ActT) == 4) {
     const int mt = (int)((A + 63) / 64) + E;
@@ -675,7 +721,9 @@ int forward_impl(mgpt_moe* h, const ActT* x, ActT* y, int N, char* ws, bool trai
     }
   }
   HIP_TRY(mark(4));
-  HIP_TRY(launch_combine<ActT>(ob, idx, topp, slot_of, N, C, k, blk.gamma ? x : nullptr, y, st));
+  HIP_TRY((launch_combine<ActT, IoT>(ob, idx, topp, slot_of, N, C, k, gamma ? xi : nullptr, yi,
+                                     st)));
+  if (h->padded()) HIP_TRY(launch_copy_cols<IoT>(yi, C, y, Cx, N, Cx, Cx, st));
   HIP_TRY(mark(5));
   if (prof) ++h->prof_count;
   if (capturing) {
@@ -692,10 +740,20 @@ template <typename ActT>
 int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, char* ws,
                   hipStream_t st) {
   const Layout L = h->layout(N, true);
-  const int C = h->C, H = h->H, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
+  const int C = h->C, Cx = h->Cx, H = h->H, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
   const int A = N * k;
   if (int rc = ensure_grad(h, st)) return rc;
   if (int rc = ensure_bwd_weights(h, st)) return rc;
+  // padded width: dy in and dx out through zero-padded rows; x is the padded
+  // copy the training forward left in the workspace
+  ActT* dx_out = dx;
+  if (h->padded()) {
+    ActT* dyp = (ActT*)(ws + L.dypad);
+    HIP_TRY(launch_copy_cols<ActT>(dy, Cx, dyp, C, N, Cx, C, st));
+    dy = dyp;
+    x = (const ActT*)(ws + L.xpad);
+    dx = (ActT*)(ws + L.dxpad);
+  }
   const int32_t* idx = (const int32_t*)(ws + L.topk_idx);
   const float* topp = (const float*)(ws + L.topk_p);
   const int32_t* slot_of = (const int32_t*)(ws + L.slot_of);
@@ -775,9 +833,20 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
                                     (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
                                     st));
+  if (h->padded()) HIP_TRY(launch_copy_cols<ActT>(dx, C, dx_out, Cx, N, Cx, Cx, st));
   HIP_TRY(mark(7));
   if (prof) ++h->prof_b_count;
   return MGPT_OK;
+}
+
+// The forward for the handle's (boundary, compute) dtype pair.
+int dispatch_forward(mgpt_moe* h, const void* x, void* y, int N, char* ws, bool train,
+                     hipStream_t st, BlockArgs blk) {
+  if (h->act == MGPT_DTYPE_F32)
+    return forward_impl<float, float>(h, (const float*)x, (float*)y, N, ws, train, st, blk);
+  if (h->io == MGPT_DTYPE_F32)
+    return forward_impl<float, bf16_t>(h, (const float*)x, (float*)y, N, ws, train, st, blk);
+  return forward_impl<bf16_t, bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, N, ws, train, st, blk);
 }
 
 // Shared argument checks of the forward entry points.
@@ -796,7 +865,7 @@ int check_forward_args(const mgpt_moe* h, const void* x, const void* y, int num_
   if (workspace_bytes < need)
     return fail(MGPT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu bytes < required %zu",
                 workspace_bytes, need);
-  const size_t xbytes = (size_t)num_tokens * h->C * h->act_bytes();
+  const size_t xbytes = (size_t)num_tokens * h->Cx * h->io_bytes();
   if ((const char*)x < (const char*)y + xbytes && (const char*)y < (const char*)x + xbytes)
     return fail(MGPT_ERR_INVALID_ARGUMENT, "y must not overlap x");
   return MGPT_OK;
@@ -813,11 +882,7 @@ int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* 
   if (num_tokens == 0) return MGPT_OK;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
-  if (h->act == MGPT_DTYPE_BF16)
-    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, num_tokens, (char*)workspace,
-                                false, st);
-  return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, false,
-                             st);
+  return dispatch_forward(h, x, y, num_tokens, (char*)workspace, false, st, BlockArgs());
 }
 
 int mgpt_moe_forward_block(mgpt_moe* h, const void* x, const float* gamma, float eps, void* out,
@@ -833,11 +898,7 @@ int mgpt_moe_forward_block(mgpt_moe* h, const void* x, const float* gamma, float
   BlockArgs blk;
   blk.gamma = gamma;
   blk.eps = eps;
-  if (h->act == MGPT_DTYPE_BF16)
-    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)out, num_tokens, (char*)workspace,
-                                false, st, blk);
-  return forward_impl<float>(h, (const float*)x, (float*)out, num_tokens, (char*)workspace, false,
-                             st, blk);
+  return dispatch_forward(h, x, out, num_tokens, (char*)workspace, false, st, blk);
 }
 
 int mgpt_moe_get_rstd(const mgpt_moe* h, int num_tokens, void* workspace, float** rstd) {
@@ -863,11 +924,7 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens, 
   if (num_tokens == 0) return MGPT_OK;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
-  if (h->act == MGPT_DTYPE_BF16)
-    return forward_impl<bf16_t>(h, (const bf16_t*)x, (bf16_t*)y, num_tokens, (char*)workspace,
-                                true, st);
-  return forward_impl<float>(h, (const float*)x, (float*)y, num_tokens, (char*)workspace, true,
-                             st);
+  return dispatch_forward(h, x, y, num_tokens, (char*)workspace, true, st, BlockArgs());
 }
 
 int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
@@ -888,7 +945,7 @@ int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int 
   if (workspace_bytes < need)
     return fail(MGPT_ERR_WORKSPACE_TOO_SMALL, "workspace %zu bytes < required %zu",
                 workspace_bytes, need);
-  const size_t nbytes = (size_t)num_tokens * h->C * h->act_bytes();
+  const size_t nbytes = (size_t)num_tokens * h->Cx * h->io_bytes();
   auto overlap = [&](const void* a, const void* b) {
     return (const char*)a < (const char*)b + nbytes && (const char*)b < (const char*)a + nbytes;
   };
@@ -928,21 +985,28 @@ int mgpt_moe_get_gradients(mgpt_moe* h, float* const* grads, int num_params, int
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
   if (int rc = ensure_grad(h, st)) return rc;
-  const size_t C = h->C, H = h->H, E = h->E;
+  // The buffers are at the padded width C; the caller's parameters at Cx:
+  // [C][*] gradients give their first Cx rows, W_down's [H][C] its first Cx
+  // columns of each row.
+  const size_t C = h->C, Cx = h->Cx, H = h->H, E = h->E;
   const hipMemcpyKind kind = grads_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
   auto copy = [&](int i, size_t off, size_t n) -> hipError_t {
     return hipMemcpyAsync(grads[i], h->grad + off, sizeof(float) * n, kind, st);
   };
-  HIP_TRY(copy(0, h->g_off[0], C * E));
+  HIP_TRY(copy(0, h->g_off[0], Cx * E));
   HIP_TRY(copy(1, h->g_off[1], E));
   for (size_t e = 0; e < E; ++e) {
     const int p = 2 + 6 * (int)e;
-    HIP_TRY(copy(p + 0, h->g_off[2] + e * C * H, C * H));
+    HIP_TRY(copy(p + 0, h->g_off[2] + e * C * H, Cx * H));
     HIP_TRY(copy(p + 1, h->g_off[3] + e * H, H));
-    HIP_TRY(copy(p + 2, h->g_off[4] + e * C * H, C * H));
+    HIP_TRY(copy(p + 2, h->g_off[4] + e * C * H, Cx * H));
     HIP_TRY(copy(p + 3, h->g_off[5] + e * H, H));
-    HIP_TRY(copy(p + 4, h->g_off[6] + e * H * C, H * C));
-    HIP_TRY(copy(p + 5, h->g_off[7] + e * C, C));
+    if (Cx == C)
+      HIP_TRY(copy(p + 4, h->g_off[6] + e * H * C, H * C));
+    else
+      HIP_TRY(hipMemcpy2DAsync(grads[p + 4], sizeof(float) * Cx, h->grad + h->g_off[6] + e * H * C,
+                               sizeof(float) * C, sizeof(float) * Cx, H, kind, st));
+    HIP_TRY(copy(p + 5, h->g_off[7] + e * C, Cx));
   }
   HIP_TRY(hipStreamSynchronize(st));
   return MGPT_OK;
@@ -1026,7 +1090,7 @@ int mgpt_moe_export_fp8(const mgpt_moe* h, int expert, int which, uint8_t* q_hos
     return fail(MGPT_ERR_INVALID_ARGUMENT, "bad arguments");
   if (h->wdt != MGPT_DTYPE_FP8_E4M3) return fail(MGPT_ERR_INVALID_ARGUMENT, "not an fp8 handle");
   if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
-  const int C = h->C, H = h->H, Hp = h->Hp, Cp = h->Cp;
+  const int C = h->C, Cx = h->Cx, H = h->H, Hp = h->Hp, Cp = h->Cp;
   if (which < 2) {
     std::vector<uint8_t> q((size_t)2 * Hp * C);
     std::vector<float> s((size_t)2 * Hp);
@@ -1037,7 +1101,7 @@ int mgpt_moe_export_fp8(const mgpt_moe* h, int expert, int which, uint8_t* q_hos
     for (int n = 0; n < H; ++n) {
       const int prow = (n / 32) * 64 + (n % 32) + 32 * which;
       scale_host[n] = s[prow];
-      for (int c = 0; c < C; ++c) q_host[(size_t)c * H + n] = q[(size_t)prow * C + c];
+      for (int c = 0; c < Cx; ++c) q_host[(size_t)c * H + n] = q[(size_t)prow * C + c];
     }
   } else {
     std::vector<uint8_t> q((size_t)Cp * Hp);
@@ -1046,9 +1110,9 @@ int mgpt_moe_export_fp8(const mgpt_moe* h, int expert, int which, uint8_t* q_hos
                       hipMemcpyDeviceToHost));
     HIP_TRY(hipMemcpy(s.data(), h->sd + (size_t)expert * Cp, sizeof(float) * Cp,
                       hipMemcpyDeviceToHost));
-    for (int c = 0; c < C; ++c) {
+    for (int c = 0; c < Cx; ++c) {
       scale_host[c] = s[c];
-      for (int n = 0; n < H; ++n) q_host[(size_t)n * C + c] = q[(size_t)c * Hp + n];
+      for (int n = 0; n < H; ++n) q_host[(size_t)n * Cx + c] = q[(size_t)c * Hp + n];
     }
   }
   return MGPT_OK;

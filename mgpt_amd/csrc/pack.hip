@@ -9,6 +9,8 @@
 // first packed as fp32 and then quantised row by row: per output channel,
 // scale = amax / 448 (1 for an all-zero channel) and q = e4m3(w / scale),
 // round-to-nearest-even, saturating at +-448, zero encoded as +0.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace mgpt {
@@ -88,14 +90,27 @@ __global__ void pad_rows_kernel(const float* __restrict__ src, int n, float* __r
   if (i < ldd) dst[i] = i < n ? src[i] : 0.0f;
 }
 
-// Router weights W_r [C][E] -> [G][C][RE] (G = ceil(E/RE)), zero-padded.
-__global__ void pack_router_kernel(const float* __restrict__ wr, int C, int E, int RE,
+// Router weights W_r [Cx][E] -> [G][C][RE] (G = ceil(E/RE)), zero-padded
+// over the experts past E and the columns c >= Cx of a padded width C.
+__global__ void pack_router_kernel(const float* __restrict__ wr, int Cx, int C, int E, int RE,
                                    float* __restrict__ out, int total) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
   const int j = i % RE, c = (i / RE) % C, g = i / (RE * C);
   const int e = g * RE + j;
-  out[i] = e < E ? wr[(size_t)c * E + e] : 0.0f;
+  out[i] = (e < E && c < Cx) ? wr[(size_t)c * E + e] : 0.0f;
+}
+
+// dst[r][0..ncopy) = src[r][0..ncopy), dst[r][ncopy..nfill) = 0: a row block
+// moved between a caller's width and the library's zero-padded width.
+template <typename T>
+__global__ __launch_bounds__(256) void copy_cols_kernel(const T* __restrict__ src, int lds,
+                                                        T* __restrict__ dst, int ldd, int ncopy,
+                                                        int nfill, int rows) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= nfill) return;
+  for (size_t r = blockIdx.y; r < (size_t)rows; r += gridDim.y)
+    dst[r * ldd + c] = c < ncopy ? src[r * lds + c] : T(0);
 }
 
 // fp8 weights [E][Npad][K] -> the decode stream's tiles
@@ -130,13 +145,29 @@ hipError_t launch_tile_fp8(const uint8_t* src, int E, int Npad, int K, uint8_t* 
 
 // RE experts per wave group; the fused router uses router_experts_per_wave(E),
 // the split decode path RE = 1 (W_r transposed).
-hipError_t launch_pack_router(const float* wr, int C, int E, int RE, float* out,
+// Cx <= C: the caller's width; columns past it are zero.
+hipError_t launch_pack_router(const float* wr, int Cx, int C, int E, int RE, float* out,
                               hipStream_t stream) {
   const int total = ((E + RE - 1) / RE) * C * RE;
-  hipLaunchKernelGGL(pack_router_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, wr, C,
-                     E, RE, out, total);
+  hipLaunchKernelGGL(pack_router_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, wr, Cx,
+                     C, E, RE, out, total);
   return hipGetLastError();
 }
+
+// rows x nfill block: copy ncopy columns, zero the rest (pad), or copy
+// ncopy = nfill columns of a wider source (unpad).
+template <typename T>
+hipError_t launch_copy_cols(const T* src, int lds, T* dst, int ldd, int rows, int ncopy, int nfill,
+                            hipStream_t stream) {
+  if (rows <= 0 || nfill <= 0) return hipSuccess;
+  hipLaunchKernelGGL(copy_cols_kernel<T>, dim3((nfill + 255) / 256, std::min(rows, 16384)),
+                     dim3(256), 0, stream, src, lds, dst, ldd, ncopy, nfill, rows);
+  return hipGetLastError();
+}
+template hipError_t launch_copy_cols<float>(const float*, int, float*, int, int, int, int,
+                                            hipStream_t);
+template hipError_t launch_copy_cols<bf16_t>(const bf16_t*, int, bf16_t*, int, int, int, int,
+                                             hipStream_t);
 
 template <typename DT>
 hipError_t launch_pack_transpose(const float* src, int Kin, int Nout, DT* dst, int ldd, int mode,

@@ -202,6 +202,8 @@ __device__ __forceinline__ int chunk_cols(int nw, int RE, int lds_bytes) {
 struct RowNorm {
   const float* gamma;   // null: no normalisation
   float eps;
+  int cn;               // the row's true width (the mean's divisor; the
+                        // columns past it are zero padding and add +0)
 };
 
 // Correctly rounded square root of a positive normal y.  The hardware
@@ -292,7 +294,7 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
       }
       b ^= 1;
     }
-    r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ms, (float)C) + nrm.eps));
+    r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ms, (float)nrm.cn) + nrm.eps));
     if (r_out) *r_out = r;
     drain_barrier();   // every wave done with the stages before they are refilled
     b = 0;
@@ -524,13 +526,14 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
 // split path through logits [N][E] (wr1 = W_r as [E][C]).  probs (nullable)
 // receives the clamped softmax [N][E] (the reference's cached_router_probs).
 // gamma (nullable): route on RMSNorm(x) * gamma instead of x, writing each
-// token's 1/rms to rstd [N].
+// token's 1/rms to rstd [N]; cn: the mean's divisor (C, or the caller's width
+// when x's rows are zero-padded to C).
 template <typename ActT>
 hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, const float* br,
                          int N, int C, int E, int k, int32_t* topk_idx, float* topk_p,
                          int32_t* hist, float* logits, float* probs, const float* gamma,
-                         float eps, float* rstd, hipStream_t stream) {
-  const RowNorm nrm{gamma, eps};
+                         float eps, int cn, float* rstd, hipStream_t stream) {
+  const RowNorm nrm{gamma, eps, cn};
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
   if (logits) {
@@ -564,11 +567,11 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
 
 template hipError_t launch_router<float>(const float*, const float*, const float*, const float*,
                                          int, int, int, int, int32_t*, float*, int32_t*, float*,
-                                         float*, const float*, float, float*, hipStream_t);
+                                         float*, const float*, float, int, float*, hipStream_t);
 template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*,
                                           const float*, int, int, int, int, int32_t*, float*,
-                                          int32_t*, float*, float*, const float*, float, float*,
-                                          hipStream_t);
+                                          int32_t*, float*, float*, const float*, float, int,
+                                          float*, hipStream_t);
 
 // Device expf over a buffer (tests compare it with the host's glibc expf).
 __global__ void expf_probe_kernel(const float* __restrict__ in, float* __restrict__ out, int n) {

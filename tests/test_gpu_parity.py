@@ -215,12 +215,14 @@ def test_bf16_gemm_shapes(N, Cm, H, E, k):
 
 
 DECODE_SHAPES = [
-    # (N, C, H, E, k): fp8-weight decode shapes (N*k < 64*E) on the
-    # weight-streaming GEMM: experts with more than one 32-row m-tile, many
+    # (N, C, H, E, k): fp8-weight decode shapes (N*k < 64*E), on the
+    # weight-streaming GEMM where C % 128 == 0: experts with more than one 32-row m-tile, many
     # experts without tokens, a hidden size that is not a multiple of 256
     (200, 512, 384, 16, 4),
     (8, 256, 256, 64, 2),
     (33, 1024, 640, 32, 8),
+    # C % 128 == 64: no tiled weight copy, the register-staged fp8 path
+    (40, 192, 256, 16, 4),
 ]
 
 
