@@ -34,7 +34,7 @@ extern "C" {
 typedef enum mgpt_status {
   MGPT_OK = 0,
   MGPT_ERR_INVALID_ARGUMENT = 1,   /* null pointer, bad size, bad shape */
-  MGPT_ERR_UNSUPPORTED = 2,        /* valid but not built for (e.g. C % 64 != 0) */
+  MGPT_ERR_UNSUPPORTED = 2,        /* valid but not built for (e.g. E > 64) */
   MGPT_ERR_WORKSPACE_TOO_SMALL = 3,
   MGPT_ERR_NOT_READY = 4,          /* forward before parameters were loaded */
   MGPT_ERR_HIP = 5,                /* a HIP runtime call failed */
@@ -52,12 +52,16 @@ typedef enum mgpt_dtype {
  * (layers/MoELayer.cpp:4-12; hidden_dim -1 means 4*embed_dim as in
  * layers/SwiGLU.cpp:4-9). */
 typedef struct mgpt_moe_config {
-  int embed_dim;     /* C: multiple of 64 */
+  int embed_dim;     /* C: any width >= 1 (widths that are not a multiple of 64
+                        run on zero-padded rows inside the library) */
   int hidden_dim;    /* H: > 0, or -1 for 4*C */
   int num_experts;   /* E: 1..64 */
   int top_k;         /* k: 1..min(E, 8) */
   int act_dtype;     /* x and y: MGPT_DTYPE_F32 or MGPT_DTYPE_BF16 */
-  int weight_dtype;  /* F32 (act F32 only), BF16 or FP8_E4M3 (act BF16 only) */
+  int weight_dtype;  /* F32 (act F32 only), BF16 or FP8_E4M3.  With act F32
+                        and BF16 / FP8 weights the caller's tensors stay fp32:
+                        routing on the fp32 rows, expert products in bf16,
+                        fp32 outputs (inference only) */
 } mgpt_moe_config;
 
 typedef struct mgpt_moe mgpt_moe;   /* opaque handle; owns packed weights */
@@ -188,6 +192,16 @@ int mgpt_moe_zero_grad(mgpt_moe* h, void* stream);
  * parameters (utils/Tensor.h:21). */
 int mgpt_moe_get_gradients(mgpt_moe* h, float* const* grads, int num_params,
                            int grads_on_device, void* stream);
+
+/* Adds the handle's 2 + 6E gradients to grads[i] (grads[i] += gradient,
+ * one rounded add per element) in get_parameters() order and reference
+ * layouts; grads_on_device = 1 for device destinations (stream-ordered, no
+ * host synchronisation), 0 for host ones (returns once added).  Replaces the
+ * Tensor::add_grad of each parameter that the reference's Linear layers do
+ * in their backward (utils/Tensor.cpp:638-650, layers/LinearLayer.cpp:33-80),
+ * so a caller accumulates without a temporary per parameter. */
+int mgpt_moe_accumulate_gradients(mgpt_moe* h, float* const* grads, int num_params,
+                                  int grads_on_device, void* stream);
 
 /* Copies the per-expert token counts of the last forward to host memory,
  * waiting for that forward to finish.  Replaces MoELayer::get_expert_counts

@@ -93,6 +93,7 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_backward": [vp, vp, vp, vp, i, vp, sz, vp],
         "mgpt_moe_zero_grad": [vp, vp],
         "mgpt_moe_get_gradients": [vp, ctypes.POINTER(vp), i, i, vp],
+        "mgpt_moe_accumulate_gradients": [vp, ctypes.POINTER(vp), i, i, vp],
         "mgpt_moe_backward_stage_times": [vp, vp, i],
         "mgpt_moe_forward_block": [vp, vp, vp, ctypes.c_float, vp, i, vp, sz, vp],
         "mgpt_moe_get_rstd": [vp, i, vp, ctypes.POINTER(vp)],

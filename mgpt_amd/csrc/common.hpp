@@ -138,4 +138,14 @@ __device__ __forceinline__ bool find_tile(const int32_t* __restrict__ counts, in
   return out->expert >= 0;
 }
 
+// A batch of gradient additions dst_j[r][c] += src[off_j + r * lds_j + c]
+// (launch_add_jobs; passed by value as a kernel argument).
+struct AddJobs {
+  static constexpr int kMax = 24;
+  float* dst[kMax];
+  size_t off[kMax];
+  int rows[kMax], cols[kMax], lds[kMax];
+  int n;
+};
+
 }  // namespace mgpt

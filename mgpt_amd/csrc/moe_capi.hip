@@ -48,6 +48,7 @@ hipError_t launch_combine(const ActT*, const int32_t*, const float*, const int32
                           const OutT*, OutT*, hipStream_t);
 template <typename T>
 hipError_t launch_copy_cols(const T*, int, T*, int, int, int, int, hipStream_t);
+hipError_t launch_add_jobs(const float*, const AddJobs&, size_t, hipStream_t);
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT*, const WT*, const float*, const float*, const float*,
                                const int32_t*, int, int, int, int, int, OutT*, int, int, OutT*,
@@ -871,6 +872,43 @@ int check_forward_args(const mgpt_moe* h, const void* x, const void* y, int num_
   return MGPT_OK;
 }
 
+// Where parameter i's gradient lives in the handle's buffer: rows x cols
+// floats at offset off with leading dimension ld (the buffers are at the
+// padded width C; the caller's tensors at Cx, so [C][*] gradients give their
+// first Cx rows and W_down's [H][C] the first Cx columns of each row).
+struct GradPiece {
+  size_t off;
+  int rows, cols, ld;
+};
+
+GradPiece grad_piece(const mgpt_moe* h, int i) {
+  const size_t C = h->C, H = h->H, E = h->E;
+  const int Cx = h->Cx;
+  if (i == 0) return {h->g_off[0], Cx, (int)E, (int)E};
+  if (i == 1) return {h->g_off[1], 1, (int)E, (int)E};
+  const size_t e = (size_t)(i - 2) / 6;
+  switch ((i - 2) % 6) {
+    case 0: return {h->g_off[2] + e * C * H, Cx, (int)H, (int)H};
+    case 1: return {h->g_off[3] + e * H, 1, (int)H, (int)H};
+    case 2: return {h->g_off[4] + e * C * H, Cx, (int)H, (int)H};
+    case 3: return {h->g_off[5] + e * H, 1, (int)H, (int)H};
+    case 4: return {h->g_off[6] + e * H * C, (int)H, Cx, (int)C};
+    default: return {h->g_off[7] + e * C, 1, Cx, Cx};
+  }
+}
+
+int check_grad_args(const mgpt_moe* h, float* const* grads, int num_params) {
+  if (!h || !grads) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle or grads");
+  if (num_params != 2 + 6 * h->E)
+    return fail(MGPT_ERR_INVALID_ARGUMENT, "expected %d gradients (2 + 6*E), got %d",
+                2 + 6 * h->E, num_params);
+  for (int i = 0; i < num_params; ++i)
+    if (!grads[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "gradient %d is null", i);
+  if (!trainable(h))
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  return MGPT_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -974,41 +1012,58 @@ int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
 
 int mgpt_moe_get_gradients(mgpt_moe* h, float* const* grads, int num_params, int grads_on_device,
                            void* stream) {
-  if (!h || !grads) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle or grads");
-  if (num_params != 2 + 6 * h->E)
-    return fail(MGPT_ERR_INVALID_ARGUMENT, "expected %d gradients (2 + 6*E), got %d",
-                2 + 6 * h->E, num_params);
-  for (int i = 0; i < num_params; ++i)
-    if (!grads[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "gradient %d is null", i);
-  if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  if (int rc = check_grad_args(h, grads, num_params)) return rc;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
   if (int rc = ensure_grad(h, st)) return rc;
-  // The buffers are at the padded width C; the caller's parameters at Cx:
-  // [C][*] gradients give their first Cx rows, W_down's [H][C] its first Cx
-  // columns of each row.
-  const size_t C = h->C, Cx = h->Cx, H = h->H, E = h->E;
   const hipMemcpyKind kind = grads_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
-  auto copy = [&](int i, size_t off, size_t n) -> hipError_t {
-    return hipMemcpyAsync(grads[i], h->grad + off, sizeof(float) * n, kind, st);
-  };
-  HIP_TRY(copy(0, h->g_off[0], Cx * E));
-  HIP_TRY(copy(1, h->g_off[1], E));
-  for (size_t e = 0; e < E; ++e) {
-    const int p = 2 + 6 * (int)e;
-    HIP_TRY(copy(p + 0, h->g_off[2] + e * C * H, Cx * H));
-    HIP_TRY(copy(p + 1, h->g_off[3] + e * H, H));
-    HIP_TRY(copy(p + 2, h->g_off[4] + e * C * H, Cx * H));
-    HIP_TRY(copy(p + 3, h->g_off[5] + e * H, H));
-    if (Cx == C)
-      HIP_TRY(copy(p + 4, h->g_off[6] + e * H * C, H * C));
-    else
-      HIP_TRY(hipMemcpy2DAsync(grads[p + 4], sizeof(float) * Cx, h->grad + h->g_off[6] + e * H * C,
-                               sizeof(float) * C, sizeof(float) * Cx, H, kind, st));
-    HIP_TRY(copy(p + 5, h->g_off[7] + e * C, Cx));
+  for (int i = 0; i < num_params; ++i) {
+    const GradPiece g = grad_piece(h, i);
+    HIP_TRY(hipMemcpy2DAsync(grads[i], sizeof(float) * g.cols, h->grad + g.off,
+                             sizeof(float) * g.ld, sizeof(float) * g.cols, g.rows, kind, st));
   }
   HIP_TRY(hipStreamSynchronize(st));
+  return MGPT_OK;
+}
+
+int mgpt_moe_accumulate_gradients(mgpt_moe* h, float* const* grads, int num_params,
+                                  int grads_on_device, void* stream) {
+  if (int rc = check_grad_args(h, grads, num_params)) return rc;
+  HIP_TRY(hipSetDevice(h->device));
+  hipStream_t st = (hipStream_t)stream;
+  if (int rc = ensure_grad(h, st)) return rc;
+  if (grads_on_device) {
+    AddJobs jobs{};
+    size_t max_elems = 0;
+    for (int i = 0; i < num_params; ++i) {
+      const GradPiece g = grad_piece(h, i);
+      const int j = jobs.n++;
+      jobs.dst[j] = grads[i];
+      jobs.off[j] = g.off;
+      jobs.rows[j] = g.rows;
+      jobs.cols[j] = g.cols;
+      jobs.lds[j] = g.ld;
+      max_elems = std::max(max_elems, (size_t)g.rows * g.cols);
+      if (jobs.n == AddJobs::kMax || i == num_params - 1) {
+        HIP_TRY(launch_add_jobs(h->grad, jobs, max_elems, st));
+        jobs.n = 0;
+        max_elems = 0;
+      }
+    }
+    return MGPT_OK;
+  }
+  // host destinations: through one host buffer, added in place
+  std::vector<float> tmp;
+  for (int i = 0; i < num_params; ++i) {
+    const GradPiece g = grad_piece(h, i);
+    tmp.resize((size_t)g.rows * g.cols);
+    HIP_TRY(hipMemcpy2DAsync(tmp.data(), sizeof(float) * g.cols, h->grad + g.off,
+                             sizeof(float) * g.ld, sizeof(float) * g.cols, g.rows,
+                             hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    float* d = grads[i];
+    for (size_t q = 0; q < tmp.size(); ++q) d[q] = d[q] + tmp[q];
+  }
   return MGPT_OK;
 }
 

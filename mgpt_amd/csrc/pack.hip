@@ -131,7 +131,32 @@ __global__ __launch_bounds__(256) void tile_fp8_kernel(const uint4* __restrict__
   dst[(tile * 256 + n % 256) * 8 + c16 % 8] = src[q];
 }
 
+// dst_j[r][c] += src[off_j + r * lds_j + c]: the handle's gradients added
+// into the caller's (Tensor::add_grad, one rounded add per element), a batch
+// of tensors per launch (blockIdx.y = tensor).
+__global__ __launch_bounds__(256) void add_jobs_kernel(const float* __restrict__ src,
+                                                       AddJobs jobs) {
+  const int j = blockIdx.y;
+  const int cols = jobs.cols[j];
+  const size_t total = (size_t)jobs.rows[j] * cols;
+  float* __restrict__ dst = jobs.dst[j];
+  const float* __restrict__ s = src + jobs.off[j];
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (size_t)gridDim.x * 256) {
+    const size_t r = i / cols, c = i % cols;
+    dst[i] = dst[i] + s[r * jobs.lds[j] + c];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_add_jobs(const float* src, const AddJobs& jobs, size_t max_elems,
+                           hipStream_t stream) {
+  if (jobs.n <= 0) return hipSuccess;
+  const unsigned gx = (unsigned)std::min<size_t>((max_elems + 255) / 256, 1024);
+  hipLaunchKernelGGL(add_jobs_kernel, dim3(std::max(gx, 1u), jobs.n), dim3(256), 0, stream, src,
+                     jobs);
+  return hipGetLastError();
+}
 
 hipError_t launch_tile_fp8(const uint8_t* src, int E, int Npad, int K, uint8_t* dst,
                            hipStream_t stream) {

@@ -6,12 +6,17 @@
 //    [W_g, b_g, W_u, b_u, W_d, b_d]), which the library's
 //    mgpt_moe_load_parameters takes verbatim;
 //  * forward_into :28-128: input [B,T,C], output allocated on the input's
-//    device when empty, every element written, the backward's caches kept;
+//    device when empty, every element written, the backward's caches kept,
+//    and the parameters' current values used (they are re-packed whenever
+//    they may have changed);
 //  * backward_into :130-223: din [B,T,C] for dout of the last forward, and
-//    every parameter's gradient added to its Tensor::grad (add_grad);
+//    every parameter's gradient added to its Tensor::grad;
 //  * get_expert_counts (MoELayer.h:39): float counts of the last forward.
-// The engine's tensors are fp32, so the handle is configured fp32/fp32 (the
-// path that matches the reference within 1e-5 with bit-exact routing).
+// The engine's tensors are fp32.  By default the handle is fp32 throughout
+// (the path that matches the reference within 1e-5 with bit-exact routing);
+// set_expert_dtype() keeps the fp32 tensors and runs the expert products in
+// bf16 or from fp8 weights.  Everything runs on the default stream, which is
+// the stream the engine's own device tensors use.
 #include "MoELayer.h"
 
 #include <hip/hip_runtime.h>
@@ -49,8 +54,7 @@ MoELayer::MoELayer(int embed_dim, int hidden_dim, int num_experts, int top_k)
 
 mgpt_moe* MoELayer::get_handle() {
   if (!handle) {
-    mgpt_moe_config cfg{embed_dim, hidden_dim, num_experts, top_k, MGPT_DTYPE_F32,
-                        MGPT_DTYPE_F32};
+    mgpt_moe_config cfg{embed_dim, hidden_dim, num_experts, top_k, MGPT_DTYPE_F32, expert_dtype};
     mgpt_moe* h = nullptr;
     check(mgpt_moe_create(&cfg, &h), "create");
     handle.reset(h);
@@ -58,9 +62,25 @@ mgpt_moe* MoELayer::get_handle() {
   return handle.get();
 }
 
+void MoELayer::set_expert_dtype(int dtype) {
+  if (dtype != MGPT_DTYPE_F32 && dtype != MGPT_DTYPE_BF16 && dtype != MGPT_DTYPE_FP8_E4M3)
+    throw std::invalid_argument("MoELayer: expert dtype must be MGPT_DTYPE_F32, _BF16 or _FP8_E4M3");
+  if (dtype == expert_dtype) return;
+  expert_dtype = dtype;
+  handle.reset();   // a new handle packs the same parameters in the new format
+  packed = false;
+  last_ws = nullptr;
+  counts_valid = false;
+}
+
+// Packs the parameters unless the handle already holds a pack of their
+// current values: a pack is dropped by to(), set_expert_dtype(),
+// refresh_weights() and every backward_into (after which the engine's
+// optimizer writes new values into the same buffers), and a pack made from
+// other buffers (a parameter reallocated, e.g. by a device round trip) is
+// never reused.
 void MoELayer::ensure_packed() {
   mgpt_moe* h = get_handle();
-  if (packed) return;
   std::vector<Tensor*> params = get_parameters();
   std::vector<const float*> ptrs;
   ptrs.reserve(params.size());
@@ -70,9 +90,11 @@ void MoELayer::ensure_packed() {
       throw std::runtime_error("MoELayer: parameters are split across devices");
     ptrs.push_back(p->get_data_ptr());
   }
+  if (packed && ptrs == packed_from) return;
   check(mgpt_moe_load_parameters(h, ptrs.data(), (int)ptrs.size(), dev == Device::CUDA ? 1 : 0,
                                  nullptr),
         "load_parameters");
+  packed_from = std::move(ptrs);
   packed = true;
 }
 
@@ -116,13 +138,17 @@ void MoELayer::forward_into(const Tensor& input, Tensor& output) {
   const int B = input.shape[0], T = input.shape[1], C = embed_dim;
   const int N = B * T;
   const bool on_dev = input.device == Device::CUDA;
+  const bool train = trains();
   mgpt_moe* h = get_handle();
   ensure_packed();
 
-  // The training forward: like the engine's layer, every forward keeps what
-  // a following backward needs.
+  // The training forward keeps what a following backward needs, as the
+  // engine's layer always does; the inference forward keeps nothing.
   size_t ws_bytes = 0;
-  check(mgpt_moe_train_workspace_bytes(h, N, &ws_bytes), "train_workspace_bytes");
+  if (train)
+    check(mgpt_moe_train_workspace_bytes(h, N, &ws_bytes), "train_workspace_bytes");
+  else
+    check(mgpt_moe_workspace_bytes(h, N, &ws_bytes), "workspace_bytes");
   void* ws;
   if (scratchpad && on_dev)
     ws = scratchpad->get_address((ws_bytes + sizeof(float) - 1) / sizeof(float));
@@ -133,28 +159,40 @@ void MoELayer::forward_into(const Tensor& input, Tensor& output) {
   if (output.size() != (size_t)N * C || output.device != input.device)
     throw std::invalid_argument("MoELayer: output must be [B, T, embed_dim] on the input's device");
 
-  // x is kept on the device for the backward (the engine's layers cache
-  // their inputs the same way): a device copy of a device input, the staged
-  // copy of a host input.
   const size_t io_bytes = (size_t)N * C * sizeof(float);
-  void* xs = device_buffer(saved_x, saved_x_bytes, io_bytes);
+  auto run = [&](const void* x, void* y) {
+    if (train)
+      check(mgpt_moe_forward_train(h, x, y, N, ws, ws_bytes, nullptr), "forward");
+    else
+      check(mgpt_moe_forward(h, x, y, N, ws, ws_bytes, nullptr), "forward");
+  };
   if (on_dev) {
-    if (N > 0)
-      check_hip(hipMemcpy(xs, input.get_data_ptr(), io_bytes, hipMemcpyDeviceToDevice), "copy x");
-    check(mgpt_moe_forward_train(h, xs, output.get_data_ptr(), N, ws, ws_bytes, nullptr),
-          "forward");
+    if (train) {
+      // the backward reads x again: keep a copy (the engine's router Linear
+      // keeps one too, layers/LinearLayer.cpp:24), stream-ordered, no wait
+      void* xs = device_buffer(saved_x, saved_x_bytes, io_bytes);
+      if (N > 0)
+        check_hip(hipMemcpyAsync(xs, input.get_data_ptr(), io_bytes, hipMemcpyDeviceToDevice,
+                                 nullptr),
+                  "copy x");
+      run(xs, output.get_data_ptr());
+    } else {
+      run(input.get_data_ptr(), output.get_data_ptr());
+    }
   } else {
     // Host tensors: stage x and y through device memory (default stream,
     // synchronous copies, as the engine's own host<->device copies).
-    void* dy = device_buffer(staging, staging_bytes, io_bytes);
+    void* xs = device_buffer(saved_x, saved_x_bytes, io_bytes);
+    void* ys = device_buffer(staging, staging_bytes, io_bytes);
     if (N > 0) check_hip(hipMemcpy(xs, input.get_data_ptr(), io_bytes, hipMemcpyHostToDevice), "copy x");
-    check(mgpt_moe_forward_train(h, xs, dy, N, ws, ws_bytes, nullptr), "forward");
-    if (N > 0) check_hip(hipMemcpy(output.get_data_ptr(), dy, io_bytes, hipMemcpyDeviceToHost), "copy y");
+    run(xs, ys);
+    if (N > 0) check_hip(hipMemcpy(output.get_data_ptr(), ys, io_bytes, hipMemcpyDeviceToHost), "copy y");
   }
   last_ws = ws;
   last_ws_bytes = ws_bytes;
   last_B = B;
   last_T = T;
+  last_trained = train;
   counts_valid = false;
 }
 
@@ -166,6 +204,10 @@ Tensor MoELayer::backward(const Tensor& dout) {
 
 void MoELayer::backward_into(const Tensor& dout, Tensor& din) {
   if (!last_ws) throw std::runtime_error("MoELayer: backward before forward");
+  if (!last_trained)
+    throw std::runtime_error(
+        "MoELayer: backward after an inference forward (set_inference(true) or bf16 / fp8 "
+        "expert products keep no caches for a backward)");
   if (dout.shape != std::vector<int>({last_B, last_T, embed_dim}))
     throw std::invalid_argument("MoELayer: dout must have the last forward's [B, T, embed_dim]");
   const int N = last_B * last_T, C = embed_dim;
@@ -193,18 +235,19 @@ void MoELayer::backward_into(const Tensor& dout, Tensor& din) {
     if (N > 0) check_hip(hipMemcpy(din.get_data_ptr(), ddx, io_bytes, hipMemcpyDeviceToHost), "copy dx");
   }
 
+  // Tensor::add_grad of every parameter, done by the library into the grad
+  // buffers themselves (no temporary per parameter).
   std::vector<Tensor*> params = get_parameters();
-  std::vector<Tensor> grads;
-  grads.reserve(params.size());
   std::vector<float*> ptrs;
-  for (Tensor* p : params) {
-    grads.emplace_back(p->shape, 0.0f, p->device);
-    ptrs.push_back(grads.back().get_data_ptr());
-  }
-  check(mgpt_moe_get_gradients(h, ptrs.data(), (int)ptrs.size(),
-                               params.front()->device == Device::CUDA ? 1 : 0, nullptr),
-        "get_gradients");
-  for (size_t i = 0; i < params.size(); ++i) params[i]->add_grad(grads[i]);
+  ptrs.reserve(params.size());
+  for (Tensor* p : params) ptrs.push_back(p->get_grad_ptr());
+  check(mgpt_moe_accumulate_gradients(h, ptrs.data(), (int)ptrs.size(),
+                                      params.front()->device == Device::CUDA ? 1 : 0, nullptr),
+        "accumulate_gradients");
+  // The engine's optimizer updates the parameters in place after the
+  // backward (Tensor::adamw_step / sgd_step, pipeline/Trainer.cpp:386):
+  // the next forward re-packs them.
+  packed = false;
 }
 
 std::vector<Tensor*> MoELayer::get_parameters() {
@@ -218,10 +261,13 @@ std::vector<Tensor*> MoELayer::get_parameters() {
 
 ScratchpadFootprint MoELayer::get_footprint(int B, int T) {
   size_t bytes = 0;
-  check(mgpt_moe_train_workspace_bytes(get_handle(), B * T, &bytes), "train_workspace_bytes");
-  // The workspace stays standing after forward (routing state and the
-  // backward's caches), as the engine's cached tensors do; the backward
-  // works inside it.
+  if (trains())
+    check(mgpt_moe_train_workspace_bytes(get_handle(), B * T, &bytes), "train_workspace_bytes");
+  else
+    check(mgpt_moe_workspace_bytes(get_handle(), B * T, &bytes), "workspace_bytes");
+  // The workspace stays standing after forward (routing state and, for
+  // training, the backward's caches), as the engine's cached tensors do;
+  // the backward works inside it.
   return {(bytes + sizeof(float) - 1) / sizeof(float), 0, 0};
 }
 

@@ -14,6 +14,7 @@
 //   ref_driver bench_block <N> <C> <H> <E> <k> <reps>   (ln2 + MoE + residual)
 //   ref_driver gptbin <out.bin> <side.bin> V S C L heads E k H steps seed
 //   ref_driver gptlogits <model.bin> <heads> <E> <k> <H> <ids.bin> <out.bin>
+//   ref_driver train <in.bin> <dy.bin> <out.bin> <steps> <lr>
 //
 // in.bin : "MGPTMOE1", int32 N C H E k, then float32 x[N*C] and the 2+6E
 //          parameters in MoELayer::get_parameters() order
@@ -40,6 +41,14 @@
 //          int32 V S C L E k H steps, then per block its ln2 scale [C] and
 //          its MoE parameters in get_parameters() order, read from the live
 //          layers (not from file offsets).
+// train  : `steps` training steps as the Trainer runs them
+//          (pipeline/Trainer.cpp:303-386: zero every parameter's grad,
+//          forward_into, backward_into with dout = dy, then
+//          AdamWOptimizer(lr)::step over get_parameters(), other
+//          hyper-parameters at their defaults), then one more forward_into;
+//          out.bin: "MGPTTRN1", int32 N C H E k steps, float32 y[N*C] of each
+//          of the steps + 1 forwards, then the parameters after each step
+//          (all 2 + 6E in get_parameters() order, sizes as in in.bin).
 // gptlogits: GPT::load_weights_bin of model.bin into the GPT its header and
 //          the given heads / E / k / H describe, then GPT::forward on the
 //          int32 token ids of ids.bin; writes the logits [T*V] float32.
@@ -69,6 +78,7 @@
 #include "RMSNormLayer.h"
 #undef private
 #include "GPT.h"
+#include "AdamWOptimiser.h"
 
 namespace {
 
@@ -165,6 +175,42 @@ int backward(const char* in_path, const char* dy_path, const char* out_path) {
     }
     std::fwrite(p->grad.data(), sizeof(float), p->size(), o);
   }
+  std::fclose(o);
+  return 0;
+}
+
+int train(const char* in_path, const char* dy_path, const char* out_path, int steps, float lr) {
+  int32_t dims[5];
+  Tensor x;
+  std::unique_ptr<MoELayer> owner;
+  if (int rc = load(in_path, dims, x, owner)) return rc;
+  MoELayer& layer = *owner;
+  const int N = dims[0], C = dims[1];
+  Tensor dy({1, N, C}, 0.0f, Device::CPU);
+  FILE* f = std::fopen(dy_path, "rb");
+  if (!f) { std::perror(dy_path); return 2; }
+  if (!read_exact(f, dy.data.data(), sizeof(float) * (size_t)N * C)) return 3;
+  std::fclose(f);
+
+  FILE* o = std::fopen(out_path, "wb");
+  if (!o) { std::perror(out_path); return 2; }
+  const int32_t hdr[6] = {dims[0], dims[1], dims[2], dims[3], dims[4], steps};
+  std::fwrite("MGPTTRN1", 1, 8, o);
+  std::fwrite(hdr, sizeof(int32_t), 6, o);
+  AdamWOptimizer opt(lr);
+  std::vector<Tensor*> params = layer.get_parameters();
+  std::vector<std::vector<float>> after;
+  Tensor y, dx;
+  for (int s = 0; s <= steps; ++s) {
+    for (Tensor* p : params) p->zero_grad();
+    layer.forward_into(x, y);
+    std::fwrite(y.data.data(), sizeof(float), (size_t)N * C, o);
+    if (s == steps) break;
+    layer.backward_into(dy, dx);
+    opt.step(params);
+    for (Tensor* p : params) after.push_back(p->data);
+  }
+  for (const auto& v : after) std::fwrite(v.data(), sizeof(float), v.size(), o);
   std::fclose(o);
   return 0;
 }
@@ -345,6 +391,8 @@ int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
   if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
   if (argc == 5 && std::string(argv[1]) == "block") return block(argv[2], argv[3], argv[4]);
+  if (argc == 7 && std::string(argv[1]) == "train")
+    return train(argv[2], argv[3], argv[4], std::atoi(argv[5]), (float)std::atof(argv[6]));
   if (argc == 9 && std::string(argv[1]) == "gptlogits")
     return gptlogits(argv[2], std::atoi(argv[3]), std::atoi(argv[4]), std::atoi(argv[5]),
                      std::atoi(argv[6]), argv[7], argv[8]);

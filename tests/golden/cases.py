@@ -110,6 +110,16 @@ def build_dy(case: Case) -> np.ndarray:
     return dy
 
 
+# Cases of the training sequence (tests/golden/train/): the Trainer's step
+# (zero grads, forward, backward with dy = build_dy(case), AdamW step,
+# pipeline/Trainer.cpp:303-386) TRAIN_STEPS times, then a forward, with the
+# engine's AdamWOptimizer at learning rate TRAIN_LR (other hyper-parameters
+# at their defaults, optimisers/AdamWOptimiser.h:20-22).
+TRAIN_CASES = ["moetests_shape", "small_f32", "ragged_k3"]
+TRAIN_STEPS = 2
+TRAIN_LR = 1e-3
+
+
 # Cases of the fused block (tests/golden/block/): out = x1 + MoE(RMSNorm(x1)*gamma).
 BLOCK_CASES = ["small_f32", "ragged_k3", "k8_bf16", "bf16_large_m", "fp8_small", "cfg1", "cfg3",
                "cfg5"]

@@ -37,7 +37,15 @@ parameters as the live layers held them (not located by file offsets), and
 the logits of the reference's whole GPT::forward (after its own
 GPT::load_weights_bin of that file) on cases.gptbin_ids().
 
-Usage: python tests/golden/make_golden.py [--backward | --block | --gptbin] [case ...]
+With --train it runs the Trainer's step sequence on the reference's layer
+(ref_driver train: zero grads, forward_into, backward_into with
+dy = cases.build_dy(case), AdamWOptimizer::step, cases.TRAIN_STEPS times,
+then a last forward_into) on cases.TRAIN_CASES and stores
+tests/golden/train/<case>.npz with the outputs y of every forward in full
+and, per step, sha256 digests and sampled flat entries of every parameter
+after the step (at the flat indices cases.sample_flat(size, 64)).
+
+Usage: python tests/golden/make_golden.py [--backward | --block | --gptbin | --train] [case ...]
 (default: all cases)
 """
 from __future__ import annotations
@@ -255,6 +263,45 @@ def make_gptbin() -> None:
     print(f"gptbin: {len(blob)} bytes, dims {dims.tolist()}", flush=True)
 
 
+def read_train(raw: bytes, cfg) -> dict:
+    """y [S+1][N][C] and params[s] (list of 2+6E arrays) of a MGPTTRN1 file."""
+    assert raw[:8] == b"MGPTTRN1", "bad training output"
+    N, Cc, H, E, k, S = (int(v) for v in np.frombuffer(raw, np.int32, 6, 8))
+    off = 32
+    y = np.frombuffer(raw, np.float32, (S + 1) * N * Cc, off).reshape(S + 1, N, Cc)
+    off += 4 * y.size
+    sizes = [Cc * E, E] + [Cc * H, H, Cc * H, H, H * Cc, Cc] * E
+    params = []
+    for _ in range(S):
+        step = []
+        for n in sizes:
+            step.append(np.frombuffer(raw, np.float32, n, off).copy())
+            off += 4 * n
+        params.append(step)
+    assert off == len(raw), "trailing bytes in the training output"
+    return {"y": y.copy(), "params": params, "steps": S}
+
+
+def make_train(case: C.Case) -> None:
+    t0 = time.time()
+    inp = C.build_inputs(case)
+    with tempfile.TemporaryDirectory() as d:
+        ip, dp, op = (os.path.join(d, n) for n in ("in.bin", "dy.bin", "out.bin"))
+        write_input(ip, inp)
+        np.ascontiguousarray(C.build_dy(case), np.float32).tofile(dp)
+        subprocess.run([REF, "train", ip, dp, op, str(C.TRAIN_STEPS), repr(C.TRAIN_LR)],
+                       check=True)
+        ref = read_train(open(op, "rb").read(), inp.cfg)
+    fx = {"y": ref["y"], "steps": np.int32(ref["steps"]), "lr": np.float32(C.TRAIN_LR)}
+    for s, step in enumerate(ref["params"]):
+        for i, p in enumerate(step):
+            fx[f"p{s}_{i}_sha"] = np.array(wl.digest(p))
+            fx[f"p{s}_{i}_val"] = p[C.sample_flat(p.size, 64)]
+    os.makedirs(os.path.join(HERE, "train"), exist_ok=True)
+    np.savez_compressed(os.path.join(HERE, "train", case.name + ".npz"), **fx)
+    print(f"{case.name} train: {ref['steps']} steps ({time.time() - t0:.1f}s)", flush=True)
+
+
 def make_case(case: C.Case) -> None:
     t0 = time.time()
     inp = C.build_inputs(case)
@@ -285,6 +332,10 @@ def main(argv):
         return
     if argv and argv[0] == "--gptbin":
         make_gptbin()
+        return
+    if argv and argv[0] == "--train":
+        for n in argv[1:] or C.TRAIN_CASES:
+            make_train(C.ALL_CASES[n])
         return
     if argv and argv[0] == "--block":
         for n in argv[1:] or C.BLOCK_CASES:

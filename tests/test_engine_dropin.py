@@ -4,11 +4,17 @@ CPU: the drop-in compiles against the engine's own headers (Layer.h,
 Tensor.h, LinearLayer.h, SwiGLU.h under /root/reference) and keeps the
 engine's public MoELayer interface (layers/MoELayer.h:36-51).
 GPU: tests/engine/_build/dropin_main -- the engine's unmodified Tensor,
-LinearLayer and SwiGLU sources with the drop-in in place of MoELayer.cpp --
-runs the engine's MoE shape and backward test, full forwards whose outputs
-are compared with the oracle (fp32: 1e-5) and whose expert counts must equal
-the reference fixture's, and full backwards whose din and parameter
-gradients are compared with the oracle's backward (fp32: 1e-5).
+LinearLayer and SwiGLU sources with the drop-in in place of MoELayer.cpp,
+host tensors -- and tests/engine/_build/dropin_dev -- the same with the
+engine's device-memory primitives over HIP, so parameters, inputs, the
+optimizer state and a Scratchpad live on the device -- each run the engine's
+own MoE test at its shape (C = 16), full forwards whose outputs are compared
+with the oracle (fp32: 1e-5) and whose expert counts must equal the reference
+fixture's, full backwards whose din and parameter gradients are compared
+with the oracle's backward (fp32: 1e-5), and the Trainer's step sequence with
+the engine's own AdamWOptimizer, whose every forward must use the parameters
+as the optimizer left them.  dropin_dev also runs the Generator's loop with
+fp8 expert weights behind the fp32 tensors, with no host wait per step.
 tests/engine/_build/gpt_main -- the engine's whole GPT with the drop-in as
 every block's MoE -- loads a reference-written checkpoint with the engine's
 own GPT::load_weights_bin and must reproduce the reference GPT's logits.
@@ -29,6 +35,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 ENGINE = "/root/reference/src/main"
 BIN = os.path.join(HERE, "engine", "_build", "dropin_main")
+DEV_BIN = os.path.join(HERE, "engine", "_build", "dropin_dev")
+BINS = [pytest.param(BIN, id="host"), pytest.param(DEV_BIN, id="device")]
 HOST = os.path.join(ROOT, "mgpt_amd", "host")
 
 
@@ -55,29 +63,33 @@ def test_dropin_keeps_engine_interface():
     assert not missing, f"drop-in lacks {missing}"
 
 
-def _run(args):
-    print("dropin_main", *args, flush=True)
-    return subprocess.run([BIN, *args], capture_output=True, text=True, timeout=300)
+def _run(args, binary=BIN):
+    if not os.path.exists(binary):
+        pytest.skip(f"{binary} not built")
+    print(os.path.basename(binary), *args, flush=True)
+    return subprocess.run([binary, *args], capture_output=True, text=True, timeout=300)
 
 
 @pytest.mark.gpu
-@pytest.mark.skipif(not os.path.exists(BIN), reason="engine test binary not built")
-def test_engine_moe_shapes():
-    r = _run(["shapes"])
+@pytest.mark.parametrize("binary", BINS)
+def test_engine_moe_shapes(binary):
+    """The engine's own MoE test (tests/networkTest/moeTests.cpp:6-76) at its
+    shape C = 16, E = 4, k = 2, all-ones input and dout."""
+    r = _run(["shapes"], binary)
     assert r.returncode == 0, r.stdout + r.stderr
 
 
 @pytest.mark.gpu
-@pytest.mark.skipif(not os.path.exists(BIN), reason="engine test binary not built")
-@pytest.mark.parametrize("name", ["small_f32", "ragged_k3", "cfg1"])
-def test_engine_forward_matches_reference(name):
+@pytest.mark.parametrize("binary", BINS)
+@pytest.mark.parametrize("name", ["moetests_shape", "small_f32", "ragged_k3", "cfg1"])
+def test_engine_forward_matches_reference(name, binary):
     case = C.ALL_CASES[name]
     inp = C.build_inputs(case)
     fx = np.load(os.path.join(HERE, "golden", name + ".npz"))
     with tempfile.TemporaryDirectory() as d:
         ip, op = os.path.join(d, "in.bin"), os.path.join(d, "out.bin")
         write_input(ip, inp)
-        r = _run(["run", ip, op])
+        r = _run(["run", ip, op], binary)
         assert r.returncode == 0, r.stdout + r.stderr
         raw = open(op, "rb").read()
     assert raw[:8] == b"MGPTDRP1"
@@ -93,9 +105,9 @@ def test_engine_forward_matches_reference(name):
 
 
 @pytest.mark.gpu
-@pytest.mark.skipif(not os.path.exists(BIN), reason="engine test binary not built")
-@pytest.mark.parametrize("name", ["small_f32", "ragged_k3", "cfg1"])
-def test_engine_backward_matches_reference(name):
+@pytest.mark.parametrize("binary", BINS)
+@pytest.mark.parametrize("name", ["moetests_shape", "small_f32", "ragged_k3", "cfg1"])
+def test_engine_backward_matches_reference(name, binary):
     """The drop-in's backward_into inside the engine: din and every
     parameter's Tensor::grad (added with the engine's own add_grad) against
     the oracle backward, which matches the reference's bit for bit; fp32
@@ -107,7 +119,7 @@ def test_engine_backward_matches_reference(name):
         ip, dp, op = (os.path.join(d, n) for n in ("in.bin", "dy.bin", "grad.bin"))
         write_input(ip, inp)
         np.ascontiguousarray(dy, np.float32).tofile(dp)
-        r = _run(["backward", ip, dp, op])
+        r = _run(["backward", ip, dp, op], binary)
         assert r.returncode == 0, r.stdout + r.stderr
         raw = open(op, "rb").read()
     assert raw[:8] == b"MGPTGRD1"
@@ -133,6 +145,114 @@ def test_engine_backward_matches_reference(name):
         worst = max(worst, rel, np.abs(dd).max() / scale)
     print(f"{name}: worst per-tensor error {worst:.3e}")
     assert worst <= 1e-5
+
+
+def _rel(got, want):
+    got = np.asarray(got, np.float64).reshape(-1)
+    want = np.asarray(want, np.float64).reshape(-1)
+    d = got - want
+    return (np.linalg.norm(d) / max(np.linalg.norm(want), 1e-30),
+            np.abs(d).max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("binary", BINS)
+@pytest.mark.parametrize("name", C.TRAIN_CASES)
+def test_engine_training_steps_use_updated_weights(name, binary):
+    """The Trainer's step (zero grads, forward_into, backward_into,
+    AdamWOptimizer::step; pipeline/Trainer.cpp:303-386) twice, then a
+    forward, through the drop-in with the engine's own optimizer.
+      * Every forward after a step equals the oracle's forward on the
+        parameters as the optimizer left them (dumped by the driver), at the
+        fp32 bar 1e-5: the layer reads the updated weights.
+      * The first forward equals the reference's (tests/golden/train/).
+      * The steps move the output far beyond 1e-5, so stale weights fail.
+      * The whole sequence tracks the reference's own (same fixture): the
+        parameters after each step entrywise within 1e-3 of the step's median
+        size, and the outputs at the fp32 bar 1e-5.  (AdamW's first steps
+        normalise each gradient entry, g / (|g| + eps), so an entry whose
+        gradient is near zero could move differently for a 1e-6 difference
+        in the gradients; on these cases the largest deviation is below 1e-5
+        of the median step, and the kernels are deterministic.)
+    """
+    from test_oracle_train import flat_params, with_params, fixture as train_fixture
+    case = C.ALL_CASES[name]
+    inp = C.build_inputs(case)
+    dy = C.build_dy(case)
+    fx = train_fixture(name)
+    cfg = inp.cfg
+    N, Cc, H, E = cfg.N, cfg.C, cfg.H, cfg.E
+    with tempfile.TemporaryDirectory() as d:
+        ip, dp, op = (os.path.join(d, n) for n in ("in.bin", "dy.bin", "out.bin"))
+        write_input(ip, inp)
+        np.ascontiguousarray(dy, np.float32).tofile(dp)
+        r = _run(["train", ip, dp, op, str(C.TRAIN_STEPS), repr(C.TRAIN_LR)], binary)
+        assert r.returncode == 0, r.stdout + r.stderr
+        from make_golden import read_train
+        got = read_train(open(op, "rb").read(), cfg)
+    S = C.TRAIN_STEPS
+    rel, mx = _rel(got["y"][0], fx["y"][0])
+    print(f"{name} y0 vs reference: {rel:.2e} {mx:.2e}", flush=True)
+    assert rel <= 1e-5 and mx <= 1e-5
+    for s in range(1, S + 1):
+        ref = O.forward(with_params(inp, got["params"][s - 1]))["y"]
+        rel, mx = _rel(got["y"][s], ref)
+        print(f"{name} y{s} vs oracle on the stepped parameters: {rel:.2e} {mx:.2e}", flush=True)
+        assert rel <= 1e-5 and mx <= 1e-5
+    moved, _ = _rel(got["y"][S], got["y"][0])
+    assert moved > 100 * 1e-5, f"the steps moved the output by only {moved}"
+    p0 = flat_params(inp)
+    for s in range(S):
+        worst = 0.0
+        for i, p in enumerate(got["params"][s]):
+            at = C.sample_flat(p.size, 64)
+            step = np.abs(fx[f"p{s}_{i}_val"].astype(np.float64) - p0[i][at])
+            scale = max(np.median(step), 1e-30)
+            dev_ = np.abs(p[at].astype(np.float64) - fx[f"p{s}_{i}_val"]).max() / scale
+            worst = max(worst, dev_)
+        print(f"{name} step {s + 1}: parameters vs reference, worst |diff| / median step "
+              f"{worst:.2e}", flush=True)
+        assert worst <= 1e-3
+    for s in range(1, S + 1):
+        rel, mx = _rel(got["y"][s], fx["y"][s])
+        print(f"{name} y{s} vs reference: {rel:.2e} {mx:.2e}", flush=True)
+        assert rel <= 1e-5 and mx <= 1e-5
+
+
+@pytest.mark.gpu
+def test_engine_decode_loop_fp8_device_tensors(tmp_path):
+    """The Generator's sampling loop (pipeline/Generator.cpp:24-36) at cfg5's
+    shape (N = 64, C = 2048, E = 64, k = 8, H = 1408) through the drop-in:
+    the engine's fp32 device tensors, fp8 e4m3 expert weights
+    (set_expert_dtype) and inference forwards (set_inference).  64 steps
+    are enqueued behind a 300 ms device spin and must return to the host
+    long before it ends (no host wait and no synchronous copy inside a
+    step); the output must match the reference's cfg5 rows (the fixture) at
+    the fp8 bar 6e-2."""
+    case = C.ALL_CASES["cfg5"]
+    cfg = case.cfg
+    inp = C.build_inputs(case)
+    fx = np.load(os.path.join(HERE, "golden", "cfg5.npz"))
+    xp, rp, op = (str(tmp_path / n) for n in ("x.bin", "router.bin", "out.bin"))
+    np.ascontiguousarray(inp.x, np.float32).tofile(xp)
+    with open(rp, "wb") as f:
+        f.write(np.ascontiguousarray(inp.Wr, np.float32).tobytes())
+        f.write(np.ascontiguousarray(inp.br, np.float32).tobytes())
+    spin_ms = 300.0
+    r = _run(["decode", xp, rp, str(C.SEED), str(cfg.C), str(cfg.H), str(cfg.E), str(cfg.k),
+              "64", str(spin_ms), op], DEV_BIN)
+    assert r.returncode == 0, r.stdout + r.stderr
+    print(r.stdout.strip(), flush=True)
+    raw = open(op, "rb").read()
+    assert raw[:8] == b"MGPTDEC1"
+    N, Cc = np.frombuffer(raw, np.int32, 2, 8)
+    enqueue_ms = float(np.frombuffer(raw, np.float32, 1, 16)[0])
+    y = np.frombuffer(raw, np.float32, N * Cc, 20).reshape(N, Cc)
+    assert enqueue_ms < 0.5 * spin_ms, f"64 steps took {enqueue_ms} ms to enqueue"
+    rows = fx["rows"]
+    rel, mx = _rel(y[rows], fx["y_rows"])
+    print(f"cfg5 fp8 through the drop-in: {rel:.2e} {mx:.2e}", flush=True)
+    assert rel <= 6e-2 and mx <= 6e-2
 
 
 GPT_BIN = os.path.join(HERE, "engine", "_build", "gpt_main")
