@@ -104,6 +104,20 @@ int mgpt_moe_workspace_bytes(const mgpt_moe* h, int num_tokens, size_t* bytes);
 int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* mgpt_moe_forward without a caller workspace, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.  The
+ * workspace is a scratch array built into the library, one per device, of
+ * MGPT_MOE_NOALLOC_SCRATCH_BYTES (held from the library's load until the
+ * process ends); a num_tokens whose workspace (mgpt_moe_workspace_bytes)
+ * exceeds it returns MGPT_ERR_WORKSPACE_TOO_SMALL.  Nothing is allocated,
+ * copied or waited for.  Every call on a device shares that device's array:
+ * calls that overlap on one device (two streams, or two handles, in flight at
+ * once) race and must be serialised by the caller; the array keeps the last
+ * call's contents (its routing, until the next call). */
+#define MGPT_MOE_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mgpt_moe_forward_noalloc(mgpt_moe* h, const void* x, void* y, int num_tokens, void* stream);
+
 /* The MoE half of a transformer block, fused: out = x + MoE(RMSNorm(x) * gamma)
  * with RMSNorm(x) = x / sqrt(mean(x^2) + eps) per token, computed as the
  * engine's ln2 RMSNormLayer does (utils/Tensor.cpp:785-800: sequential sum of

@@ -82,6 +82,7 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_load_parameters": [vp, ctypes.POINTER(vp), i, i, vp],
         "mgpt_moe_workspace_bytes": [vp, i, ctypes.POINTER(sz)],
         "mgpt_moe_forward": [vp, vp, vp, i, vp, sz, vp],
+        "mgpt_moe_forward_noalloc": [vp, vp, vp, i, vp],
         "mgpt_moe_get_routing": [vp, i, vp, ctypes.POINTER(Routing)],
         "mgpt_moe_expert_counts": [vp, vp, i],
         "mgpt_moe_set_profiling": [vp, i],

@@ -21,6 +21,7 @@
 
 #include <algorithm>
 #include <cstdarg>
+#include <mutex>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -136,6 +137,39 @@ struct Layout {
   size_t dypad, dxpad;   // padded width: dy and dx at width C
   size_t total;
 };
+
+// The workspace of mgpt_moe_forward_noalloc: one array per device, part of
+// the library's code object (no allocation call ever makes it), held until
+// the process ends.  Host code never passes its name to a kernel or a copy:
+// it uses the device address hipGetSymbolAddress returns for the current
+// device (scratch_address below).
+static __device__ __align__(256) char scratch[MGPT_MOE_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`, looked up once per device with
+// that device current.
+int scratch_address(int device, void** out) {
+  if (device < 0 || device >= kMaxDevices)
+    return fail(MGPT_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", device,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    int cur = -1;
+    HIP_TRY(hipGetDevice(&cur));
+    if (cur != device) HIP_TRY(hipSetDevice(device));
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (cur != device) (void)hipSetDevice(cur);
+    if (e != hipSuccess || !ptr)
+      return fail(MGPT_ERR_HIP, "hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return MGPT_OK;
+}
 
 }  // namespace
 
@@ -921,6 +955,25 @@ int mgpt_moe_forward(mgpt_moe* h, const void* x, void* y, int num_tokens, void* 
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
   return dispatch_forward(h, x, y, num_tokens, (char*)workspace, false, st, BlockArgs());
+}
+
+int mgpt_moe_forward_noalloc(mgpt_moe* h, const void* x, void* y, int num_tokens, void* stream) {
+  if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  if (num_tokens < 0) return fail(MGPT_ERR_INVALID_ARGUMENT, "negative num_tokens");
+  const size_t need = h->layout(num_tokens).total;
+  if (need > (size_t)MGPT_MOE_NOALLOC_SCRATCH_BYTES)
+    return fail(MGPT_ERR_WORKSPACE_TOO_SMALL,
+                "%d tokens need %zu workspace bytes; the built-in scratch holds %zu "
+                "(use mgpt_moe_forward with a caller workspace)",
+                num_tokens, need, (size_t)MGPT_MOE_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (int rc = scratch_address(h->device, &ws)) return rc;
+  if (int rc = check_forward_args(h, x, y, num_tokens, ws, MGPT_MOE_NOALLOC_SCRATCH_BYTES, false))
+    return rc;
+  if (num_tokens == 0) return MGPT_OK;
+  HIP_TRY(hipSetDevice(h->device));
+  return dispatch_forward(h, x, y, num_tokens, (char*)ws, false, (hipStream_t)stream,
+                          BlockArgs());
 }
 
 int mgpt_moe_forward_block(mgpt_moe* h, const void* x, const float* gamma, float eps, void* out,
