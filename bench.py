@@ -55,6 +55,10 @@ METRIC_DECODE = ("MoE decode steps/s in the sampling loop (Generator B=1, no KV 
 METRIC_BLOCK = ("MoE block tokens/s, out = x + MoE(RMSNorm(x) * gamma) "
                 "(N=16384,C=1024,E=16,k=2)")
 CALIB_MIB = 512               # known-size elementwise copy for counter calibration
+NUM_XCD = 8                   # MI355X: 8 XCDs; GRBM_GUI_ACTIVE is counted per XCD
+SIMD_NUM = 256 * 4            # MI355X: 256 CUs x 4 SIMDs (rocprof's MfmaUtil denominator)
+MFMA_COUNTERS = ("SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_BF16",
+                 "SQ_BUSY_CU_CYCLES")
 
 
 def stage_of(kernel_name: str):
@@ -134,6 +138,64 @@ def summarize_traffic(fetch_dir: str, write_dir: str, workload: str, commands) -
             "calib_write_kib_read": round(write["calib_copy"], 1),
             "fetch_factor": round(ff, 4), "write_factor": round(fw, 4),
             "kernels": kern, "commands": commands}
+
+
+def summarize_mfma(pmc_dir: str, cfg, command: str) -> dict:
+    """MFMA utilisation of the expert GEMMs from one rocprofv3 --pmc run with
+    MFMA_COUNTERS.  Per dispatch: rocprof's MfmaUtil,
+    sum(SQ_VALU_MFMA_BUSY_CYCLES) / (GRBM_GUI_ACTIVE per XCD x SIMD_NUM) (the
+    csv sums GRBM_GUI_ACTIVE over the XCDs); the shader clock during the
+    kernel, GRBM_GUI_ACTIVE per XCD / duration; the MFMA flops the hardware
+    counted (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512, padding rows included)
+    against the algorithmic 4ACH (gate/up) and 2ACH (down).  Means over the
+    dispatches of each stage."""
+    import csv
+    per = {}
+    with open(os.path.join(pmc_dir, "run_counter_collection.csv")) as f:
+        for r in csv.DictReader(f):
+            st = stage_of(r["Kernel_Name"])
+            if st not in ("gemm_gateup", "gemm_down") or "split_reduce" in r["Kernel_Name"]:
+                continue
+            d = per.setdefault(st, {}).setdefault(r["Dispatch_Id"], {})
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+            d["dur_ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    A = cfg.N * cfg.k
+    alg = {"gemm_gateup": 4.0 * A * cfg.C * cfg.H, "gemm_down": 2.0 * A * cfg.H * cfg.C}
+    out = {"workload": workload_name(cfg), "command": command, "simd_num": SIMD_NUM,
+           "xcds": NUM_XCD, "kernels": {}}
+    for st, ds in per.items():
+        ds = [d for d in ds.values() if all(c in d for c in MFMA_COUNTERS)]
+        if not ds:
+            continue
+        mean = lambda f: sum(f(d) for d in ds) / len(ds)   # noqa: E731
+        grbm = mean(lambda d: d["GRBM_GUI_ACTIVE"] / NUM_XCD)
+        busy = mean(lambda d: d["SQ_VALU_MFMA_BUSY_CYCLES"])
+        dur = mean(lambda d: d["dur_ns"])
+        mops = mean(lambda d: d["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512)
+        out["kernels"][st] = {
+            "dispatches": len(ds),
+            "mean_duration_us": round(dur / 1e3, 2),
+            "mfma_busy_cycles": round(busy),
+            "grbm_gui_active_per_xcd": round(grbm),
+            "mfma_util": round(busy / (grbm * SIMD_NUM), 4),
+            "shader_clock_ghz": round(grbm / dur, 3),
+            "counted_mfma_flops": round(mops),
+            "algorithmic_flops": alg[st],
+            "algorithmic_tflops": round(alg[st] / dur / 1e3, 2),
+            "frac_of_peak_at_measured_clock": round(
+                alg[st] / dur / 1e3 / (PEAK_BF16_TFLOPS * (grbm / dur) / 2.4), 4),
+        }
+    return out
+
+
+def cpu_sample_tokens(cfg) -> int:
+    """A CPU-baseline sample of about the work of 4096 cfg3 tokens (the
+    reference runs one core at roughly 1000 cfg3 tokens/s): 4096 tokens
+    scaled by cfg3's per-token flops over this config's, in multiples of 64."""
+    per_token = 6.0 * cfg.k * cfg.C * cfg.H + 2.0 * cfg.C * cfg.E
+    cfg3_per_token = 6.0 * 2 * 1024 * 2816 + 2.0 * 1024 * 16
+    n = int(4096 * cfg3_per_token / per_token) // 64 * 64
+    return max(64, min(n, cfg.N))
 
 
 def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
@@ -269,7 +331,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="cfg3")
-    ap.add_argument("--cpu-tokens", type=int, default=4096)
+    ap.add_argument("--cpu-tokens", type=int, default=None,
+                    help="tokens of the CPU baseline's sample (default: about 10 s of the "
+                         "reference's work per run, 4096 tokens at cfg3's per-token cost)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pass", dest="mode", choices=["forward", "train", "block", "decode"],
@@ -286,7 +350,18 @@ def main() -> int:
     ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_CSV", "BENCH_JSON"),
                     help="no GPU run: markdown summary of a rocprofv3 --kernel-trace --stats run "
                          "of this script and of the JSON line that run printed")
+    ap.add_argument("--summarize-mfma", metavar="PMC_DIR",
+                    help="no GPU run: MFMA utilisation of the expert GEMMs from a rocprofv3 "
+                         "--pmc " + " ".join(MFMA_COUNTERS) + " run of this script")
     args = ap.parse_args()
+    if args.summarize_mfma:
+        from mgpt_amd import workload as wl
+        cfg = wl.CONFIGS[args.config]
+        cmd = ("rocprofv3 --pmc " + " ".join(MFMA_COUNTERS) + " --output-format csv -d <dir> "
+               f"-o run -- python bench.py --config {args.config} --steps 3 --warmup 1 "
+               "--no-cpu-baseline")
+        print(json.dumps(summarize_mfma(args.summarize_mfma, cfg, cmd), indent=1))
+        return 0
     if args.summarize_stats:
         print(summarize_stats(*args.summarize_stats, args.config))
         return 0
@@ -386,6 +461,7 @@ def main() -> int:
     t_dn = stages["gemm_down"] * 1e-3
     gu_tflops = gateup_flops / t_gu / 1e12
     gemm_tflops = (gateup_flops + down_flops) / (t_gu + t_dn) / 1e12
+    # SURVEY 8(d)'s byte counts; the permute's counts x once per assignment
     permute_bytes = 2.0 * A * C * a + 8 * A
     combine_bytes = A * C * a + N * C * a + 8 * A
     router_bytes = N * C * a + C * E * 4 + 8 * A
@@ -394,6 +470,10 @@ def main() -> int:
         "permute_GBs": permute_bytes / (stages["permute"] * 1e-3) / 1e9,
         "combine_GBs": combine_bytes / (stages["combine"] * 1e-3) / 1e9,
     }
+    # the bytes each kernel must move: the permute reads each row once and
+    # writes it k times (plus perm and slot_of)
+    moved = {"router_topk": router_bytes, "permute": N * C * a + A * C * a + 8.0 * A,
+             "combine": combine_bytes}
     total_flops = 2.0 * N * C * E + 6.0 * A * C * H
     # fp32 runs on the fp32 matrix cores (v_mfma_f32_32x32x2f32), whose peak differs
     peak_mm = PEAK_F32_TFLOPS if cfg.weights == "f32" else PEAK_BF16_TFLOPS
@@ -424,6 +504,8 @@ def main() -> int:
         "stage_ms": {kk: round(v, 4) for kk, v in stages.items()},
         "stage_ms_forwards_averaged": n_prof,
         "hbm_frac": {kk.replace("_GBs", ""): round(v / PEAK_HBM_GBS, 4) for kk, v in hbm.items()},
+        "hbm_frac_moved_bytes": {kk: round(v / (stages[kk] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+                                 for kk, v in moved.items()},
         "expert_counts_max_over_mean": round(max(counts) / (sum(counts) / len(counts)), 3),
         "roofline": ({
             "kernel": "gate/up fp8 weight-streaming GEMM + SwiGLU epilogue",
@@ -484,6 +566,11 @@ def main() -> int:
             f"{CALIB_MIB} MiB copy (factors {traffic['fetch_factor']}, {traffic['write_factor']}); "
             "profiles/" + os.path.basename(traffic_path(cfg)))
         result["hbm_bytes_per_launch"] = {st: v["hbm_bytes"] for st, v in traffic["kernels"].items()}
+        # achieved bandwidth by the counters' bytes (what the kernel moved)
+        result["hbm_frac_counters"] = {
+            st: round(traffic["kernels"][st]["hbm_bytes"] / (stages[st] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+            for st in ("router_topk", "permute", "combine")
+            if st in traffic["kernels"] and stages.get(st)}
     if args.calib_copy:
         n = CALIB_MIB * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device=dev)
@@ -494,7 +581,8 @@ def main() -> int:
         result["calib_copy_mib"] = CALIB_MIB
     if not args.no_cpu_baseline:
         print("cpu baseline ...", file=sys.stderr, flush=True)
-        tokens = min(args.cpu_tokens // 4 if train else args.cpu_tokens, N)
+        tokens = args.cpu_tokens or cpu_sample_tokens(cfg)
+        tokens = min(tokens // 4 if train else tokens, N)
         result["cpu_baseline"] = cpu_baseline(cfg, tokens, args.cpu_reps, args.mode)
     print(json.dumps(result))
     return 0

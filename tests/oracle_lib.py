@@ -133,6 +133,19 @@ def tokens(inp, idx, topp, rows) -> np.ndarray:
     return y
 
 
+def tokens_parallel(inp, idx, topp, rows, threads: int | None = None) -> np.ndarray:
+    """tokens() over chunks of rows on several host threads (the oracle is
+    reentrant and ctypes releases the GIL during the call); every output row
+    is an independent computation, so the result equals one call's."""
+    import concurrent.futures as cf
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    threads = threads or max(1, min(16, os.cpu_count() or 1))
+    chunks = [c for c in np.array_split(rows, threads * 4) if c.size]
+    with cf.ThreadPoolExecutor(max_workers=threads) as ex:
+        parts = list(ex.map(lambda c: tokens(inp, idx, topp, c), chunks))
+    return np.concatenate(parts) if parts else np.empty((0, inp.cfg.C), np.float32)
+
+
 GRAD_NAMES = ("dWr", "dbr", "dWg", "dbg", "dWu", "dbu", "dWd", "dbd")
 
 

@@ -7,9 +7,11 @@ written by the compiled reference, which the oracle also matches bit for bit
 on the same inputs, normwise and elementwise:
     ||y - y_ref||_2 / ||y_ref||_2 <= tol  and  max|y - y_ref| <= tol * max|y_ref|
 with tol = 1e-5 (fp32), 2e-2 (bf16), 6e-2 (fp8 e4m3 weights), the bars the
-task states.  Full-size configurations are checked on routing digests and
-on sampled token rows (each row of the reference is an independent
-sequential sum, so the oracle's per-token rows equal the full run's).
+task states.  Full-size configurations are checked on routing digests, on
+the reference's sampled rows and on every token (cfg2, cfg3) or a row of
+every m-tile (cfg4) of the oracle's per-token forward (each row of the
+reference is an independent sequential sum, so the oracle's per-token rows
+equal the full run's).
 """
 import os
 
@@ -102,8 +104,28 @@ def test_parity_small(name):
     check_close(y, ref["y"], TOL[case.cfg.weights], name)
 
 
+def tile_rows(counts, perm, k, tile=256):
+    """Tokens that put a row into every 256-row m-tile of every expert
+    segment: the first and last slot of each segment and the first and last
+    slot of each of its m-tiles (slot -> token = perm[slot] // k)."""
+    slots = []
+    start = 0
+    for c in (int(v) for v in counts):
+        for t0 in range(start, start + c, tile):
+            slots += [t0, min(t0 + tile, start + c) - 1]
+        start += c
+    return np.unique(perm[np.array(slots, dtype=np.int64)] // k).astype(np.int32)
+
+
 @pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg4"])
 def test_parity_full_size(name):
+    """The benchmark shapes at full size.  Routing bit for bit (the
+    reference's digests); outputs against the reference's own sampled rows
+    (the fixture), and against the oracle's per-token forward under that
+    routing: every token at cfg2 and cfg3 (so every m-tile and feature tile
+    of both expert GEMMs, the down GEMM's split last round included), and at
+    cfg4 the tokens of the first and last row of every expert segment and of
+    every 256-row m-tile."""
     case = C.ALL_CASES[name]
     print(f"case {name}: {case.cfg}", flush=True)
     fx = fixture(name)
@@ -111,7 +133,14 @@ def test_parity_full_size(name):
     layer, y, r, counts_host, _ = run_gpu(inp)
     check_routing(r, fx, full=False)
     rows = fx["rows"]
-    check_close(y[rows], fx["y_rows"], TOL[case.cfg.weights], name)
+    check_close(y[rows], fx["y_rows"], TOL[case.cfg.weights], f"{name} reference rows")
+    if name == "cfg4":
+        dense = tile_rows(r["counts"], r["perm"], case.cfg.k)
+    else:
+        dense = np.arange(case.cfg.N, dtype=np.int32)
+    print(f"{name}: {dense.size} tokens against the oracle", flush=True)
+    ref = O.tokens_parallel(inp, r["topk_idx"], r["topk_p"], dense)
+    check_close(y[dense], ref, TOL[case.cfg.weights], f"{name} dense rows")
 
 
 @pytest.mark.parametrize("tile", ["128", "256"])
