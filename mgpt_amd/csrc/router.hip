@@ -90,11 +90,14 @@ __device__ __forceinline__ void topk_merge_lanes(float (&ov)[KP], int (&oi)[KP],
       }
 }
 
+// The chosen experts are counted into hist[e * hist_stride] (LDS or global
+// memory, integer atomics: the counts do not depend on the order).
 template <int K>
 __device__ __forceinline__ void softmax_topk_lanes(const float* __restrict__ ex, float inv, int E,
                                                   int q, int L, bool write,
                                                   int32_t* __restrict__ idx_out,
-                                                  float* __restrict__ p_out, int* s_hist) {
+                                                  float* __restrict__ p_out, int* hist,
+                                                  int hist_stride = 1) {
   constexpr int KP = K <= 1 ? 1 : (K <= 2 ? 2 : (K <= 4 ? 4 : 8));
   float lv[K];
   int li[K];
@@ -119,7 +122,7 @@ __device__ __forceinline__ void softmax_topk_lanes(const float* __restrict__ ex,
     for (int j = 0; j < K; ++j) {
       idx_out[j] = oi[j];
       p_out[j] = ov[j];
-      atomicAdd(&s_hist[oi[j]], 1);
+      atomicAdd(&hist[oi[j] * hist_stride], 1);
     }
   }
 }
@@ -520,6 +523,221 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
   softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks, probs);
 }
 
+// Decode-shaped logits without row normalisation (the split path's common
+// case): a block of NW waves owns 64 tokens (one per lane) and NW experts
+// (one per wave).  Column chunks of the 64 token rows are loaded with
+// coalesced 16-byte loads into registers one chunk ahead, widened to fp32
+// once (not once per expert) and stored to LDS, row stride CB + 4 floats so
+// that the 16 lanes of a 16-byte read hit 16 distinct bank groups; the NW
+// experts' weight slices of the chunk go to LDS beside them (read by a whole
+// wave at one address: a broadcast).  Each column then costs one rounded
+// product and one rounded add, in column order, the reference's sequence;
+// the LDS reads of the next 16 columns are in flight while the current 16
+// are multiplied and added.  Block (b, 0) also clears hist[.][b] for
+// router_softmax_split_kernel's atomics.
+constexpr int kFastCB = 128;   // columns per chunk
+template <int V>
+struct IntC {
+  static constexpr int value = V;
+};
+template <typename ActT, int NW>
+__global__ __launch_bounds__(NW * 64) void router_logits_fast_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr1, const float* __restrict__ br,
+    int N, int C, int E, float* __restrict__ logits, int32_t* __restrict__ hist, int nb) {
+  constexpr int LD = kFastCB + 4;                                  // floats per LDS row
+  constexpr int kPer = 16 / (int)sizeof(ActT);                     // columns per 16-byte piece
+  constexpr int kPieces = kRT * kFastCB / kPer;                    // x pieces per chunk
+  constexpr int kPPT = kPieces / (NW * 64);                        // x pieces per thread
+  constexpr int kWPieces = NW * kFastCB / 4;                       // weight float4 per chunk
+  static_assert(kPieces % (NW * 64) == 0 && kWPieces <= NW * 64, "chunk split");
+  __shared__ float4 s_x[2][kRT * LD / 4];
+  __shared__ float4 s_w[2][NW][kFastCB / 4];
+  const int tid = threadIdx.x;
+  const int lane = lane_id();
+  const int g = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int tok0 = blockIdx.x * kRT;
+  const int last_row = min(kRT, N - tok0) - 1;
+  if (blockIdx.y == 0 && tid < E) hist[(size_t)tid * nb + blockIdx.x] = 0;
+  // the weight float4 this thread stages: expert row tid / (CB/4) of the block
+  const int we = min((int)blockIdx.y * NW + tid / (kFastCB / 4), E - 1);
+  const int wq4 = tid % (kFastCB / 4);
+
+  // two register stages: chunk c + 2 is requested while chunk c's chain
+  // runs, so its loads have a chain's time to land before they are moved to
+  // LDS (deeper staging measured no faster: the chain bounds the kernel)
+  uint4 raws[2][kPPT];
+  // initialised: with undefined lanes (threads that stage no weights) the
+  // compiler's code for the loop measured 8 us slower at cfg5
+  float4 wraws[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
+  auto load = [&](int c0, int cnum, uint4 (&raw)[kPPT], float4& wraw) __attribute__((always_inline)) {
+    const int ppr = cnum / kPer;
+#pragma unroll
+    for (int i = 0; i < kPPT; ++i) {
+      const int p = tid + i * NW * 64;
+      const int r = p / (kFastCB / kPer), cp = p % (kFastCB / kPer);
+      raw[i] = cp < ppr ? *reinterpret_cast<const uint4*>(
+                              x + (size_t)(tok0 + min(r, last_row)) * C + c0 + cp * kPer)
+                        : make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (tid < kWPieces && 4 * wq4 < cnum)
+      wraw = *reinterpret_cast<const float4*>(wr1 + (size_t)we * C + c0 + 4 * wq4);
+  };
+  auto store = [&](int b, const uint4 (&raw)[kPPT], const float4& wraw) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPPT; ++i) {
+      const int p = tid + i * NW * 64;
+      const int r = p / (kFastCB / kPer), cp = p % (kFastCB / kPer);
+      float4* dst = &s_x[b][(r * LD + cp * kPer) / 4];
+      if constexpr (kPer == 8) {
+        dst[0] = make_float4(widen<bf16_t>(raw[i], 0), widen<bf16_t>(raw[i], 1),
+                             widen<bf16_t>(raw[i], 2), widen<bf16_t>(raw[i], 3));
+        dst[1] = make_float4(widen<bf16_t>(raw[i], 4), widen<bf16_t>(raw[i], 5),
+                             widen<bf16_t>(raw[i], 6), widen<bf16_t>(raw[i], 7));
+      } else {
+        dst[0] = make_float4(__uint_as_float(raw[i].x), __uint_as_float(raw[i].y),
+                             __uint_as_float(raw[i].z), __uint_as_float(raw[i].w));
+      }
+    }
+    if (tid < kWPieces) s_w[b][tid / (kFastCB / 4)][wq4] = wraw;
+  };
+
+  float acc = 0.0f;
+  const int nch = (C + kFastCB - 1) / kFastCB;
+  auto cols = [&](int ch) { return min(kFastCB, C - ch * kFastCB); };   // a multiple of 64
+  load(0, cols(0), raws[0], wraws[0]);
+  if (nch > 1) load(kFastCB, cols(1), raws[1], wraws[1]);
+  store(0, raws[0], wraws[0]);
+  __syncthreads();
+  // chunk ch: request ch + 2 into the register stage ch left, run ch's
+  // chain from LDS, then move ch + 1 (requested a chain earlier) into LDS
+  auto step = [&](int ch, uint4 (&mine)[kPPT], float4& wmine, const uint4 (&nxt)[kPPT],
+                  const float4& wnxt) __attribute__((always_inline)) {
+    const int b = ch & 1;
+    if (ch + 2 < nch) load((ch + 2) * kFastCB, cols(ch + 2), mine, wmine);
+    const float4* xr = &s_x[b][lane * LD / 4];
+    const float4* wr = s_w[b][g];
+    // a fixed-size, fully unrolled chunk lets the compiler keep the LDS
+    // reads of later columns in flight during the chain
+    auto chain = [&](auto n4_c) __attribute__((always_inline)) {
+      constexpr int n4 = decltype(n4_c)::value;   // a multiple of 8
+      float4 xa[4], wa[4], xb[4], wb[4];
+      auto rd = [&](int u, float4 (&xv)[4], float4 (&wv)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          xv[v] = xr[u + v];
+          wv[v] = wr[u + v];
+        }
+      };
+      // the 16 products first (independent), then the 16 dependent adds:
+      // each add then waits only for the previous add, not for a product
+      // issued just before it
+      auto mul_add = [&](const float4 (&xv)[4], const float4 (&wv)[4])
+          __attribute__((always_inline)) {
+        float pr[16];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          pr[4 * v + 0] = xv[v].x * wv[v].x;
+          pr[4 * v + 1] = xv[v].y * wv[v].y;
+          pr[4 * v + 2] = xv[v].z * wv[v].z;
+          pr[4 * v + 3] = xv[v].w * wv[v].w;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc = acc + pr[j];
+      };
+      rd(0, xa, wa);
+#pragma unroll
+      for (int u = 0; u < n4; u += 8) {
+        rd(u + 4, xb, wb);
+        mul_add(xa, wa);
+        if (u + 8 < n4) rd(u + 8, xa, wa);
+        mul_add(xb, wb);
+      }
+    };
+    if (cols(ch) == kFastCB)
+      chain(IntC<kFastCB / 4>{});
+    else
+      chain(IntC<16>{});   // a last chunk of 64 columns
+    if (ch + 1 < nch) {
+      store(b ^ 1, nxt, wnxt);
+      __syncthreads();   // the next chunk is in LDS, every wave done with this one
+    }
+  };
+  for (int ch = 0; ch < nch; ch += 2) {
+    step(ch, raws[0], wraws[0], raws[1], wraws[1]);
+    if (ch + 1 < nch) step(ch + 1, raws[1], wraws[1], raws[0], wraws[0]);
+  }
+  const int ew = blockIdx.y * NW + g;
+  if (ew < E && lane <= last_row) logits[(size_t)(tok0 + lane) * E + ew] = acc + br[ew];
+}
+
+// Softmax, top-k and histogram for decode shapes: one wave per token, lane e
+// holding expert e (E <= 64), the row in LDS.  Every lane computes the
+// row's reductions itself, in the reference's order: the running max from
+// element 0 with a strict '>' (NaN-aware as the reference is), then after the
+// exponentials the sequential sum in expert order.  Lane e's rank among the
+// clamped probabilities under (p descending, id ascending) -- the order the
+// reference's insertion top-k with a strict '>' produces -- is the number of
+// experts before it; ranks below k are the choices, written at their rank,
+// and counted into hist[e][token / 64] with integer atomics
+// (router_logits_fast_kernel cleared those entries).  No shuffles or merge
+// rounds: four passes over the row in LDS, latency hidden across lanes.
+constexpr int kSoftmaxWaves = 4;   // tokens per block
+__global__ __launch_bounds__(kSoftmaxWaves * 64) void router_softmax_wave_kernel(
+    const float* __restrict__ logits, int N, int E, int k, int32_t* __restrict__ topk_idx,
+    float* __restrict__ topk_p, int32_t* __restrict__ hist, int nb, float* __restrict__ probs) {
+  __shared__ float s_row[kSoftmaxWaves][kMaxExperts];
+  __shared__ uint64_t s_tab[32];
+  const int w = threadIdx.x / kWave, e = lane_id();
+  const int t = blockIdx.x * kSoftmaxWaves + w;
+  if (threadIdx.x < 32) s_tab[threadIdx.x] = c_exp2_tab[threadIdx.x];
+  float* row = s_row[w];
+  const bool valid = t < N;   // wave-uniform
+  const bool mine = e < E;
+  const float l = (valid && mine) ? logits[(size_t)t * E + e] : 0.0f;
+  row[e] = l;
+  __syncthreads();
+  float m = row[0];
+  for (int v = 1; v < E; ++v) {
+    const float lv = row[v];
+    if (lv > m) m = lv;
+  }
+  const float ex = mgpt_expf::expf_glibc(l - m, s_tab);
+  __builtin_amdgcn_wave_barrier();   // every lane has read the logits
+  row[e] = ex;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float sum = 0.0f;
+  for (int v = 0; v < E; ++v) sum = sum + row[v];
+  const float inv = 1.0f / fmaxf(sum, 1e-15f);
+  const float p = fminf(fmaxf(ex * inv, 1e-7f), 1.0f);
+  __builtin_amdgcn_wave_barrier();
+  row[e] = p;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (!valid || !mine) return;
+  if (probs) probs[(size_t)t * E + e] = p;   // kept for the backward pass
+  int rank = 0;
+  for (int v = 0; v < E; ++v) {
+    const float pv = row[v];
+    rank += (pv > p) || (pv == p && v < e);
+  }
+  if (rank < k) {
+    topk_idx[(size_t)t * k + rank] = e;
+    topk_p[(size_t)t * k + rank] = p;
+    atomicAdd(&hist[(size_t)e * nb + t / kRT], 1);
+  }
+}
+
+// Waves (experts) per block of router_logits_fast_kernel.  Measured at cfg5:
+// 4 waves 23 us, 2 waves 26 us, 8 waves 26.5 us.  The chain costs about the
+// same number of cycles per wave whatever the block shape (s_memtime
+// stamps): one wave issues two 16-byte LDS reads and eight VALU operations
+// per 4 columns, and that issue stream, not LDS bandwidth or load latency,
+// bounds it.
+#ifndef MGPT_ROUTER_FAST_WAVES
+#define MGPT_ROUTER_FAST_WAVES 4
+#endif
+
 }  // namespace
 
 // logits == nullptr: the fused kernel.  Otherwise (E > 16, few tokens) the
@@ -536,6 +754,17 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
   const RowNorm nrm{gamma, eps, cn};
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
+  if (logits && !gamma) {
+    // decode shapes without normalisation: the lean chain kernel, then the
+    // softmax / top-k with one wave per token
+    constexpr int NW = MGPT_ROUTER_FAST_WAVES;
+    hipLaunchKernelGGL((router_logits_fast_kernel<ActT, NW>), dim3(nb, (E + NW - 1) / NW),
+                       dim3(NW * kWave), 0, stream, x, wr1, br, N, C, E, logits, hist, nb);
+    hipLaunchKernelGGL(router_softmax_wave_kernel, dim3((N + kSoftmaxWaves - 1) / kSoftmaxWaves),
+                       dim3(kSoftmaxWaves * kWave), 0, stream, logits, N, E, k, topk_idx, topk_p,
+                       hist, nb, probs);
+    return hipGetLastError();
+  }
   if (logits) {
     hipLaunchKernelGGL(router_logits_kernel<ActT>,
                        dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
