@@ -358,14 +358,20 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
 // the tiles of that last round are split along K into s parts (s <= 8,
 // G/(T % G) of them), each a work item of its own whose fp32 partial sums
 // go to a workspace; gemm_split_reduce_kernel adds the parts in order and
-// runs the epilogue.  All tiles of the full rounds are whole items.
+// runs the epilogue.  All tiles of the full rounds are whole items.  A
+// split item writes a 256 KB fp32 partial tile and the reduce kernel reads
+// them back, a cost that only a long K amortises: tiles of fewer than
+// kMinSplitSlabs 64-column slabs stay whole.  Measured on MI355X at the
+// cfg3 shapes (skewed counts): gate/up (K = 1024, 16 slabs) 0.426 ms whole
+// vs 0.439 split; down (K = 2816, 44 slabs) 0.214 split vs 0.246 whole.
+constexpr int kMinSplitSlabs = 24;
 struct SplitPlan {
   int full, rem, s, items;
   __device__ __forceinline__ void init(int T, int G, int KT, bool enable) {
     full = (T / G) * G;
     rem = T - full;
     s = 1;
-    if (enable && rem > 0) {
+    if (enable && rem > 0 && KT >= kMinSplitSlabs) {
       s = min(min(G / rem, 8), KT);
       if (s < 2) s = 1;
     }
@@ -749,6 +755,7 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                (reinterpret_cast<uintptr_t>(save) & 15) != 0))
     return hipErrorInvalidValue;
   if (EPI == kEpiSwigluBwd && !save) return hipErrorInvalidValue;
+  if (K / 64 < kMinSplitSlabs) partials = nullptr;   // no split, no reduce launch
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
   hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves>), dim3(grid), dim3(kRingWaves * kWave), 0,

@@ -80,7 +80,8 @@ hipError_t launch_transpose_pad(const T*, int, int, size_t, T*, int, int, size_t
                                 hipStream_t);
 template <typename T, int MODE>
 hipError_t launch_wgrad(const T*, int, int, const T*, int, int, const int32_t*, int, float*,
-                        float*, int, size_t, int, int, float*, float*, size_t, hipStream_t);
+                        float*, int, size_t, int, int, float*, float*, size_t, int, float*,
+                        size_t, float*, size_t, int, hipStream_t);
 hipError_t launch_tile_fp8(const uint8_t*, int, int, int, uint8_t*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
@@ -132,8 +133,10 @@ struct Layout {
   // training only (after the forward regions, so those keep their offsets):
   // router probabilities [N][E] f32, gate/up pre-activations (then their
   // gradients) [A+pad][2Hp], dgo [A+pad][C], d(top-k p) [A] f32,
-  // d(logits) [N][E] f32, router weight-gradient partials
-  size_t probs, gu, dgo, dtp, dlog, rw_part, rw_part_b;
+  // d(logits) [N][E] f32, router weight-gradient partials, and the bias
+  // partials of the expert weight gradients' row chunks (their tile
+  // partials reuse the split-K partial region)
+  size_t probs, gu, dgo, dtp, dlog, rw_part, rw_part_b, wg_bpart;
   size_t dypad, dxpad;   // padded width: dy and dx at width C
   size_t total;
 };
@@ -233,6 +236,12 @@ struct mgpt_moe {
   // blocks (one expert per wave) instead of one block per 64 tokens.
   bool router_split(int N) const { return E > 16 && N < 4096; }
   // The bf16 large-M path (gemm_dma.hip), which may split its last round.
+  // bias partials of the weight gradients' row chunks: at most 64 chunks of
+  // the wider tile row (2Hp gate/up columns or C down columns) of
+  // 256-column tiles
+  size_t wg_bpart_bytes() const {
+    return (size_t)64 * ((std::max(2 * Hp, C) + 255) / 256) * 256 * 4;
+  }
   bool uses_gemm_dma(int N) const {
     return act == MGPT_DTYPE_BF16 && wdt == MGPT_DTYPE_BF16 && gemm_tile == 256 &&
            (size_t)N * k >= (size_t)64 * E;
@@ -279,6 +288,7 @@ struct mgpt_moe {
       const size_t chunks = (size_t)router_wgrad_chunks(N);
       L.rw_part = take(chunks * C * E * 4);
       L.rw_part_b = take(chunks * E * 4);
+      L.wg_bpart = take(uses_gemm_dma(N) ? wg_bpart_bytes() : 0);
       L.dypad = take(pad_rows);
       L.dxpad = take(pad_rows);
     }
@@ -855,12 +865,20 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   HIP_TRY(mark(3));
   // dW_down [H][C] and db_down from (h, dgo); dW_gate/up [C][H] and their
   // biases from (gathered x, d(gate)/d(up))
+  // (an expert's long contraction is cut into row chunks whose partial
+  // tiles go to the split-K region, free again once the dX product is done)
+  float* wpart = h->uses_gemm_dma(N) ? (float*)(ws + L.partials) : nullptr;
+  const size_t wpart_bytes = wpart ? (size_t)h->num_cus * kGemmPartialBytes : 0;
+  float* wbpart = h->uses_gemm_dma(N) ? (float*)(ws + L.wg_bpart) : nullptr;
+  const size_t wbpart_bytes = wbpart ? h->wg_bpart_bytes() : 0;
   HIP_TRY((launch_wgrad<ActT, 0>(hb, Hp, Hp, dgo, C, C, counts, E, g + h->g_off[6], nullptr, C,
-                                 (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, st)));
+                                 (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, A,
+                                 wpart, wpart_bytes, wbpart, wbpart_bytes, h->num_cus, st)));
   HIP_TRY(mark(4));
   HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
                                  g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
-                                 g + h->g_off[5], (size_t)H, st)));
+                                 g + h->g_off[5], (size_t)H, A, wpart, wpart_bytes, wbpart,
+                                 wbpart_bytes, h->num_cus, st)));
   HIP_TRY(mark(5));
   HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wrt, N, C, E, k, dx,
                                  dlog, st));

@@ -32,6 +32,9 @@
 // longest contractions start first.
 #include "common.hpp"
 
+#include <algorithm>
+#include <climits>
+
 namespace mgpt {
 namespace {
 
@@ -52,32 +55,58 @@ __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 4)) & 7; }
 
 typedef __attribute__((address_space(3))) char lds_char;
 
-// The tile and expert segment of this block (see the block -> tile map
-// above); false past the last tile or for an expert without rows.  Called
-// by every thread of the block (shared memory and a barrier).
+// The tile and row segment of this block (see the block -> tile map
+// above); false past the last tile.  Called by every thread of the block
+// (shared memory and a barrier).  An expert's rows are cut into chunks of
+// chunk_rows rows (the last one shorter), each a "virtual expert" with the
+// expert's whole tile grid; lane v of wave 0 describes virtual expert v
+// (at most 64 of them).  Chunk 0 of an expert accumulates into the
+// gradient; chunk c >= 1 writes partial slot `pslot` (its expert's earlier
+// chunks and the other experts' extra chunks before it, in expert order),
+// which wgrad_reduce_kernel adds in chunk order afterwards.
 struct WgTile {
-  int seg0, cnt, e, ty, tx;
+  int seg0, cnt, e, ty, tx, pslot;
 };
 
-__device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, int E, int Iy,
-                                          int Jx, int gy, int gx, WgTile* out) {
-  __shared__ int s_seg[5];
+__device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, int E,
+                                          int chunk_rows, int Iy, int Jx, int gy, int gx,
+                                          WgTile* out) {
+  __shared__ int s_seg[6];
   if (threadIdx.x < kWave) {
     const int l = lane_id();
     const int cnt = l < E ? counts[l] : 0;
     const int incl = wave_incl_scan(cnt);
-    // rank of expert l in (count descending, id ascending)
+    const int nch = cnt > 0 ? (cnt - 1) / chunk_rows + 1 : 0;   // chunks of expert l
+    const int ch_incl = wave_incl_scan(nch);
+    const int xtra = nch > 0 ? nch - 1 : 0;                     // partial slots of expert l
+    const int x_incl = wave_incl_scan(xtra);
+    const int V = __shfl(ch_incl, kWave - 1, kWave);
+    // virtual expert l: chunk c of expert ve (ve = experts whose chunks all
+    // precede l); lanes l >= V describe nothing
+    int ve = 0;
+    for (int e2 = 0; e2 < E; ++e2) ve += __shfl(ch_incl, e2, kWave) <= l;
+    const int src = ve < E ? ve : 0;
+    const int c = l - (__shfl(ch_incl, src, kWave) - __shfl(nch, src, kWave));
+    const int cnt_e = __shfl(cnt, src, kWave);
+    const bool valid = l < V;
+    const int off = valid ? c * chunk_rows : 0;   // c * chunk_rows < cnt_e on valid lanes
+    const int vcnt = valid ? min(chunk_rows, cnt_e - off) : 0;
+    const int vseg = __shfl(incl - cnt, src, kWave) + off;
+    // (the cross-lane read outside the condition: lane src must be active)
+    const int xex = __shfl(x_incl - xtra, src, kWave);
+    const int pslot = c >= 1 ? xex + c - 1 : -1;
+    // rank of virtual expert l in (rows descending, index ascending)
     int rank = 0;
-    for (int e2 = 0; e2 < E; ++e2) {
-      const int c2 = __shfl(cnt, e2, kWave);
-      rank += (c2 > cnt) || (c2 == cnt && e2 < l);
+    for (int v2 = 0; v2 < V; ++v2) {
+      const int c2 = __shfl(vcnt, v2, kWave);
+      rank += (c2 > vcnt) || (c2 == vcnt && v2 < l);
     }
     const int ngx = (Jx + gx - 1) / gx;
-    const int ng = ((Iy + gy - 1) / gy) * ngx;   // groups per expert
+    const int ng = ((Iy + gy - 1) / gy) * ngx;   // groups per virtual expert
     const int b = blockIdx.x, sidx = b / kNumXcd;
     const int j = (sidx / 16) * kNumXcd + b % kNumXcd, r = sidx % 16;
     const int pos = j / ng, gi = j % ng;
-    const bool mine = l < E && rank == pos;
+    const bool mine = valid && rank == pos;
     const unsigned long long m = __ballot(mine);
     if (l == 0) {
       const int ty = (gi / ngx) * gy + r / gx, tx = (gi % ngx) * gx + r % gx;
@@ -86,9 +115,10 @@ __device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, in
       s_seg[3] = tx;
     }
     if (mine) {
-      s_seg[0] = incl - cnt;
-      s_seg[1] = cnt;
-      s_seg[4] = l;
+      s_seg[0] = vseg;
+      s_seg[1] = vcnt;
+      s_seg[4] = src;
+      s_seg[5] = pslot;
     }
   }
   __syncthreads();
@@ -98,6 +128,7 @@ __device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, in
   out->cnt = s_seg[1];
   out->tx = s_seg[3];
   out->e = s_seg[4];
+  out->pslot = s_seg[5];
   return out->cnt > 0;
 }
 
@@ -194,7 +225,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(
   __shared__ __attribute__((aligned(1024))) char smem[2 * 2 * kOpBytes];
   const int tid = threadIdx.x;
   WgTile tl;
-  if (!wg_locate(counts, E, Iy, Jx, gy, gx, &tl)) return;
+  if (!wg_locate(counts, E, INT_MAX, Iy, Jx, gy, gx, &tl)) return;
   const int seg0 = tl.seg0, cnt = tl.cnt, e = tl.e, ty = tl.ty, tx = tl.tx;
   const int seg_end = seg0 + cnt;
   const int i0 = ty * kTI, j0 = tx * kTJ;
@@ -435,11 +466,12 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
     const bf16_t* __restrict__ P, int ldp, const bf16_t* __restrict__ Q, int ldq,
     const int32_t* __restrict__ counts, int E, int Iy, int Jx, int gy, int gx,
     float* __restrict__ out0, float* __restrict__ out1, int ldo, size_t out_estride, int i_store,
-    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride) {
+    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride,
+    int chunk_rows, float* __restrict__ part, float* __restrict__ bpart) {
   __shared__ __attribute__((aligned(1024))) char smem[kTrStages * kTrStageBytes];
   const int tid = threadIdx.x;
   WgTile tl;
-  if (!wg_locate(counts, E, Iy, Jx, gy, gx, &tl)) return;
+  if (!wg_locate(counts, E, chunk_rows, Iy, Jx, gy, gx, &tl)) return;
   const int seg0 = tl.seg0, cnt = tl.cnt, e = tl.e;
   const int i0 = tl.ty * kTI, j0 = tl.tx * kTJ;
   const bool do_bias = tl.ty == 0 && bias0 != nullptr;
@@ -546,8 +578,23 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeated tail loads
 
-  wg_accumulate<MODE>(acc, i0 + wi * 128, j0 + wj * 64, lrow, lhalf, e, out0, out1, ldo,
-                      out_estride, i_store, j_store);
+  if (tl.pslot < 0) {
+    wg_accumulate<MODE>(acc, i0 + wi * 128, j0 + wj * 64, lrow, lhalf, e, out0, out1, ldo,
+                        out_estride, i_store, j_store);
+  } else {
+    // a later chunk: the whole 256 x 256 tile to its partial slot, [i][j]
+    float* tp = part + ((size_t)tl.pslot * Iy * Jx + (size_t)tl.ty * Jx + tl.tx) * (kTI * kTJ);
+#pragma unroll
+    for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+      for (int tj = 0; tj < TJ; ++tj)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int li = wi * 128 + ti * 32 + 8 * (v / 4) + 4 * lhalf + (v % 4);
+          const int lj = wj * 64 + tj * 32 + lrow;
+          tp[li * kTJ + lj] = acc[ti][tj][v];
+        }
+  }
   if (!do_bias) return;
   // Column sums: thread t holds features 8*(t%32) .. +7 of row group t/32;
   // one thread per feature then adds the 16 row groups in order.
@@ -559,7 +606,89 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
   if (tid < 256) {
     float sum = 0.0f;
     for (int g = 0; g < 16; ++g) sum += s_b[g * 256 + tid];
-    wg_bias_add<MODE>(sum, j0 + tid, e, bias0, bias1, bias_estride, j_store);
+    if (tl.pslot < 0)
+      wg_bias_add<MODE>(sum, j0 + tid, e, bias0, bias1, bias_estride, j_store);
+    else
+      bpart[((size_t)tl.pslot * Jx + tl.tx) * kTJ + tid] = sum;
+  }
+}
+
+// Adds the partial slots of every expert that was cut into chunks to its
+// gradients, grad += (p_1 + p_2 + ...) in chunk order (chunk 0 accumulated
+// directly), so the result does not depend on which chunk finished first.
+// Blocks b < 64 * Iy * Jx take 4 rows x 256 columns of tile b / 64, one
+// float4 of 4 columns per thread; the Jx blocks after them take the bias
+// columns of tile column b - 64 * Iy * Jx.  The chunking is recomputed from
+// the counts exactly as wg_locate does it.
+template <int MODE>
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(
+    const float* __restrict__ part, const float* __restrict__ bpart,
+    const int32_t* __restrict__ counts, int E, int chunk_rows, int Iy, int Jx,
+    float* __restrict__ out0, float* __restrict__ out1, int ldo, size_t out_estride, int i_store,
+    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride) {
+  __shared__ int s_e[kWave], s_x0[kWave], s_n[kWave], s_ns;
+  if (threadIdx.x < kWave) {
+    const int l = lane_id();
+    const int cnt = l < E ? counts[l] : 0;
+    const int nch = cnt > 0 ? (cnt - 1) / chunk_rows + 1 : 0;
+    const int xtra = nch > 0 ? nch - 1 : 0;
+    const int x_incl = wave_incl_scan(xtra);
+    const unsigned long long m = __ballot(xtra > 0);
+    if (xtra > 0) {
+      const int pos = __popcll(m & ((1ull << l) - 1ull));
+      s_e[pos] = l;
+      s_x0[pos] = x_incl - xtra;
+      s_n[pos] = xtra;
+    }
+    if (l == 0) s_ns = __popcll(m);
+  }
+  __syncthreads();
+  const int ns = s_ns;
+  if (ns == 0) return;
+  const int tiles = Iy * Jx;
+  const int b = blockIdx.x;
+  if (b < 64 * tiles) {
+    const int tile = b / 64, ty = tile / Jx, tx = tile % Jx;
+    const int li = (b % 64) * 4 + (int)threadIdx.x / 64;
+    const int lj = ((int)threadIdx.x % 64) * 4;
+    const int gi = ty * kTI + li;
+    if (gi >= i_store) return;
+    for (int q = 0; q < ns; ++q) {
+      const int e = s_e[q], x0 = s_x0[q], n = s_n[q];
+      float4 a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int c = 0; c < n; ++c) {
+        const float4 v = *reinterpret_cast<const float4*>(
+            part + ((size_t)(x0 + c) * tiles + tile) * (kTI * kTJ) + li * kTJ + lj);
+        a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
+      }
+      const float av[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int j = tx * kTJ + lj + t;
+        float* ob;
+        int col;
+        if constexpr (MODE == 0) {
+          ob = out0;
+          col = j;
+        } else {
+          ob = ((j >> 5) & 1) ? out1 : out0;
+          col = (j >> 6) * 32 + (j & 31);
+        }
+        if (col < j_store) {
+          float* o = ob + (size_t)e * out_estride + (size_t)gi * ldo + col;
+          *o = *o + av[t];
+        }
+      }
+    }
+  } else {
+    const int tx = b - 64 * tiles;
+    if (!bias0 || tx >= Jx) return;
+    for (int q = 0; q < ns; ++q) {
+      const int e = s_e[q], x0 = s_x0[q], n = s_n[q];
+      float sum = 0.0f;
+      for (int c = 0; c < n; ++c) sum += bpart[((size_t)(x0 + c) * Jx + tx) * kTJ + threadIdx.x];
+      wg_bias_add<MODE>(sum, tx * kTJ + (int)threadIdx.x, e, bias0, bias1, bias_estride, j_store);
+    }
   }
 }
 
@@ -576,21 +705,50 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
 template <typename T, int MODE>
 hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, int q_valid, const int32_t* counts, int E, float* out0, float* out1,
                         int ldo, size_t out_estride, int i_store, int j_store, float* bias0,
-                        float* bias1, size_t bias_estride, hipStream_t stream) {
+                        float* bias1, size_t bias_estride, int rows_total, float* part,
+                        size_t part_bytes, float* bpart, size_t bpart_bytes, int num_cus,
+                        hipStream_t stream) {
   constexpr int EPV = WgT<T>::EPV;
   if (E <= 0 || E > kMaxExperts || p_valid % EPV || q_valid % EPV || ldp % EPV || ldq % EPV ||
-      (reinterpret_cast<uintptr_t>(P) & 15) || (reinterpret_cast<uintptr_t>(Q) & 15))
+      (reinterpret_cast<uintptr_t>(P) & 15) || (reinterpret_cast<uintptr_t>(Q) & 15) ||
+      rows_total < 0 || (reinterpret_cast<uintptr_t>(part) & 15))
     return hipErrorInvalidValue;
   if (i_store <= 0 || q_valid <= 0) return hipSuccess;
   const int Iy = (i_store + kTI - 1) / kTI, Jx = (q_valid + kTJ - 1) / kTJ;
   const int gx = Jx < 4 ? Jx : 4, gy = 16 / gx;
   const int ng = ((Iy + gy - 1) / gy) * ((Jx + gx - 1) / gx);
-  const int groups = E * ng;
+  // Rows per chunk: about one CU's share of the whole contraction
+  // (tiles x rows / CUs, at least kMinChunkRows, a multiple of the 32-row
+  // slab), so that no tile's contraction is much longer than the average
+  // CU's work while the partial tiles stay few: at most rows/chunk_rows <=
+  // num_cus / tiles slots of 256 KB, num_cus x 256 KB in all.  bf16 only,
+  // and only with a partial workspace that holds them; at most 64 chunks in
+  // all (one lane each).
+  constexpr long kMinChunkRows = 1024;
+  int chunk_rows = INT_MAX, slots = 0;
+  const long tiles = (long)Iy * Jx;
+  if (sizeof(T) == 2 && part && bpart && E < 64 && num_cus > 0 && rows_total > 0) {
+    long r = (tiles * rows_total + num_cus - 1) / num_cus;
+    r = std::max(r, kMinChunkRows);
+    r = std::max(r, ((long)rows_total + (63 - E)) / (64 - E));   // E + rows/r <= 64
+    r = (r + 31) / 32 * 32;
+    const long sl = rows_total / r;   // bound on the extra chunks over all experts
+    if (r < INT_MAX && sl > 0 && (size_t)sl * tiles * kTI * kTJ * 4 <= part_bytes &&
+        (size_t)sl * Jx * kTJ * 4 <= bpart_bytes) {
+      chunk_rows = (int)r;
+      slots = (int)sl;
+    }
+  }
+  const int groups = (E + slots) * ng;
   const int blocks = 16 * kNumXcd * ((groups + kNumXcd - 1) / kNumXcd);
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((wgrad_tr_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, stream, P, ldp,
                        Q, ldq, counts, E, Iy, Jx, gy, gx, out0, out1, ldo, out_estride, i_store,
-                       j_store, bias0, bias1, bias_estride);
+                       j_store, bias0, bias1, bias_estride, chunk_rows, part, bpart);
+    if (slots > 0)
+      hipLaunchKernelGGL((wgrad_reduce_kernel<MODE>), dim3((unsigned)(64 * tiles + Jx)), dim3(256),
+                         0, stream, part, bpart, counts, E, chunk_rows, Iy, Jx, out0, out1, ldo,
+                         out_estride, i_store, j_store, bias0, bias1, bias_estride);
   } else {
     hipLaunchKernelGGL((wgrad_kernel<T, MODE>), dim3(blocks), dim3(kThreads), 0, stream, P, ldp,
                        p_valid, Q, ldq, q_valid, counts, E, Iy, Jx, gy, gx, out0, out1, ldo,
@@ -602,7 +760,8 @@ hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, i
 #define MGPT_INST_WGRAD(T, MODE)                                                             \
   template hipError_t launch_wgrad<T, MODE>(const T*, int, int, const T*, int, int,           \
                                             const int32_t*, int, float*, float*, int, size_t, \
-                                            int, int, float*, float*, size_t, hipStream_t);
+                                            int, int, float*, float*, size_t, int, float*,     \
+                                            size_t, float*, size_t, int, hipStream_t);
 MGPT_INST_WGRAD(bf16_t, 0)
 MGPT_INST_WGRAD(bf16_t, 1)
 MGPT_INST_WGRAD(float, 0)

@@ -159,14 +159,14 @@ def test_large_m_tiles(name, tile, monkeypatch):
 
 def test_split_k_last_round():
     """The down GEMM's split last round with s = 2 parts (cfg3 exercises
-    s = 8): bf16, C = 1024 (4 feature blocks), H = 256 (4 slabs of K),
-    E = 4, k = 1, near-uniform routing over 22528 tokens -> about 90 token
-    blocks and 360 tiles, so on 256 CUs a last round of about 100 tiles
-    split in two, with ragged segment ends.  Routing is checked bit for bit
+    s = 8): bf16, C = 1024 (4 feature blocks), H = 1536 (24 slabs of K, the
+    fewest that the GEMM splits), E = 4, k = 1, near-uniform routing over
+    22528 tokens -> about 90 token blocks and 360 tiles, so on 256 CUs a
+    last round of about 100 tiles split in two, with ragged segment ends.  Routing is checked bit for bit
     against the oracle's; sampled output rows against the oracle's per-token
     forward under that routing (no fixture: the oracle is pinned to the
     reference by tests/test_oracle.py)."""
-    cfg = wl.MoEConfig("split_k", 22528, 1024, 4, 1, 256, "bf16", "bf16", "zero")
+    cfg = wl.MoEConfig("split_k", 22528, 1024, 4, 1, 1536, "bf16", "bf16", "zero")
     inp = wl.make_inputs(cfg, C.SEED, bias_std=0.02)
     inp.x[:] = wl.bf16_round(inp.x)
     inp.Wr[:] = wl.bf16_round(inp.Wr)
