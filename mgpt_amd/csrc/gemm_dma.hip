@@ -174,21 +174,20 @@ __device__ __forceinline__ void mfma_drain() {
 // l+32 features 8g+4..8g+7 (bf16 pairs).  Swapping two quads across the pair
 // leaves lane l with the whole 8-feature groups 0 and 2 and lane l+32 with 1
 // and 3, so each lane writes 16-byte vectors and a store covers 32 bytes of
-// each of the 32 token rows (instead of 16).  Every lane of the pair must
-// run this (it exchanges registers); `store` gates the memory writes.
+// each of the 32 token rows (instead of 16).  The swap is gfx950's
+// v_permlane32_swap (a VALU op, no LDS round trip): swap(a, b) gives lane
+// l < 32 the pair (a[l], a[l+32]) and lane l >= 32 (b[l-32], b[l]), which
+// with (a, b) = (q[0], q[1]) is each lane's 8-feature group as it is stored.
+// Every lane of the pair must run this (it exchanges registers); `store`
+// gates the memory writes.
 __device__ __forceinline__ void store_group32(bf16_t* base, const uint2 (&q)[4], int lhalf,
                                               bool store) {
-  const uint2 s0 = lhalf ? q[0] : q[1];
-  const uint2 s1 = lhalf ? q[2] : q[3];
-  uint2 r0, r1;
-  r0.x = __shfl_xor(s0.x, 32);
-  r0.y = __shfl_xor(s0.y, 32);
-  r1.x = __shfl_xor(s1.x, 32);
-  r1.y = __shfl_xor(s1.y, 32);
-  const uint4 w0 = lhalf ? make_uint4(r0.x, r0.y, q[1].x, q[1].y)
-                         : make_uint4(q[0].x, q[0].y, r0.x, r0.y);
-  const uint4 w1 = lhalf ? make_uint4(r1.x, r1.y, q[3].x, q[3].y)
-                         : make_uint4(q[2].x, q[2].y, r1.x, r1.y);
+  const auto ax = __builtin_amdgcn_permlane32_swap(q[0].x, q[1].x, false, false);
+  const auto ay = __builtin_amdgcn_permlane32_swap(q[0].y, q[1].y, false, false);
+  const auto bx = __builtin_amdgcn_permlane32_swap(q[2].x, q[3].x, false, false);
+  const auto by = __builtin_amdgcn_permlane32_swap(q[2].y, q[3].y, false, false);
+  const uint4 w0 = make_uint4(ax[0], ay[0], ax[1], ay[1]);
+  const uint4 w1 = make_uint4(bx[0], by[0], bx[1], by[1]);
   if (store) {
     *reinterpret_cast<uint4*>(base + 8 * lhalf) = w0;
     *reinterpret_cast<uint4*>(base + 16 + 8 * lhalf) = w1;
