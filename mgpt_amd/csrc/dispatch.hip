@@ -160,12 +160,24 @@ __global__ __launch_bounds__(256) void permute_kernel(
     while (ep < E) ep <<= 1;
     const int G = min(kWave, 256 / ep);
     const int e = tid / G, part = tid % G;
+    // 16 loads per lane in flight before the first add (one L2 round trip
+    // per 16 entries instead of one per entry)
+    constexpr int kHU = 16;
     int pre = 0, tot = 0;
     if (e < E) {
-      for (int bb = part; bb < nb; bb += G) {
-        const int v = hist[(size_t)e * nb + bb];
-        tot += v;
-        if (bb < b) pre += v;
+      const int32_t* hrow = hist + (size_t)e * nb;
+      for (int bb0 = part; bb0 < nb; bb0 += kHU * G) {
+        int v[kHU];
+#pragma unroll
+        for (int u = 0; u < kHU; ++u) {
+          const int bb = bb0 + u * G;
+          v[u] = bb < nb ? hrow[bb] : 0;
+        }
+#pragma unroll
+        for (int u = 0; u < kHU; ++u) {
+          tot += v[u];
+          if (bb0 + u * G < b) pre += v[u];
+        }
       }
     }
     for (int d = G / 2; d >= 1; d >>= 1) {
@@ -194,9 +206,20 @@ __global__ __launch_bounds__(256) void permute_kernel(
   if (tid < kWave) {
     const int l = tid;
     const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (kWave - l));
-    for (int f0 = 0; f0 < nflat; f0 += kWave) {
+    // every id of the block loaded before the ranking uses any
+    constexpr int kIdPerLane = kRouterTokens * kMaxTopK / kWave;
+    int ids[kIdPerLane];
+#pragma unroll
+    for (int u = 0; u < kIdPerLane; ++u) {
+      const int f = u * kWave + l;
+      ids[u] = f < nflat ? topk_idx[flat0 + f] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kIdPerLane; ++u) {
+      const int f0 = u * kWave;
+      if (f0 >= nflat) break;
       const int f = f0 + l;
-      int e = (f < nflat) ? topk_idx[flat0 + f] : -1;
+      int e = ids[u];
       // Ids outside [0, E) are skipped, as the reference's histogram and
       // gather skip them (utils/Tensor.cpp:1348, :1368).
       const bool valid = e >= 0 && e < E;
