@@ -523,151 +523,156 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
   softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks, probs);
 }
 
-// Decode-shaped logits without row normalisation (the split path's common
-// case): a block of NW waves owns 64 tokens (one per lane) and NW experts
-// (one per wave).  Column chunks of the 64 token rows are loaded with
-// coalesced 16-byte loads into registers one chunk ahead, widened to fp32
-// once (not once per expert) and stored to LDS, row stride CB + 4 floats so
-// that the 16 lanes of a 16-byte read hit 16 distinct bank groups; the NW
-// experts' weight slices of the chunk go to LDS beside them (read by a whole
-// wave at one address: a broadcast).  Each column then costs one rounded
-// product and one rounded add, in column order, the reference's sequence;
-// the LDS reads of the next 16 columns are in flight while the current 16
-// are multiplied and added.  Block (b, 0) also clears hist[.][b] for
-// router_softmax_split_kernel's atomics.
-constexpr int kFastCB = 128;   // columns per chunk
+// Logits for decode shapes with the products and the chains on different
+// waves.  A block owns kRT tokens and one expert e: wave 0 runs the 64
+// chains acc = acc + p[c] (lane t = token t, columns ascending, bias last),
+// reading four products per 16-byte LDS read, while waves 1-3 (the other
+// SIMDs) load x and W_r[e] and write the products p[t][c] = x[t][c] *
+// W_r[e][c] of the next 128-column chunk into the other half of a double
+// buffer.  The chain wave then issues one add and a quarter of an LDS read
+// per column instead of a product, an add and two half reads; the rounding
+// sequence (one rounded product, one rounded add per term) is unchanged.
+// Loads run two chunks ahead in registers.  hist[e][block] is cleared for
+// router_softmax_wave_kernel.  Measured at cfg5 (64 tokens, C = 2048, E =
+// 64): 15 us, against 23 us for four experts' chains per block with each
+// wave forming its own products; the chains alone (products skipped) take
+// 10.8 us, 2048 dependent fp32 adds of about 11 cycles each, which no
+// block shape shortens.
 template <int V>
 struct IntC {
   static constexpr int value = V;
 };
-template <typename ActT, int NW>
-__global__ __launch_bounds__(NW * 64) void router_logits_fast_kernel(
+constexpr int kPcCB = 128;            // columns per chunk
+constexpr int kPcLD = kPcCB + 4;      // floats per LDS product row
+constexpr int kPcTokStep = 6;         // tokens between one lane's pieces (192 lanes / 32 quads)
+constexpr int kPcPieces = (kRT + kPcTokStep - 1) / kPcTokStep;   // pieces per lane and chunk
+// register stages: loads run two chunks ahead (three measured no faster)
+constexpr int kPcStages = 3;
+template <typename ActT> struct PcPiece;
+template <> struct PcPiece<bf16_t> {
+  using type = uint2;   // 4 bf16
+  __device__ static float4 widen(const uint2& q) {
+    return make_float4(__uint_as_float(q.x << 16), __uint_as_float(q.x & 0xFFFF0000u),
+                       __uint_as_float(q.y << 16), __uint_as_float(q.y & 0xFFFF0000u));
+  }
+};
+template <> struct PcPiece<float> {
+  using type = uint4;   // 4 fp32
+  __device__ static float4 widen(const uint4& q) {
+    return make_float4(__uint_as_float(q.x), __uint_as_float(q.y), __uint_as_float(q.z),
+                       __uint_as_float(q.w));
+  }
+};
+template <typename ActT>
+__global__ __launch_bounds__(256) void router_logits_pc_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr1, const float* __restrict__ br,
     int N, int C, int E, float* __restrict__ logits, int32_t* __restrict__ hist, int nb) {
-  constexpr int LD = kFastCB + 4;                                  // floats per LDS row
-  constexpr int kPer = 16 / (int)sizeof(ActT);                     // columns per 16-byte piece
-  constexpr int kPieces = kRT * kFastCB / kPer;                    // x pieces per chunk
-  constexpr int kPPT = kPieces / (NW * 64);                        // x pieces per thread
-  constexpr int kWPieces = NW * kFastCB / 4;                       // weight float4 per chunk
-  static_assert(kPieces % (NW * 64) == 0 && kWPieces <= NW * 64, "chunk split");
-  __shared__ float4 s_x[2][kRT * LD / 4];
-  __shared__ float4 s_w[2][NW][kFastCB / 4];
+  __shared__ float4 s_p[2][kRT * kPcLD / 4];
   const int tid = threadIdx.x;
   const int lane = lane_id();
-  const int g = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int tok0 = blockIdx.x * kRT;
+  const int e = blockIdx.y;
   const int last_row = min(kRT, N - tok0) - 1;
-  if (blockIdx.y == 0 && tid < E) hist[(size_t)tid * nb + blockIdx.x] = 0;
-  // the weight float4 this thread stages: expert row tid / (CB/4) of the block
-  const int we = min((int)blockIdx.y * NW + tid / (kFastCB / 4), E - 1);
-  const int wq4 = tid % (kFastCB / 4);
-
-  // two register stages: chunk c + 2 is requested while chunk c's chain
-  // runs, so its loads have a chain's time to land before they are moved to
-  // LDS (deeper staging measured no faster: the chain bounds the kernel)
-  uint4 raws[2][kPPT];
-  // initialised: with undefined lanes (threads that stage no weights) the
-  // compiler's code for the loop measured 8 us slower at cfg5
-  float4 wraws[2] = {make_float4(0.f, 0.f, 0.f, 0.f), make_float4(0.f, 0.f, 0.f, 0.f)};
-  auto load = [&](int c0, int cnum, uint4 (&raw)[kPPT], float4& wraw) __attribute__((always_inline)) {
-    const int ppr = cnum / kPer;
+  if (e == 0 && tid < E) hist[(size_t)tid * nb + blockIdx.x] = 0;
+  const int nch = (C + kPcCB - 1) / kPcCB;
+  auto cols = [&](int ch) { return min(kPcCB, C - ch * kPcCB); };   // a multiple of 64
+  if (w == 0) {
+    float acc = 0.0f;
+    const float4* prow0 = &s_p[0][lane * kPcLD / 4];
+    const float4* prow1 = &s_p[1][lane * kPcLD / 4];
+    auto consume = [&](int ch) __attribute__((always_inline)) {
+      const float4* pr = (ch & 1) ? prow1 : prow0;
+      // all of the chunk's reads first (the scheduler otherwise keeps one
+      // or two ahead and the chain waits an LDS latency every 8 columns)
+      auto run = [&](auto n4_c) __attribute__((always_inline)) {
+        constexpr int n4 = decltype(n4_c)::value;
+        float4 p[n4];
 #pragma unroll
-    for (int i = 0; i < kPPT; ++i) {
-      const int p = tid + i * NW * 64;
-      const int r = p / (kFastCB / kPer), cp = p % (kFastCB / kPer);
-      raw[i] = cp < ppr ? *reinterpret_cast<const uint4*>(
-                              x + (size_t)(tok0 + min(r, last_row)) * C + c0 + cp * kPer)
-                        : make_uint4(0u, 0u, 0u, 0u);
+        for (int u = 0; u < n4; ++u) p[u] = pr[u];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < n4; ++u) {
+          acc = acc + p[u].x;
+          acc = acc + p[u].y;
+          acc = acc + p[u].z;
+          acc = acc + p[u].w;
+        }
+      };
+      if (cols(ch) == kPcCB)
+        run(IntC<kPcCB / 4>{});
+      else
+        run(IntC<16>{});   // a last chunk of 64 columns
+    };
+    for (int i = 0; i <= nch; ++i) {
+      if (i >= 1) consume(i - 1);
+      __syncthreads();
     }
-    if (tid < kWPieces && 4 * wq4 < cnum)
-      wraw = *reinterpret_cast<const float4*>(wr1 + (size_t)we * C + c0 + 4 * wq4);
-  };
-  auto store = [&](int b, const uint4 (&raw)[kPPT], const float4& wraw) __attribute__((always_inline)) {
+    if (lane <= last_row) logits[(size_t)(tok0 + lane) * E + e] = acc + br[e];
+  } else {
+    using PT = PcPiece<ActT>;
+    using Piece = typename PT::type;
+    const int pl = (w - 1) * kWave + lane;   // 0 .. 191
+    const int c4 = pl % 32;                  // this lane's column quad in every chunk
+    const int tq = pl / 32;                  // its first token; then every kPcTokStep-th
+    const float* wrow = wr1 + (size_t)e * C;
+    Piece xs[kPcStages][kPcPieces];
+    float4 ws[kPcStages];
+    // Every lane issues the same loads in every chunk (lanes past a 64-column
+    // last chunk read a column quad that is in bounds and skip its
+    // products): with a lane-dependent load count the compiler can only
+    // wait for all loads (vmcnt(0)), which would also wait for the chunk
+    // requested two ahead.
+    auto load = [&](int ch, Piece (&xv)[kPcPieces], float4& wv) __attribute__((always_inline)) {
+      const int c0 = ch * kPcCB + min(4 * c4, cols(ch) - 4);
 #pragma unroll
-    for (int i = 0; i < kPPT; ++i) {
-      const int p = tid + i * NW * 64;
-      const int r = p / (kFastCB / kPer), cp = p % (kFastCB / kPer);
-      float4* dst = &s_x[b][(r * LD + cp * kPer) / 4];
-      if constexpr (kPer == 8) {
-        dst[0] = make_float4(widen<bf16_t>(raw[i], 0), widen<bf16_t>(raw[i], 1),
-                             widen<bf16_t>(raw[i], 2), widen<bf16_t>(raw[i], 3));
-        dst[1] = make_float4(widen<bf16_t>(raw[i], 4), widen<bf16_t>(raw[i], 5),
-                             widen<bf16_t>(raw[i], 6), widen<bf16_t>(raw[i], 7));
-      } else {
-        dst[0] = make_float4(__uint_as_float(raw[i].x), __uint_as_float(raw[i].y),
-                             __uint_as_float(raw[i].z), __uint_as_float(raw[i].w));
+      for (int j = 0; j < kPcPieces; ++j) {
+        const int t = min(tq + kPcTokStep * j, last_row);
+        xv[j] = *reinterpret_cast<const Piece*>(x + (size_t)(tok0 + t) * C + c0);
       }
-    }
-    if (tid < kWPieces) s_w[b][tid / (kFastCB / 4)][wq4] = wraw;
-  };
-
-  float acc = 0.0f;
-  const int nch = (C + kFastCB - 1) / kFastCB;
-  auto cols = [&](int ch) { return min(kFastCB, C - ch * kFastCB); };   // a multiple of 64
-  load(0, cols(0), raws[0], wraws[0]);
-  if (nch > 1) load(kFastCB, cols(1), raws[1], wraws[1]);
-  store(0, raws[0], wraws[0]);
-  __syncthreads();
-  // chunk ch: request ch + 2 into the register stage ch left, run ch's
-  // chain from LDS, then move ch + 1 (requested a chain earlier) into LDS
-  auto step = [&](int ch, uint4 (&mine)[kPPT], float4& wmine, const uint4 (&nxt)[kPPT],
-                  const float4& wnxt) __attribute__((always_inline)) {
-    const int b = ch & 1;
-    if (ch + 2 < nch) load((ch + 2) * kFastCB, cols(ch + 2), mine, wmine);
-    const float4* xr = &s_x[b][lane * LD / 4];
-    const float4* wr = s_w[b][g];
-    // a fixed-size, fully unrolled chunk lets the compiler keep the LDS
-    // reads of later columns in flight during the chain
-    auto chain = [&](auto n4_c) __attribute__((always_inline)) {
-      constexpr int n4 = decltype(n4_c)::value;   // a multiple of 8
-      float4 xa[4], wa[4], xb[4], wb[4];
-      auto rd = [&](int u, float4 (&xv)[4], float4 (&wv)[4]) __attribute__((always_inline)) {
+      wv = *reinterpret_cast<const float4*>(wrow + c0);
+    };
+    auto compute = [&](int ch, const Piece (&xv)[kPcPieces], const float4& wv)
+        __attribute__((always_inline)) {
+      if (4 * c4 >= cols(ch)) return;
+      float4* dst = s_p[ch & 1];
+      // every product first, then the LDS writes: the chain wave's reads of
+      // the previous chunk (issued at the same barrier) meet fewer writes
+      float4 pv[kPcPieces];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          xv[v] = xr[u + v];
-          wv[v] = wr[u + v];
-        }
-      };
-      // the 16 products first (independent), then the 16 dependent adds:
-      // each add then waits only for the previous add, not for a product
-      // issued just before it
-      auto mul_add = [&](const float4 (&xv)[4], const float4 (&wv)[4])
-          __attribute__((always_inline)) {
-        float pr[16];
+      for (int j = 0; j < kPcPieces; ++j) {
+        const float4 xf = PT::widen(xv[j]);
+        pv[j] = make_float4(xf.x * wv.x, xf.y * wv.y, xf.z * wv.z, xf.w * wv.w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          pr[4 * v + 0] = xv[v].x * wv[v].x;
-          pr[4 * v + 1] = xv[v].y * wv[v].y;
-          pr[4 * v + 2] = xv[v].z * wv[v].z;
-          pr[4 * v + 3] = xv[v].w * wv[v].w;
-        }
-#pragma unroll
-        for (int j = 0; j < 16; ++j) acc = acc + pr[j];
-      };
-      rd(0, xa, wa);
-#pragma unroll
-      for (int u = 0; u < n4; u += 8) {
-        rd(u + 4, xb, wb);
-        mul_add(xa, wa);
-        if (u + 8 < n4) rd(u + 8, xa, wa);
-        mul_add(xb, wb);
+      for (int j = 0; j < kPcPieces; ++j) {
+        const int t = tq + kPcTokStep * j;
+        if (t < kRT) dst[(t * kPcLD) / 4 + c4] = pv[j];
       }
     };
-    if (cols(ch) == kFastCB)
-      chain(IntC<kFastCB / 4>{});
-    else
-      chain(IntC<16>{});   // a last chunk of 64 columns
-    if (ch + 1 < nch) {
-      store(b ^ 1, nxt, wnxt);
-      __syncthreads();   // the next chunk is in LDS, every wave done with this one
+    // iteration i: request chunk i + kPcStages - 1, write chunk i's
+    // products, meet the chain wave (which consumes chunk i - 1 meanwhile)
+    auto step = [&](int i, auto s_c) __attribute__((always_inline)) {
+      constexpr int st = decltype(s_c)::value;                    // chunk i's stage
+      constexpr int ahead = (st + kPcStages - 1) % kPcStages;     // i + kPcStages - 1's
+      if (i > nch) return;
+      // past the last chunk the request repeats it (in bounds, never used),
+      // so that every step issues the same loads
+      load(min(i + kPcStages - 1, nch - 1), xs[ahead], ws[ahead]);
+      if (i < nch) compute(i, xs[st], ws[st]);
+      __syncthreads();
+    };
+#pragma unroll
+    for (int j = 0; j < kPcStages - 1; ++j) load(min(j, nch - 1), xs[j], ws[j]);
+    for (int i = 0; i <= nch; i += kPcStages) {
+      step(i, IntC<0>{});
+      step(i + 1, IntC<1>{});
+      step(i + 2, IntC<2>{});
+      if constexpr (kPcStages > 3) step(i + 3, IntC<3>{});
+      static_assert(kPcStages == 3 || kPcStages == 4, "stages");
     }
-  };
-  for (int ch = 0; ch < nch; ch += 2) {
-    step(ch, raws[0], wraws[0], raws[1], wraws[1]);
-    if (ch + 1 < nch) step(ch + 1, raws[1], wraws[1], raws[0], wraws[0]);
   }
-  const int ew = blockIdx.y * NW + g;
-  if (ew < E && lane <= last_row) logits[(size_t)(tok0 + lane) * E + ew] = acc + br[ew];
 }
 
 // Softmax, top-k and histogram for decode shapes: one wave per token, lane e
@@ -679,7 +684,7 @@ __global__ __launch_bounds__(NW * 64) void router_logits_fast_kernel(
 // reference's insertion top-k with a strict '>' produces -- is the number of
 // experts before it; ranks below k are the choices, written at their rank,
 // and counted into hist[e][token / 64] with integer atomics
-// (router_logits_fast_kernel cleared those entries).  No shuffles or merge
+// (router_logits_pc_kernel cleared those entries).  No shuffles or merge
 // rounds: four passes over the row in LDS, latency hidden across lanes.
 constexpr int kSoftmaxWaves = 4;   // tokens per block
 __global__ __launch_bounds__(kSoftmaxWaves * 64) void router_softmax_wave_kernel(
@@ -728,15 +733,6 @@ __global__ __launch_bounds__(kSoftmaxWaves * 64) void router_softmax_wave_kernel
   }
 }
 
-// Waves (experts) per block of router_logits_fast_kernel.  Measured at cfg5:
-// 4 waves 23 us, 2 waves 26 us, 8 waves 26.5 us.  The chain costs about the
-// same number of cycles per wave whatever the block shape (s_memtime
-// stamps): one wave issues two 16-byte LDS reads and eight VALU operations
-// per 4 columns, and that issue stream, not LDS bandwidth or load latency,
-// bounds it.
-#ifndef MGPT_ROUTER_FAST_WAVES
-#define MGPT_ROUTER_FAST_WAVES 4
-#endif
 
 }  // namespace
 
@@ -755,11 +751,10 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
   if (logits && !gamma) {
-    // decode shapes without normalisation: the lean chain kernel, then the
-    // softmax / top-k with one wave per token
-    constexpr int NW = MGPT_ROUTER_FAST_WAVES;
-    hipLaunchKernelGGL((router_logits_fast_kernel<ActT, NW>), dim3(nb, (E + NW - 1) / NW),
-                       dim3(NW * kWave), 0, stream, x, wr1, br, N, C, E, logits, hist, nb);
+    // decode shapes without normalisation: products and chains on separate
+    // waves, then the softmax / top-k with one wave per token
+    hipLaunchKernelGGL((router_logits_pc_kernel<ActT>), dim3(nb, E), dim3(256), 0, stream, x, wr1,
+                       br, N, C, E, logits, hist, nb);
     hipLaunchKernelGGL(router_softmax_wave_kernel, dim3((N + kSoftmaxWaves - 1) / kSoftmaxWaves),
                        dim3(kSoftmaxWaves * kWave), 0, stream, logits, N, E, k, topk_idx, topk_p,
                        hist, nb, probs);
