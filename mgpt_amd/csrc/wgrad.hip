@@ -518,12 +518,16 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
 #pragma unroll
   for (int q = 0; q < 8; ++q) bsum[q] = 0.0f;
 
-  dma_slab(0);
-  dma_slab(1);
-  dma_slab(2);
-  for (int kt = 0; kt < KT; ++kt) {
+  // Slab s becomes readable at its barrier: its DMA has landed, and every
+  // wave has finished its reads of slab s - 1, whose stage then takes the
+  // DMA of slab s + 3.  A slab's two 16-row k-steps are software-pipelined
+  // across the barrier: the barrier of slab s + 1 sits between the MFMAs
+  // of slab s's k-steps, so the fragment reads of slab s + 1 (issued just
+  // after it) have the MFMAs of slab s's second k-step to hide their
+  // latency instead of stalling behind the barrier.
+  static_assert(kTrBK == 32, "two k-steps per slab");
+  auto enter_slab = [&](int kt) __attribute__((always_inline)) {
     tr_wait_barrier<8>();
-    const char* st = smem + (kt % kTrStages) * kTrStageBytes;
     const int valid = cnt - kt * kTrBK;
     if (valid < kTrBK) {
       // last slab: rows past the segment (other experts' rows or padding)
@@ -539,7 +543,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
     }
     dma_slab(kt + 3);   // into the stage of slab kt-1, which every wave has finished
     if (do_bias) {
-      const char* qs = st + kTrOpBytes;
+      const char* qs = smem + (kt % kTrStages) * kTrStageBytes + kTrOpBytes;
       const int fb = tid & 31, c = fb >> 2, sub = fb & 3;
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
@@ -554,27 +558,37 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
         }
       }
     }
-    const char* ps = st;
-    const char* qs = st + kTrOpBytes;
-    bf16x8 af[2][TI], bfr[2][TJ];
-    auto frags = [&](int ks, bf16x8 (&a)[TI], bf16x8 (&b)[TJ]) __attribute__((always_inline)) {
-      const int kb = ks * 16 + krow;
+  };
+  bf16x8 af[2][TI], bfr[2][TJ];
+  auto frags = [&](int kt, int ks, bf16x8 (&a)[TI], bf16x8 (&b)[TJ]) __attribute__((always_inline)) {
+    const char* ps = smem + (kt % kTrStages) * kTrStageBytes;
+    const char* qs = ps + kTrOpBytes;
+    const int kb = ks * 16 + krow;
 #pragma unroll
-      for (int ti = 0; ti < TI; ++ti) a[ti] = tr_frag(ps, kb, wi * 4 + ti, moff);
+    for (int ti = 0; ti < TI; ++ti) a[ti] = tr_frag(ps, kb, wi * 4 + ti, moff);
 #pragma unroll
-      for (int tj = 0; tj < TJ; ++tj) b[tj] = tr_frag(qs, kb, wj * 2 + tj, moff);
-    };
-    frags(0, af[0], bfr[0]);
+    for (int tj = 0; tj < TJ; ++tj) b[tj] = tr_frag(qs, kb, wj * 2 + tj, moff);
+  };
+  auto mfmas = [&](const bf16x8 (&a)[TI], const bf16x8 (&b)[TJ]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < kTrBK / 16; ++ks) {
-      if (ks + 1 < kTrBK / 16) frags(ks + 1, af[(ks + 1) & 1], bfr[(ks + 1) & 1]);
+    for (int ti = 0; ti < TI; ++ti)
 #pragma unroll
-      for (int ti = 0; ti < TI; ++ti)
-#pragma unroll
-        for (int tj = 0; tj < TJ; ++tj)
-          acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][ti], bfr[ks & 1][tj],
-                                                                acc[ti][tj], 0, 0, 0);
+      for (int tj = 0; tj < TJ; ++tj)
+        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[ti], b[tj], acc[ti][tj], 0, 0, 0);
+  };
+  dma_slab(0);
+  dma_slab(1);
+  dma_slab(2);
+  enter_slab(0);
+  frags(0, 0, af[0], bfr[0]);
+  for (int kt = 0; kt < KT; ++kt) {
+    frags(kt, 1, af[1], bfr[1]);
+    mfmas(af[0], bfr[0]);
+    if (kt + 1 < KT) {
+      enter_slab(kt + 1);
+      frags(kt + 1, 0, af[0], bfr[0]);
     }
+    mfmas(af[1], bfr[1]);
   }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the repeated tail loads
 
