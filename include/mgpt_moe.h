@@ -228,7 +228,11 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
  * waits for the last profiled forward and returns the mean stage durations
  * in ms over the recorded forwards: [0] router+top-k+histogram, [1] dispatch
  * (count scan + permutation), [2] gate/up GEMM + SwiGLU, [3] down GEMM,
- * [4] combine; if n > 5, ms[5] receives the number of forwards averaged. */
+ * [4] combine; if n > 5, ms[5] receives the number of forwards averaged.
+ * enable: 0 off, 1 every stage boundary, 2 only the two boundaries of the
+ * gate/up GEMM (the other launches keep their spacing; stage_times then
+ * returns -1 for the other stages).  The backward records its stages
+ * whenever enable is nonzero. */
 #define MGPT_MOE_NUM_STAGES 5
 int mgpt_moe_set_profiling(mgpt_moe* h, int enable);
 int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n);

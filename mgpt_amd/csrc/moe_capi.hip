@@ -221,6 +221,7 @@ struct mgpt_moe {
   // i % kProfSlots; stage_times averages over the recorded slots.
   static constexpr int kProfSlots = 64;
   bool profiling = false;
+  bool prof_gemm_only = false;   // forward: only the gate/up GEMM's two boundaries
   hipEvent_t ev[kProfSlots][MGPT_MOE_NUM_STAGES + 1] = {};
   int prof_count = 0;
   hipEvent_t evb[kProfSlots][MGPT_MOE_NUM_BWD_STAGES + 1] = {};
@@ -661,8 +662,11 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
   HIP_TRY(hipStreamIsCapturing(st, &cap));
   const bool capturing = cap != hipStreamCaptureStatusNone;
   const bool prof = h->profiling && !capturing;
+  const bool gemm_only = h->prof_gemm_only;
   hipEvent_t* evs = h->ev[h->prof_count % mgpt_moe::kProfSlots];
-  auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
+  auto mark = [&](int i) -> hipError_t {
+    return prof && (!gemm_only || i == 2 || i == 3) ? hipEventRecord(evs[i], st) : hipSuccess;
+  };
 
   HIP_TRY(mark(0));
   // A caller width that is not a multiple of 64: the rows (and gamma) are
@@ -1164,7 +1168,9 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts) {
 
 int mgpt_moe_set_profiling(mgpt_moe* h, int enable) {
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
+  if (enable < 0 || enable > 2) return fail(MGPT_ERR_INVALID_ARGUMENT, "enable must be 0, 1 or 2");
   h->profiling = enable != 0;
+  h->prof_gemm_only = enable == 2;
   h->prof_count = 0;
   h->prof_b_count = 0;
   return MGPT_OK;
@@ -1196,8 +1202,12 @@ int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n) {
   if (h->prof_count == 0) return fail(MGPT_ERR_NOT_READY, "no profiled forward has been run");
   const int slots = std::min(h->prof_count, mgpt_moe::kProfSlots);
   const int last = (h->prof_count - 1) % mgpt_moe::kProfSlots;
-  HIP_TRY(hipEventSynchronize(h->ev[last][MGPT_MOE_NUM_STAGES]));
+  HIP_TRY(hipEventSynchronize(h->ev[last][h->prof_gemm_only ? 3 : MGPT_MOE_NUM_STAGES]));
   for (int i = 0; i < MGPT_MOE_NUM_STAGES; ++i) {
+    if (h->prof_gemm_only && i != 2) {
+      ms[i] = -1.0f;   // not recorded in this mode
+      continue;
+    }
     double sum = 0.0;
     for (int s = 0; s < slots; ++s) {
       float t = 0.0f;

@@ -260,8 +260,12 @@ class MoELayer:
         return [float(v) for v in c]
 
     # ----------------------------------------------------------- measurement
-    def set_profiling(self, on: bool) -> None:
-        capi.check(capi.lib().mgpt_moe_set_profiling(self._h, int(on)))
+    def set_profiling(self, on: bool, gemm_only: bool = False) -> None:
+        """Record HIP events at the forward's stage boundaries (gemm_only:
+        only around the gate/up GEMM, leaving the other launches' spacing
+        as it is unprofiled)."""
+        mode = 0 if not on else (2 if gemm_only else 1)
+        capi.check(capi.lib().mgpt_moe_set_profiling(self._h, mode))
 
     def stage_times(self) -> dict:
         """Mean stage durations (ms) over the profiled forwards since

@@ -278,6 +278,33 @@ def test_deterministic_and_repeatable():
         assert np.array_equal(y.view(np.uint32), ys[0].view(np.uint32))
 
 
+def test_profiling_modes():
+    """Stage timing: mode 1 times every stage; mode 2 (events only around the
+    gate/up GEMM, as bench.py's timed steps use it) times that stage and
+    reports -1 for the others; the profiled forwards give the same output as
+    unprofiled ones; a mode outside 0..2 is refused."""
+    from mgpt_amd import capi
+    case = C.ALL_CASES["bf16_large_m"]
+    inp = C.build_inputs(case)
+    layer, y0, _, _, _ = run_gpu(inp)
+    x = torch.from_numpy(np.ascontiguousarray(inp.x)).to("cuda").to(torch.bfloat16)
+    for gemm_only in (False, True):
+        layer.set_profiling(True, gemm_only=gemm_only)
+        for _ in range(3):
+            y = layer.forward(x)
+        st = layer.stage_times()
+        layer.set_profiling(False)
+        assert st["forwards"] == 3
+        assert np.array_equal(y.float().cpu().numpy().view(np.uint32), y0.view(np.uint32))
+        assert st["gemm_gateup"] > 0.0
+        others = [v for k, v in st.items() if k not in ("gemm_gateup", "forwards")]
+        if gemm_only:
+            assert all(v == -1.0 for v in others), st
+        else:
+            assert all(v > 0.0 for v in others), st
+    assert capi.lib().mgpt_moe_set_profiling(layer._h, 3) == capi.MGPT_ERR_INVALID_ARGUMENT
+
+
 def test_device_expf_matches_host_expf():
     from mgpt_amd import capi
     # every 61st float in [-104, -0] plus the edges of the special-case paths
