@@ -12,11 +12,12 @@ dominant kernel (the gate/up grouped GEMM, MFMA-bound) measured with HIP
 events inside the timed region, and the reference CPU path timed on a
 bounded sample of the same workload on this host.
 
---pass train measures a training step instead (the training forward, which
-also keeps the backward's caches, then the backward with dy ~ N(0,1)):
-tokens/s of forward + backward, the forward and backward stage times, the
-roofline of the backward's dominant GEMM, and the reference's CPU forward +
-backward on a sample.
+--pass train measures a training step instead, in the reference Trainer's
+per-step order (pipeline/Trainer.cpp:303-305, then forward and backward):
+zero_grad, the training forward (which also keeps the backward's caches),
+then the backward with dy ~ N(0,1).  It reports tokens/s of the step, the
+forward and backward stage times, the roofline of the backward's dominant
+GEMM, and the reference's CPU zero_grad + forward + backward on a sample.
 
 --pass block measures the fused MoE half of a transformer block,
 out = x + MoE(RMSNorm(x) * gamma) (mgpt_moe_forward_block), beside the same
@@ -48,7 +49,7 @@ PEAK_F32_TFLOPS = 157.3      # MI355X dense fp32 matrix
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 METRIC = "MoE layer tokens/s + expert-GEMM % MFMA peak (N=16384,C=1024,E=16,k=2)"
-METRIC_TRAIN = ("MoE layer training tokens/s, forward + backward "
+METRIC_TRAIN = ("MoE layer training tokens/s, zero_grad + forward + backward "
                 "(N=16384,C=1024,E=16,k=2)")
 METRIC_DECODE = ("MoE decode steps/s in the sampling loop (Generator B=1, no KV cache, "
                  "context S=64, C=2048, E=64, k=8, H=1408, fp8 weights)")
@@ -199,8 +200,8 @@ def cpu_sample_tokens(cfg) -> int:
 
 
 def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
-    """The reference's own CPU MoE forward (train: forward + backward; block:
-    ln2 RMSNormLayer + forward + residual add)
+    """The reference's own CPU MoE forward (train: zero_grad + forward +
+    backward; block: ln2 RMSNormLayer + forward + residual add)
     (oracle/_ref/ref_driver, built from the unmodified reference sources),
     single-threaded as the reference is, on `sample_tokens` tokens of the
     workload's shape."""
@@ -209,7 +210,7 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
         return None
     sub = {"forward": "bench", "train": "bench_train", "block": "bench_block"}[mode]
     what = {"forward": "MoELayer::forward_into",
-            "train": "MoELayer::forward_into + backward_into",
+            "train": "Tensor::zero_grad + MoELayer::forward_into + backward_into",
             "block": "RMSNormLayer::forward_into + MoELayer::forward_into + Tensor::add_into"}[mode]
     cmd = [drv, sub, str(sample_tokens), str(cfg.C), str(cfg.H),
            str(cfg.E), str(cfg.k), str(reps)]
@@ -248,7 +249,7 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
     cmd = (f"rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python bench.py "
            f"{cfg_arg}{extra.strip()} --steps {b['steps']} --warmup {b['warmup']} "
            "--no-cpu-baseline").replace("  ", " ")
-    what = {"train": "training step (forward + backward)",
+    what = {"train": "training step (zero_grad + forward + backward)",
             "block": "fused block (RMSNorm + MoE + residual)",
             "decode": "decode steps in the sampling loop"}.get(mode, "forward")
     runs = {"train": f"{b['warmup'] + b['steps']} training steps ({b['warmup']} warmup + "
@@ -338,7 +339,7 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--pass", dest="mode", choices=["forward", "train", "block", "decode"],
                     default="forward",
-                    help="forward (default, the headline), train (forward + backward), "
+                    help="forward (default, the headline), train (zero_grad + forward + backward), "
                          "block (RMSNorm + MoE + residual, fused) or decode (the sampling "
                          "loop at cfg5's shape)")
     ap.add_argument("--calib-copy", action="store_true",
@@ -417,6 +418,8 @@ def main() -> int:
         if block:
             layer.forward_block_into(x, gamma, eps, y)
             return
+        if train:
+            layer.zero_grad()
         layer.forward_into(x, y, train)
         if train:
             layer.backward_into(dy, dx)
@@ -545,7 +548,7 @@ def main() -> int:
         bwd_ms = sum(bstages.values())
         result.update({
             "metric": METRIC_TRAIN,
-            "pass": "train (forward_train + backward)",
+            "pass": "train (zero_grad + forward_train + backward)",
             "layer_tflops": round(train_flops / (ms_per_step * 1e-3) / 1e12, 2),
             "backward_stage_ms": {kk: round(v, 4) for kk, v in bstages.items()},
             "backward_ms": round(bwd_ms, 4),

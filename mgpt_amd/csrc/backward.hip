@@ -278,10 +278,11 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
 // entries followed by the E bias entries, as a fixed two-level tree (so the
 // result does not depend on scheduling): a block takes 16 entries; thread
 // (entry, g) adds the g-th of 16 consecutive chunk ranges in order, then
-// one thread per entry adds the 16 range sums in order.
+// one thread per entry adds the 16 range sums in order.  With `store` the
+// gradient is taken to be zero and the sum is written without reading it.
 __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(
     const float* __restrict__ partial, const float* __restrict__ partial_b, int chunks, int CE,
-    int E, float* __restrict__ gW, float* __restrict__ gb) {
+    int E, float* __restrict__ gW, float* __restrict__ gb, int store) {
   __shared__ float s_part[16][16];
   const int el = threadIdx.x % 16, g = threadIdx.x / 16;
   const int i = blockIdx.x * 16 + el;
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(
 #pragma unroll
     for (int q = 0; q < 16; ++q) t += s_part[q][el];
     float* o = w ? gW + i : gb + (i - CE);
-    *o = *o + t;
+    *o = store ? t : *o + t;
   }
 }
 
@@ -376,7 +377,7 @@ int router_wgrad_chunks(int N) { return (N + kRwChunk - 1) / kRwChunk; }
 template <typename ActT>
 hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int E,
                                float* partial, float* partial_b, float* gW, float* gb,
-                               hipStream_t stream) {
+                               bool store, hipStream_t stream) {
   if (N <= 0) return hipSuccess;
   const int chunks = router_wgrad_chunks(N);
   const dim3 grid((C + 255) / 256, chunks);
@@ -391,7 +392,7 @@ hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int
                        E, partial, partial_b);
   const int CE = C * E;
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 15) / 16), dim3(256), 0, stream,
-                     partial, partial_b, chunks, CE, E, gW, gb);
+                     partial, partial_b, chunks, CE, E, gW, gb, (int)store);
   return hipGetLastError();
 }
 
@@ -413,7 +414,7 @@ hipError_t launch_transpose_pad(const T* src, int src_rows, int src_cols, size_t
                                           const float*, int, int, int, int, T*, float*,        \
                                           hipStream_t);                                        \
   template hipError_t launch_router_wgrad<T>(const T*, const float*, int, int, int, float*,    \
-                                             float*, float*, float*, hipStream_t);             \
+                                             float*, float*, float*, bool, hipStream_t);       \
   template hipError_t launch_transpose_pad<T>(const T*, int, int, size_t, T*, int, int, size_t, \
                                               int, hipStream_t);
 MGPT_INST_BWD(bf16_t)

@@ -148,4 +148,14 @@ struct AddJobs {
   int n;
 };
 
+// Per-expert gradient slices (expert e's slice of piece p: base[p] +
+// e * len[p], len[p] floats) that launch_zero_idle_experts clears for the
+// experts without rows; passed by value as a kernel argument.
+struct IdleSlices {
+  static constexpr int kMax = 6;
+  float* base[kMax];
+  size_t len[kMax];
+  int n;
+};
+
 }  // namespace mgpt

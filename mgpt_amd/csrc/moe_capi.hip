@@ -74,14 +74,15 @@ hipError_t launch_token_bwd(const ActT*, const int32_t*, const int32_t*, const f
 int router_wgrad_chunks(int N);
 template <typename ActT>
 hipError_t launch_router_wgrad(const ActT*, const float*, int, int, int, float*, float*, float*,
-                               float*, hipStream_t);
+                               float*, bool, hipStream_t);
 template <typename T>
 hipError_t launch_transpose_pad(const T*, int, int, size_t, T*, int, int, size_t, int,
                                 hipStream_t);
 template <typename T, int MODE>
 hipError_t launch_wgrad(const T*, int, int, const T*, int, int, const int32_t*, int, float*,
                         float*, int, size_t, int, int, float*, float*, size_t, int, float*,
-                        size_t, float*, size_t, int, hipStream_t);
+                        size_t, float*, size_t, int, bool, hipStream_t);
+hipError_t launch_zero_idle_experts(const int32_t*, int, const IdleSlices&, hipStream_t);
 hipError_t launch_tile_fp8(const uint8_t*, int, int, int, uint8_t*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
@@ -217,6 +218,10 @@ struct mgpt_moe {
                            // gWu [E][C][H], gbu [E][H], gWd [E][H][C], gbd [E][C]
   size_t g_off[8] = {};
   size_t g_total = 0;
+  // The gradients are zero without the buffer holding zeros (set by
+  // zero_grad and at allocation): the next backward writes every gradient
+  // instead of adding to it, and a read clears the buffer first.
+  bool grad_zero = false;
   // Profiling ring: forward i records its stage boundaries into slot
   // i % kProfSlots; stage_times averages over the recorded slots.
   static constexpr int kProfSlots = 64;
@@ -339,8 +344,8 @@ void free_weights(mgpt_moe* h) {
 // inference option).
 bool trainable(const mgpt_moe* h) { return h->wdt == h->act && h->io == h->act; }
 
-// Allocates and zeroes the gradient buffer on first use (stream-ordered).
-int ensure_grad(mgpt_moe* h, hipStream_t st) {
+// Allocates the gradient buffer on first use, its contents logically zero.
+int ensure_grad(mgpt_moe* h) {
   if (h->grad) return MGPT_OK;
   const size_t C = h->C, H = h->H, E = h->E;
   const size_t sizes[8] = {C * E, E, E * C * H, E * H, E * C * H, E * H, E * H * C, E * C};
@@ -351,7 +356,18 @@ int ensure_grad(mgpt_moe* h, hipStream_t st) {
   }
   h->g_total = off;
   HIP_TRY(hipMalloc(&h->grad, sizeof(float) * off));
-  HIP_TRY(hipMemsetAsync(h->grad, 0, sizeof(float) * off, st));
+  h->grad_zero = true;
+  return MGPT_OK;
+}
+
+// The gradient buffer with its contents, zeroing it (stream-ordered) if
+// it is only logically zero.
+int materialize_grad(mgpt_moe* h, hipStream_t st) {
+  if (int rc = ensure_grad(h)) return rc;
+  if (h->grad_zero) {
+    HIP_TRY(hipMemsetAsync(h->grad, 0, sizeof(float) * h->g_total, st));
+    h->grad_zero = false;
+  }
   return MGPT_OK;
 }
 
@@ -791,7 +807,7 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   const Layout L = h->layout(N, true);
   const int C = h->C, Cx = h->Cx, H = h->H, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
   const int A = N * k;
-  if (int rc = ensure_grad(h, st)) return rc;
+  if (int rc = ensure_grad(h)) return rc;
   if (int rc = ensure_bwd_weights(h, st)) return rc;
   // padded width: dy in and dx out through zero-padded rows; x is the padded
   // copy the training forward left in the workspace
@@ -875,21 +891,37 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   const size_t wpart_bytes = wpart ? (size_t)h->num_cus * kGemmPartialBytes : 0;
   float* wbpart = h->uses_gemm_dma(N) ? (float*)(ws + L.wg_bpart) : nullptr;
   const size_t wbpart_bytes = wbpart ? h->wg_bpart_bytes() : 0;
+  // After zero_grad the gradients are written, not added to; the experts
+  // without rows are cleared instead.
+  const bool store = h->grad_zero;
+  if (store) {
+    IdleSlices z{};
+    const size_t lens[6] = {(size_t)C * H, (size_t)H, (size_t)C * H, (size_t)H, (size_t)H * C,
+                            (size_t)C};
+    for (int p = 0; p < 6; ++p) {
+      z.base[p] = g + h->g_off[2 + p];
+      z.len[p] = lens[p];
+    }
+    z.n = 6;
+    HIP_TRY(launch_zero_idle_experts(counts, E, z, st));
+  }
   HIP_TRY((launch_wgrad<ActT, 0>(hb, Hp, Hp, dgo, C, C, counts, E, g + h->g_off[6], nullptr, C,
                                  (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, A,
-                                 wpart, wpart_bytes, wbpart, wbpart_bytes, h->num_cus, st)));
+                                 wpart, wpart_bytes, wbpart, wbpart_bytes, h->num_cus, store,
+                                 st)));
   HIP_TRY(mark(4));
   HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
                                  g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
                                  g + h->g_off[5], (size_t)H, A, wpart, wpart_bytes, wbpart,
-                                 wbpart_bytes, h->num_cus, st)));
+                                 wbpart_bytes, h->num_cus, store, st)));
   HIP_TRY(mark(5));
   HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wrt, N, C, E, k, dx,
                                  dlog, st));
   HIP_TRY(mark(6));
   HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
                                     (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
-                                    st));
+                                    store, st));
+  h->grad_zero = false;
   if (h->padded()) HIP_TRY(launch_copy_cols<ActT>(dx, C, dx_out, Cx, N, Cx, Cx, st));
   HIP_TRY(mark(7));
   if (prof) ++h->prof_b_count;
@@ -1079,9 +1111,8 @@ int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
     return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
-  const bool fresh = h->grad == nullptr;
-  if (int rc = ensure_grad(h, st)) return rc;
-  if (!fresh) HIP_TRY(hipMemsetAsync(h->grad, 0, sizeof(float) * h->g_total, st));
+  if (int rc = ensure_grad(h)) return rc;
+  h->grad_zero = true;   // the next backward stores instead of adding
   return MGPT_OK;
 }
 
@@ -1090,7 +1121,7 @@ int mgpt_moe_get_gradients(mgpt_moe* h, float* const* grads, int num_params, int
   if (int rc = check_grad_args(h, grads, num_params)) return rc;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
-  if (int rc = ensure_grad(h, st)) return rc;
+  if (int rc = materialize_grad(h, st)) return rc;
   const hipMemcpyKind kind = grads_on_device ? hipMemcpyDeviceToDevice : hipMemcpyDeviceToHost;
   for (int i = 0; i < num_params; ++i) {
     const GradPiece g = grad_piece(h, i);
@@ -1106,7 +1137,7 @@ int mgpt_moe_accumulate_gradients(mgpt_moe* h, float* const* grads, int num_para
   if (int rc = check_grad_args(h, grads, num_params)) return rc;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
-  if (int rc = ensure_grad(h, st)) return rc;
+  if (int rc = materialize_grad(h, st)) return rc;
   if (grads_on_device) {
     AddJobs jobs{};
     size_t max_elems = 0;

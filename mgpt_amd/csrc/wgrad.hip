@@ -132,20 +132,21 @@ __device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, in
   return out->cnt > 0;
 }
 
-// Accumulates a wave's 128 (i) x 64 (j) block of D into the gradient
-// (+=, like add_grad).  Register v of tile (ti, tj) is D[i][j] with
-// i = 8*(v/4) + 4*lhalf + v%4 and j = lrow inside the tile.  All loads of
-// a 16-value group are issued before any add, so the read-modify-write
-// costs one memory round trip per group instead of one per value; rows
-// past i_store (only in the last row tile) take a guarded path.  MODE 1:
-// the j columns are gate/up interleaved (32 gate, then 32 up, per 32
-// units) and go to out0 / out1 at column h.
-template <int MODE>
-__device__ __forceinline__ void wg_accumulate(const f32x16 (&acc)[4][2], int i_base, int j_base,
+// Accumulates a wave's 128 (i) x 32*TJ (j) block of D into the gradient
+// (+=, like add_grad), or stores it when `store` (the gradient is known to
+// be zero, so the read is skipped).  Register v of tile (ti, tj) is
+// D[i][j] with i = 8*(v/4) + 4*lhalf + v%4 and j = lrow inside the tile.
+// All loads of a 16-value group are issued before any add, so the
+// read-modify-write costs one memory round trip per group instead of one
+// per value; rows past i_store (only in the last row tile) take a guarded
+// path.  MODE 1: the j columns are gate/up interleaved (32 gate, then 32
+// up, per 32 units) and go to out0 / out1 at column h.
+template <int MODE, int TJ>
+__device__ __forceinline__ void wg_accumulate(const f32x16 (&acc)[4][TJ], int i_base, int j_base,
                                               int lrow, int lhalf, int e, float* out0,
                                               float* out1, int ldo, size_t out_estride,
-                                              int i_store, int j_store) {
-  constexpr int TI = 4, TJ = 2;
+                                              int i_store, int j_store, bool store) {
+  constexpr int TI = 4;
   const bool rows_full = i_base + TI * 32 <= i_store;   // wave-uniform
 #pragma unroll
   for (int tj = 0; tj < TJ; ++tj) {
@@ -165,7 +166,13 @@ __device__ __forceinline__ void wg_accumulate(const f32x16 (&acc)[4][2], int i_b
     if (!jok) continue;
     ob += (size_t)e * out_estride + col;
     float* orow = ob + (size_t)(i_base + 4 * lhalf) * ldo;
-    if (rows_full) {
+    if (rows_full && store) {
+#pragma unroll
+      for (int ti = 0; ti < TI; ++ti)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          orow[(size_t)(ti * 32 + 8 * (v / 4) + (v % 4)) * ldo] = acc[ti][tj][v];
+    } else if (rows_full) {
 #pragma unroll
       for (int ti = 0; ti < TI; ++ti) {
         float old[16];
@@ -183,17 +190,19 @@ __device__ __forceinline__ void wg_accumulate(const f32x16 (&acc)[4][2], int i_b
           const int di = ti * 32 + 8 * (v / 4) + (v % 4);
           if (i_base + 4 * lhalf + di < i_store) {
             float* o = orow + (size_t)di * ldo;
-            *o = *o + acc[ti][tj][v];
+            *o = store ? acc[ti][tj][v] : *o + acc[ti][tj][v];
           }
         }
     }
   }
 }
 
-// Adds column sum `sum` of tile column j to the bias gradient.
+// Adds column sum `sum` of tile column j to the bias gradient (stores it
+// when `store`).
 template <int MODE>
 __device__ __forceinline__ void wg_bias_add(float sum, int j, int e, float* bias0, float* bias1,
-                                            size_t bias_estride, int j_store) {
+                                            size_t bias_estride, int j_store,
+                                            bool store = false) {
   float* bb;
   int col;
   bool ok;
@@ -208,7 +217,7 @@ __device__ __forceinline__ void wg_bias_add(float sum, int j, int e, float* bias
   }
   if (ok) {
     float* o = bb + (size_t)e * bias_estride + col;
-    *o = *o + sum;
+    *o = store ? sum : *o + sum;
   }
 }
 
@@ -217,7 +226,8 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(
     const T* __restrict__ P, int ldp, int p_valid, const T* __restrict__ Q, int ldq, int q_valid,
     const int32_t* __restrict__ counts, int E, int Iy, int Jx, int gy, int gx,
     float* __restrict__ out0, float* __restrict__ out1, int ldo, size_t out_estride, int i_store,
-    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride) {
+    int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride,
+    int store) {
   constexpr int BK = WgT<T>::BK, EPV = WgT<T>::EPV;
   constexpr int NB = (BK / EPV) * (256 / EPV) / 256;   // transposed blocks per thread
   constexpr int FB = 256 / EPV;                        // feature blocks per tile
@@ -385,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(
   }
 
   wg_accumulate<MODE>(acc, i0 + wi * 128, j0 + wj * 64, lrow, lhalf, e, out0, out1, ldo,
-                      out_estride, i_store, j_store);
+                      out_estride, i_store, j_store, store != 0);
 
   if (!do_bias) return;
   // Column sums: the partial of feature block fb from row block sb goes to
@@ -407,7 +417,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_kernel(
     float sum = 0.0f;
 #pragma unroll
     for (int sb = 0; sb < BK / EPV; ++sb) sum += s_b[sb * 256 + tid];
-    wg_bias_add<MODE>(sum, j, e, bias0, bias1, bias_estride, j_store);
+    wg_bias_add<MODE>(sum, j, e, bias0, bias1, bias_estride, j_store, store != 0);
   }
 }
 
@@ -467,7 +477,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
     const int32_t* __restrict__ counts, int E, int Iy, int Jx, int gy, int gx,
     float* __restrict__ out0, float* __restrict__ out1, int ldo, size_t out_estride, int i_store,
     int j_store, float* __restrict__ bias0, float* __restrict__ bias1, size_t bias_estride,
-    int chunk_rows, float* __restrict__ part, float* __restrict__ bpart) {
+    int chunk_rows, float* __restrict__ part, float* __restrict__ bpart, int store) {
   __shared__ __attribute__((aligned(1024))) char smem[kTrStages * kTrStageBytes];
   const int tid = threadIdx.x;
   WgTile tl;
@@ -594,7 +604,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
 
   if (tl.pslot < 0) {
     wg_accumulate<MODE>(acc, i0 + wi * 128, j0 + wj * 64, lrow, lhalf, e, out0, out1, ldo,
-                        out_estride, i_store, j_store);
+                        out_estride, i_store, j_store, store != 0);
   } else {
     // a later chunk: the whole 256 x 256 tile to its partial slot, [i][j]
     float* tp = part + ((size_t)tl.pslot * Iy * Jx + (size_t)tl.ty * Jx + tl.tx) * (kTI * kTJ);
@@ -621,7 +631,7 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
     float sum = 0.0f;
     for (int g = 0; g < 16; ++g) sum += s_b[g * 256 + tid];
     if (tl.pslot < 0)
-      wg_bias_add<MODE>(sum, j0 + tid, e, bias0, bias1, bias_estride, j_store);
+      wg_bias_add<MODE>(sum, j0 + tid, e, bias0, bias1, bias_estride, j_store, store != 0);
     else
       bpart[((size_t)tl.pslot * Jx + tl.tx) * kTJ + tid] = sum;
   }
@@ -629,7 +639,8 @@ __global__ __launch_bounds__(kThreads) void wgrad_tr_kernel(
 
 // Adds the partial slots of every expert that was cut into chunks to its
 // gradients, grad += (p_1 + p_2 + ...) in chunk order (chunk 0 accumulated
-// directly), so the result does not depend on which chunk finished first.
+// or stored directly, before), so the result does not depend on which
+// chunk finished first.
 // Blocks b < 64 * Iy * Jx take 4 rows x 256 columns of tile b / 64, one
 // float4 of 4 columns per thread; the Jx blocks after them take the bias
 // columns of tile column b - 64 * Iy * Jx.  The chunking is recomputed from
@@ -706,7 +717,33 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(
   }
 }
 
+// Zeroes the gradient slices of the experts that have no rows: expert e's
+// slice of piece p is base[p] + e * len[p] .. + len[p].  Blocks (x, e); the
+// experts with rows return at once.
+__global__ __launch_bounds__(256) void zero_idle_experts_kernel(const int32_t* __restrict__ counts,
+                                                                IdleSlices z) {
+  const int e = blockIdx.y;
+  if (counts[e] != 0) return;
+  const size_t step = (size_t)gridDim.x * blockDim.x;
+  for (int p = 0; p < z.n; ++p) {
+    float* b = z.base[p] + (size_t)e * z.len[p];
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < z.len[p]; i += step)
+      b[i] = 0.0f;
+  }
+}
+
 }  // namespace
+
+// The store-mode companion of launch_wgrad: clears the slices of every
+// expert with counts[e] == 0, which the weight-gradient launches leave as
+// they were.
+hipError_t launch_zero_idle_experts(const int32_t* counts, int E, const IdleSlices& z,
+                                    hipStream_t stream) {
+  if (E <= 0 || E > kMaxExperts || z.n < 0 || z.n > IdleSlices::kMax) return hipErrorInvalidValue;
+  if (z.n == 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_idle_experts_kernel, dim3(64, E), dim3(256), 0, stream, counts, z);
+  return hipGetLastError();
+}
 
 // D_e = P_e^T . Q_e accumulated into out (fp32) for every expert with rows:
 // P [rows][ldp] with p_valid valid columns (the i dimension), Q [rows][ldq]
@@ -714,14 +751,17 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(
 // segment.  MODE 0: out0[e][i][j] (i < i_store, j < j_store); MODE 1: the
 // j columns are gate/up interleaved and go to out0 (gate) / out1 (up) at
 // column h (h < j_store).  bias0/bias1 (nullable) receive the column sums
-// of Q the same way.  p_valid and q_valid must be multiples of 8 (bf16) or
-// 4 (fp32); ldp, ldq likewise, and P, Q 16-byte aligned.
+// of Q the same way.  With `store` the gradients are taken to be zero
+// and are written instead of read and added (experts without rows are not
+// touched: launch_zero_idle_experts clears them).  p_valid and q_valid must
+// be multiples of 8 (bf16) or 4 (fp32); ldp, ldq likewise, and P, Q 16-byte
+// aligned.
 template <typename T, int MODE>
 hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, int q_valid, const int32_t* counts, int E, float* out0, float* out1,
                         int ldo, size_t out_estride, int i_store, int j_store, float* bias0,
                         float* bias1, size_t bias_estride, int rows_total, float* part,
                         size_t part_bytes, float* bpart, size_t bpart_bytes, int num_cus,
-                        hipStream_t stream) {
+                        bool store, hipStream_t stream) {
   constexpr int EPV = WgT<T>::EPV;
   if (E <= 0 || E > kMaxExperts || p_valid % EPV || q_valid % EPV || ldp % EPV || ldq % EPV ||
       (reinterpret_cast<uintptr_t>(P) & 15) || (reinterpret_cast<uintptr_t>(Q) & 15) ||
@@ -758,7 +798,7 @@ hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, i
   if constexpr (sizeof(T) == 2) {
     hipLaunchKernelGGL((wgrad_tr_kernel<MODE>), dim3(blocks), dim3(kThreads), 0, stream, P, ldp,
                        Q, ldq, counts, E, Iy, Jx, gy, gx, out0, out1, ldo, out_estride, i_store,
-                       j_store, bias0, bias1, bias_estride, chunk_rows, part, bpart);
+                       j_store, bias0, bias1, bias_estride, chunk_rows, part, bpart, (int)store);
     if (slots > 0)
       hipLaunchKernelGGL((wgrad_reduce_kernel<MODE>), dim3((unsigned)(64 * tiles + Jx)), dim3(256),
                          0, stream, part, bpart, counts, E, chunk_rows, Iy, Jx, out0, out1, ldo,
@@ -766,7 +806,7 @@ hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, i
   } else {
     hipLaunchKernelGGL((wgrad_kernel<T, MODE>), dim3(blocks), dim3(kThreads), 0, stream, P, ldp,
                        p_valid, Q, ldq, q_valid, counts, E, Iy, Jx, gy, gx, out0, out1, ldo,
-                       out_estride, i_store, j_store, bias0, bias1, bias_estride);
+                       out_estride, i_store, j_store, bias0, bias1, bias_estride, (int)store);
   }
   return hipGetLastError();
 }
@@ -775,7 +815,7 @@ hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, i
   template hipError_t launch_wgrad<T, MODE>(const T*, int, int, const T*, int, int,           \
                                             const int32_t*, int, float*, float*, int, size_t, \
                                             int, int, float*, float*, size_t, int, float*,     \
-                                            size_t, float*, size_t, int, hipStream_t);
+                                            size_t, float*, size_t, int, bool, hipStream_t);
 MGPT_INST_WGRAD(bf16_t, 0)
 MGPT_INST_WGRAD(bf16_t, 1)
 MGPT_INST_WGRAD(float, 0)

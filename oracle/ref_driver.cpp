@@ -10,7 +10,7 @@
 //   ref_driver backward <in.bin> <dy.bin> <grad.bin>
 //   ref_driver block <in.bin> <gamma.bin> <out.bin>
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
-//   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (forward + backward)
+//   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (zero_grad + forward + backward)
 //   ref_driver bench_block <N> <C> <H> <E> <k> <reps>   (ln2 + MoE + residual)
 //   ref_driver gptbin <out.bin> <side.bin> V S C L heads E k H steps seed
 //   ref_driver gptlogits <model.bin> <heads> <E> <k> <H> <ids.bin> <out.bin>
@@ -289,6 +289,8 @@ int bench(int N, int C, int H, int E, int k, int reps, BenchPass pass) {
       Tensor::add_into(x, y, out);
       return;
     }
+    if (train)   // the Trainer's per-step order (pipeline/Trainer.cpp:303-305)
+      for (Tensor* p : layer.get_parameters()) p->zero_grad();
     layer.forward_into(x, y);
     if (train) layer.backward_into(dy, dx);
   };
@@ -305,7 +307,7 @@ int bench(int N, int C, int H, int E, int k, int reps, BenchPass pass) {
   double med = s[s.size() / 2];
   std::printf("{\"pass\": \"%s\", \"N\": %d, \"C\": %d, \"H\": %d, \"E\": %d, \"k\": %d, "
               "\"reps\": %d, \"median_s\": %.6f, \"runs_s\": [",
-              train ? "forward+backward" : pass == kBenchBlock ? "block" : "forward", N, C, H,
+              train ? "zero_grad+forward+backward" : pass == kBenchBlock ? "block" : "forward", N, C, H,
               E, k, reps, med);
   for (size_t i = 0; i < t.size(); ++i) std::printf("%s%.6f", i ? ", " : "", t[i]);
   std::printf("], \"tokens_per_s\": %.3f, \"threads\": 1}\n", N / med);

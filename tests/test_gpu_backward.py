@@ -142,6 +142,60 @@ def test_backward_accumulates_and_is_deterministic(act):
 
 
 @pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_backward_after_zero_grad_overwrites_stale_gradients(act):
+    """zero_grad only marks the gradients zero; the next backward writes
+    them.  After a backward that gave every expert a gradient, zero_grad and
+    a backward routed to experts 0 and 1 only must equal a fresh layer's
+    gradients bit for bit (the other experts exactly zero), and
+    get_gradients right after zero_grad must read zeros."""
+    from mgpt_amd import workload as wl
+    cfg = wl.MoEConfig("stale", 256, 64, 6, 2, 96, act, act, "zero")   # every expert chosen
+    inp = wl.make_inputs(cfg, seed=4, bias_std=0.05)
+    if act == "bf16":
+        inp.x[:] = wl.bf16_round(inp.x)
+    dy = wl.bf16_round(np.random.default_rng(2).standard_normal((cfg.N, cfg.C)).astype(np.float32))
+    layer = make_layer(inp)
+    first = run_backward(layer, inp, dy)
+    for n in ("dWg", "dWd", "dbd"):
+        assert np.all(np.any(first[n].reshape(cfg.E, -1) != 0, axis=1)), n
+    inp.br[:] = np.array([9, 8, -9, -9, -9, -9], np.float32)   # experts 0, 1 always win
+    layer.load_parameters(inp.params(raw=True))
+    again = run_backward(layer, inp, dy)
+    fresh = run_backward(make_layer(inp), inp, dy)
+    assert np.array_equal(again["dx"], fresh["dx"])
+    for n in NAMES:
+        assert np.array_equal(again[n], fresh[n]), n
+    for n in ("dWg", "dbg", "dWu", "dbu", "dWd", "dbd"):
+        assert np.all(again[n][2:] == 0) and np.any(again[n][:2] != 0), n
+    layer.zero_grad()
+    assert all(not torch.any(t != 0) for t in layer.get_gradients())
+
+
+def test_accumulation_with_row_chunks():
+    """bf16 large-M shape whose weight-gradient contraction is cut into row
+    chunks (experts of 3943, 2410, 1837 and 2 rows against 1024-row
+    chunks): a second backward without zero_grad adds the same contribution
+    again (to within one rounding of the sum per element), and zero_grad +
+    backward repeats the first result bit for bit."""
+    from mgpt_amd import workload as wl
+    cfg = wl.MoEConfig("chunks", 4096, 256, 4, 2, 256, "bf16", "bf16", "normal")
+    inp = wl.make_inputs(cfg, seed=21, bias_std=0.05)
+    inp.x[:] = wl.bf16_round(inp.x)
+    dy = wl.bf16_round(np.random.default_rng(8).standard_normal((cfg.N, cfg.C)).astype(np.float32))
+    layer = make_layer(inp)
+    a = run_backward(layer, inp, dy)
+    b = run_backward(layer, inp, dy, zero=False)
+    c = run_backward(layer, inp, dy)
+    ref = O.backward(inp, dy)
+    check_all(a, ref, TOL["bf16"], "chunks")
+    for n in NAMES:
+        assert np.array_equal(c[n], a[n]), n
+        two = 2.0 * a[n].astype(np.float64)
+        err = np.max(np.abs(b[n] - two)) / max(np.max(np.abs(two)), 1e-30)
+        assert err <= 1e-6, (n, err)
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
 def test_unchosen_experts_get_no_gradient(act):
     from mgpt_amd import workload as wl
     cfg = wl.MoEConfig("unchosen", 128, 64, 6, 2, 96, act, act, "zero")
