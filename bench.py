@@ -437,11 +437,11 @@ def main() -> int:
     counts = layer.get_expert_counts()
 
     # The timed steps record HIP events on the launch stream around the
-    # dominant kernel only (the gate/up GEMM; the training pass records every
-    # stage, its dominant kernel being a backward one): events at every stage
-    # boundary add a gap between launches (about 2.5% at cfg3).  The other
-    # stage times come from a separate, fully profiled pass of as many steps.
-    layer.set_profiling(True, gemm_only=not train)
+    # gate/up GEMM only: an event at every stage boundary adds a gap of a few
+    # microseconds between launches (about 2.5% of the cfg3 forward, 3.5% of
+    # its training step).  The other stage times, the backward's included,
+    # come from a separate, fully profiled pass of as many steps.
+    layer.set_profiling(True, gemm_only=True)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
@@ -454,18 +454,17 @@ def main() -> int:
     ms_per_step = start.elapsed_time(stop) / args.steps
     stages = layer.stage_times()
     n_prof = stages.pop("forwards")
+    gemm_gateup_timed = stages["gemm_gateup"]
+    layer.set_profiling(True)
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    stages = layer.stage_times()
+    stages.pop("forwards")
+    stages["gemm_gateup"] = gemm_gateup_timed
     bstages = layer.backward_stage_times() if train else None
     if bstages:
         bstages.pop("backwards")
-    if not train:
-        gemm_gateup_timed = stages["gemm_gateup"]
-        layer.set_profiling(True)
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        stages = layer.stage_times()
-        stages.pop("forwards")
-        stages["gemm_gateup"] = gemm_gateup_timed
     layer.set_profiling(False)
 
     N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k

@@ -232,7 +232,7 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
  * enable: 0 off, 1 every stage boundary, 2 only the two boundaries of the
  * gate/up GEMM (the other launches keep their spacing; stage_times then
  * returns -1 for the other stages).  The backward records its stages
- * whenever enable is nonzero. */
+ * with enable = 1 only. */
 #define MGPT_MOE_NUM_STAGES 5
 int mgpt_moe_set_profiling(mgpt_moe* h, int enable);
 int mgpt_moe_stage_times(mgpt_moe* h, float* ms, int n);

@@ -214,9 +214,50 @@ __global__ __launch_bounds__(64) void token_dx_kernel(const ActT* __restrict__ d
 
 constexpr int kRwChunk = 64;    // tokens per router_wgrad partial
 
-// partial[chunk][c][e] = sum over the chunk's tokens of x[t][c] * dL[t][e]
-// (a thread per column, EP >= E experts in registers, dL rows read from LDS
-// as float4 broadcasts), and in the blocks of the first column range
+// CPT consecutive columns of row p of x as floats (one vector load).
+template <int CPT>
+__device__ __forceinline__ void rw_load_cols(const bf16_t* p, float (&v)[CPT]) {
+  if constexpr (CPT == 4) {
+    const uint2 w = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(w.x << 16);
+    v[1] = __uint_as_float(w.x & 0xFFFF0000u);
+    v[2] = __uint_as_float(w.y << 16);
+    v[3] = __uint_as_float(w.y & 0xFFFF0000u);
+  } else if constexpr (CPT == 2) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
+    v[0] = __uint_as_float(w << 16);
+    v[1] = __uint_as_float(w & 0xFFFF0000u);
+  } else {
+    v[0] = bf16_to_f32(*p);
+  }
+}
+template <int CPT>
+__device__ __forceinline__ void rw_load_cols(const float* p, float (&v)[CPT]) {
+  if constexpr (CPT == 4) {
+    const float4 w = *reinterpret_cast<const float4*>(p);
+    v[0] = w.x;
+    v[1] = w.y;
+    v[2] = w.z;
+    v[3] = w.w;
+  } else if constexpr (CPT == 2) {
+    const float2 w = *reinterpret_cast<const float2*>(p);
+    v[0] = w.x;
+    v[1] = w.y;
+  } else {
+    v[0] = *p;
+  }
+}
+
+// partial[chunk][e][c] = sum over the chunk's tokens of x[t][c] * dL[t][e]
+// (tokens in order, fused multiply-adds).  A thread holds CPT = 64 / EP
+// consecutive columns x EP >= E experts (64 accumulators), reads each
+// token's CPT values of x as one vector load and the token's dL row from
+// LDS as float4 broadcasts: CPT * EP FMAs per 1 + EP / 4 loads.  The x
+// loads run a group of 8 tokens ahead of the FMAs (two register groups;
+// every load is issued, past the chunk's end at a clamped row whose
+// values are then zeroed, so the wait counts stay exact), and each
+// expert's CPT sums go out as one vector store, lanes on consecutive
+// columns.  The blocks of the first column range also write
 // partial_b[chunk][e] = sum_t dL[t][e].
 template <typename ActT, int EP>
 __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restrict__ x,
@@ -224,65 +265,90 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
                                                            int C, int E,
                                                            float* __restrict__ partial,
                                                            float* __restrict__ partial_b) {
-  __shared__ float4 s_dl[64][EP / 4];
+  constexpr int CPT = 64 / EP;
+  constexpr int kG = 8;   // tokens per load group
+  static_assert(kRwChunk % (2 * kG) == 0, "whole group pairs per chunk");
+  __shared__ float4 s_dl[kRwChunk][EP / 4];
   const int tid = threadIdx.x;
   const int chunk = blockIdx.y;
-  const int c = blockIdx.x * 256 + tid;
-  const int t_begin = chunk * kRwChunk, t_end = min(N, t_begin + kRwChunk);
-  float acc[EP];
+  const int c0 = (blockIdx.x * 256 + tid) * CPT;
+  const int t0 = chunk * kRwChunk, nt = min(kRwChunk, N - t0);
+  float* sl = reinterpret_cast<float*>(s_dl);
+  for (int p = tid; p < kRwChunk * EP; p += 256) {
+    const int r = p / EP, e = p % EP;
+    sl[p] = (r < nt && e < E) ? dL[(size_t)(t0 + r) * E + e] : 0.0f;
+  }
+  __syncthreads();
+  if (blockIdx.x == 0 && tid < E) {
+    float bsum = 0.0f;
+    for (int r = 0; r < nt; ++r) bsum += sl[r * EP + tid];
+    partial_b[(size_t)chunk * E + tid] = bsum;
+  }
+  if (c0 >= C) return;   // C is a multiple of CPT
+  float acc[CPT][EP];
 #pragma unroll
-  for (int e = 0; e < EP; ++e) acc[e] = 0.0f;
-  float bsum = 0.0f;
-  for (int tb = t_begin; tb < t_end; tb += 64) {
-    const int nt = min(64, t_end - tb);
-    __syncthreads();
-    float* sl = reinterpret_cast<float*>(s_dl);
-    for (int p = tid; p < 64 * EP; p += 256) {
-      const int r = p / EP, e = p % EP;
-      sl[p] = (r < nt && e < E) ? dL[(size_t)(tb + r) * E + e] : 0.0f;
-    }
-    __syncthreads();
-    if (blockIdx.x == 0 && tid < E)
-      for (int r = 0; r < nt; ++r) bsum += sl[r * EP + tid];
-    if (c < C) {
-      // 16 tokens' loads in flight at a time (rows past nt are zero in s_dl)
-      for (int r0 = 0; r0 < nt; r0 += 16) {
-        float xv[16];
+  for (int cc = 0; cc < CPT; ++cc)
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
-          xv[u] = r0 + u < nt ? to_f32(x[(size_t)(tb + r0 + u) * C + c]) : 0.0f;
+    for (int e = 0; e < EP; ++e) acc[cc][e] = 0.0f;
+  const ActT* xp = x + (size_t)t0 * C + c0;
+  auto load = [&](int r0, float (&xv)[kG][CPT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+    for (int u = 0; u < kG; ++u) rw_load_cols<CPT>(xp + (size_t)min(r0 + u, nt - 1) * C, xv[u]);
+  };
+  auto fmas = [&](int r0, float (&xv)[kG][CPT]) __attribute__((always_inline)) {
 #pragma unroll
-          for (int e4 = 0; e4 < EP / 4; ++e4) {
-            const float4 d = s_dl[r0 + u][e4];
-            acc[4 * e4 + 0] += xv[u] * d.x;
-            acc[4 * e4 + 1] += xv[u] * d.y;
-            acc[4 * e4 + 2] += xv[u] * d.z;
-            acc[4 * e4 + 3] += xv[u] * d.w;
-          }
+    for (int u = 0; u < kG; ++u) {
+      if (r0 + u >= nt) {   // a clamped row (its dL row is zero as well)
+#pragma unroll
+        for (int cc = 0; cc < CPT; ++cc) xv[u][cc] = 0.0f;
+      }
+#pragma unroll
+      for (int e4 = 0; e4 < EP / 4; ++e4) {
+        const float4 d = s_dl[r0 + u][e4];
+#pragma unroll
+        for (int cc = 0; cc < CPT; ++cc) {
+          acc[cc][4 * e4 + 0] = __builtin_fmaf(xv[u][cc], d.x, acc[cc][4 * e4 + 0]);
+          acc[cc][4 * e4 + 1] = __builtin_fmaf(xv[u][cc], d.y, acc[cc][4 * e4 + 1]);
+          acc[cc][4 * e4 + 2] = __builtin_fmaf(xv[u][cc], d.z, acc[cc][4 * e4 + 2]);
+          acc[cc][4 * e4 + 3] = __builtin_fmaf(xv[u][cc], d.w, acc[cc][4 * e4 + 3]);
         }
       }
     }
+  };
+  float xa[kG][CPT], xb[kG][CPT];
+  load(0, xa);
+  for (int r0 = 0; r0 < nt; r0 += 2 * kG) {
+    load(r0 + kG, xb);
+    fmas(r0, xa);
+    if (r0 + 2 * kG < nt) load(r0 + 2 * kG, xa);
+    fmas(r0 + kG, xb);
   }
-  if (c < C) {
-    float* o = partial + ((size_t)chunk * C + c) * E;
+  float* o = partial + (size_t)chunk * C * E + c0;
 #pragma unroll
-    for (int e = 0; e < EP; ++e)
-      if (e < E) o[e] = acc[e];
+  for (int e = 0; e < EP; ++e) {
+    if (e >= E) break;
+    if constexpr (CPT == 4) {
+      *reinterpret_cast<float4*>(o + (size_t)e * C) =
+          make_float4(acc[0][e], acc[1][e], acc[2][e], acc[3][e]);
+    } else if constexpr (CPT == 2) {
+      *reinterpret_cast<float2*>(o + (size_t)e * C) = make_float2(acc[0][e], acc[1][e]);
+    } else {
+      o[(size_t)e * C] = acc[0][e];
+    }
   }
-  if (blockIdx.x == 0 && tid < E) partial_b[(size_t)chunk * E + tid] = bsum;
 }
 
-// grad[i] += sum over chunks of partial[chunk][i], for the C*E weight
-// entries followed by the E bias entries, as a fixed two-level tree (so the
-// result does not depend on scheduling): a block takes 16 entries; thread
-// (entry, g) adds the g-th of 16 consecutive chunk ranges in order, then
-// one thread per entry adds the 16 range sums in order.  With `store` the
-// gradient is taken to be zero and the sum is written without reading it.
+// grad += sum over chunks of partial[chunk][i], for the C*E weight
+// entries (i = e * C + c, gradient entry gW[c][e]) followed by the E bias
+// entries, as a fixed two-level tree (so the result does not depend on
+// scheduling): a block takes 16 entries; thread (entry, g) adds the g-th of
+// 16 consecutive chunk ranges in order, then one thread per entry adds the
+// 16 range sums in order.  With `store` the gradient is taken to be zero
+// and the sum is written without reading it.
 __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(
-    const float* __restrict__ partial, const float* __restrict__ partial_b, int chunks, int CE,
+    const float* __restrict__ partial, const float* __restrict__ partial_b, int chunks, int C,
     int E, float* __restrict__ gW, float* __restrict__ gb, int store) {
+  const int CE = C * E;
   __shared__ float s_part[16][16];
   const int el = threadIdx.x % 16, g = threadIdx.x / 16;
   const int i = blockIdx.x * 16 + el;
@@ -308,7 +374,7 @@ __global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(
     float t = 0.0f;
 #pragma unroll
     for (int q = 0; q < 16; ++q) t += s_part[q][el];
-    float* o = w ? gW + i : gb + (i - CE);
+    float* o = w ? gW + (size_t)(i % C) * E + i / C : gb + (i - CE);
     *o = store ? t : *o + t;
   }
 }
@@ -378,21 +444,22 @@ template <typename ActT>
 hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int E,
                                float* partial, float* partial_b, float* gW, float* gb,
                                bool store, hipStream_t stream) {
+  if (E <= 0 || E > kMaxExperts || C % 4) return hipErrorInvalidValue;
   if (N <= 0) return hipSuccess;
   const int chunks = router_wgrad_chunks(N);
-  const dim3 grid((C + 255) / 256, chunks);
+  // a block covers 256 threads x 64 / EP columns
   if (E <= 16)
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16>), grid, dim3(256), 0, stream, x, dL, N, C,
-                       E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16>), dim3((C + 1023) / 1024, chunks), dim3(256),
+                       0, stream, x, dL, N, C, E, partial, partial_b);
   else if (E <= 32)
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32>), grid, dim3(256), 0, stream, x, dL, N, C,
-                       E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32>), dim3((C + 511) / 512, chunks), dim3(256),
+                       0, stream, x, dL, N, C, E, partial, partial_b);
   else
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64>), grid, dim3(256), 0, stream, x, dL, N, C,
-                       E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64>), dim3((C + 255) / 256, chunks), dim3(256),
+                       0, stream, x, dL, N, C, E, partial, partial_b);
   const int CE = C * E;
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 15) / 16), dim3(256), 0, stream,
-                     partial, partial_b, chunks, CE, E, gW, gb, (int)store);
+                     partial, partial_b, chunks, C, E, gW, gb, (int)store);
   return hipGetLastError();
 }
 

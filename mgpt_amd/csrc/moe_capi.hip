@@ -835,7 +835,7 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   float* g = h->grad;
   const ActT* wdb = (const ActT*)h->wdb;
   const ActT* wgub = (const ActT*)h->wgub;
-  const bool prof = h->profiling;
+  const bool prof = h->profiling && !h->prof_gemm_only;
   hipEvent_t* evs = h->evb[h->prof_b_count % mgpt_moe::kProfSlots];
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 

@@ -211,6 +211,33 @@ def test_unchosen_experts_get_no_gradient(act):
     check_all(out, ref, TOL[act], f"unchosen-{act}")
 
 
+def test_backward_profiling_modes():
+    """Profiling mode 1 times every backward stage; mode 2 (events only
+    around the forward's gate/up GEMM) records no backward events, so the
+    backward stage times report no profiled backward; profiled backwards
+    give the same bits as unprofiled ones."""
+    from mgpt_amd import capi
+    from mgpt_amd import workload as wl
+    cfg = wl.MoEConfig("prof", 512, 128, 4, 2, 256, "bf16", "bf16", "zero")
+    inp = wl.make_inputs(cfg, seed=6, bias_std=0.05)
+    inp.x[:] = wl.bf16_round(inp.x)
+    dy = wl.bf16_round(np.random.default_rng(4).standard_normal((cfg.N, cfg.C)).astype(np.float32))
+    layer = make_layer(inp)
+    ref = run_backward(layer, inp, dy)
+    layer.set_profiling(True)
+    out = run_backward(layer, inp, dy)
+    st = layer.backward_stage_times()
+    assert st["backwards"] == 1 and all(v > 0.0 for k, v in st.items() if k != "backwards"), st
+    layer.set_profiling(True, gemm_only=True)
+    out2 = run_backward(layer, inp, dy)
+    with pytest.raises(capi.MoEError) as ei:
+        layer.backward_stage_times()
+    assert ei.value.status == capi.MGPT_ERR_NOT_READY
+    layer.set_profiling(False)
+    for n in ("dx",) + NAMES:
+        assert np.array_equal(out[n], ref[n]) and np.array_equal(out2[n], ref[n]), n
+
+
 def test_fp8_handle_has_no_backward():
     from mgpt_amd import capi
     from mgpt_amd import workload as wl
