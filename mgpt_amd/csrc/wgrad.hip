@@ -686,23 +686,29 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(
             part + ((size_t)(x0 + c) * tiles + tile) * (kTI * kTJ) + li * kTJ + lj);
         a.x += v.x; a.y += v.y; a.z += v.z; a.w += v.w;
       }
-      const float av[4] = {a.x, a.y, a.z, a.w};
+      // the 4 columns stay in one 32-column gate or up group, so they are
+      // consecutive gradient entries: one float4 read-modify-write where the
+      // row layout keeps them 16-byte aligned
+      const int j = tx * kTJ + lj;
+      float* ob;
+      int col;
+      if constexpr (MODE == 0) {
+        ob = out0;
+        col = j;
+      } else {
+        ob = ((j >> 5) & 1) ? out1 : out0;
+        col = (j >> 6) * 32 + (j & 31);
+      }
+      float* o = ob + (size_t)e * out_estride + (size_t)gi * ldo + col;
+      if (col + 3 < j_store && (reinterpret_cast<uintptr_t>(o) & 15) == 0) {
+        float4 v = *reinterpret_cast<float4*>(o);
+        v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+        *reinterpret_cast<float4*>(o) = v;
+      } else {
+        const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int j = tx * kTJ + lj + t;
-        float* ob;
-        int col;
-        if constexpr (MODE == 0) {
-          ob = out0;
-          col = j;
-        } else {
-          ob = ((j >> 5) & 1) ? out1 : out0;
-          col = (j >> 6) * 32 + (j & 31);
-        }
-        if (col < j_store) {
-          float* o = ob + (size_t)e * out_estride + (size_t)gi * ldo + col;
-          *o = *o + av[t];
-        }
+        for (int t = 0; t < 4; ++t)
+          if (col + t < j_store) o[t] = o[t] + av[t];
       }
     }
   } else {
@@ -725,10 +731,18 @@ __global__ __launch_bounds__(256) void zero_idle_experts_kernel(const int32_t* _
   const int e = blockIdx.y;
   if (counts[e] != 0) return;
   const size_t step = (size_t)gridDim.x * blockDim.x;
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (int p = 0; p < z.n; ++p) {
     float* b = z.base[p] + (size_t)e * z.len[p];
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < z.len[p]; i += step)
-      b[i] = 0.0f;
+    const size_t n = z.len[p];
+    // scalar head up to 16-byte alignment, float4 body, scalar tail
+    const size_t head = std::min(n, (size_t)((16 - (reinterpret_cast<uintptr_t>(b) & 15)) & 15) / 4);
+    if (t0 < head) b[t0] = 0.0f;
+    float4* b4 = reinterpret_cast<float4*>(b + head);
+    const size_t n4 = (n - head) / 4;
+    for (size_t i = t0; i < n4; i += step) b4[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    const size_t tail = head + 4 * n4;
+    if (tail + t0 < n) b[tail + t0] = 0.0f;
   }
 }
 
@@ -741,7 +755,7 @@ hipError_t launch_zero_idle_experts(const int32_t* counts, int E, const IdleSlic
                                     hipStream_t stream) {
   if (E <= 0 || E > kMaxExperts || z.n < 0 || z.n > IdleSlices::kMax) return hipErrorInvalidValue;
   if (z.n == 0) return hipSuccess;
-  hipLaunchKernelGGL(zero_idle_experts_kernel, dim3(64, E), dim3(256), 0, stream, counts, z);
+  hipLaunchKernelGGL(zero_idle_experts_kernel, dim3(256, E), dim3(256), 0, stream, counts, z);
   return hipGetLastError();
 }
 
