@@ -252,15 +252,15 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
     what = {"train": "training step (zero_grad + forward + backward)",
             "block": "fused block (RMSNorm + MoE + residual)",
             "decode": "decode steps in the sampling loop"}.get(mode, "forward")
-    runs = {"train": f"{b['warmup'] + b['steps']} training steps ({b['warmup']} warmup + "
-                     f"{b['steps']} timed)",
-            "block": f"{b['warmup'] + b['steps']} fused block forwards and as many unfused "
-                     f"({b['warmup']} warmup + {b['steps']} timed each)",
-            "decode": f"{b['warmup'] + 1} growing loops of {b.get('growing_phase_steps')} steps "
-                      f"(N = 1 .. {b['config']['N']}), then {b['steps']} eager, {b['steps']} "
-                      f"profiled, 1 + {b['warmup'] + b['steps']} graph-replayed steady-state "
+    w, k = b["warmup"], b["steps"]
+    runs = {"train": f"{w + 2 * k} training steps ({w} warmup, {k} timed, {k} profiled)",
+            "block": f"{w + 2 * k} fused block forwards ({w} warmup, {k} timed, {k} profiled) "
+                     f"and {w + k} unfused ({w} warmup, {k} timed)",
+            "decode": f"{w + 1} growing loops of {b.get('growing_phase_steps')} steps "
+                      f"(N = 1 .. {b['config']['N']}), then {k} eager, {k} "
+                      f"profiled, 1 + {w + k} graph-replayed steady-state "
                       "steps (kernel averages mix every N)"}.get(
-        mode, f"{b['warmup'] + b['steps']} forwards ({b['warmup']} warmup + {b['steps']} timed)")
+        mode, f"{w + 2 * k} forwards ({w} warmup, {k} timed, {k} profiled)")
     out = [f"# {b['config']['workload'].split(':')[0]} MoE {what}: rocprofv3 kernel statistics "
            "(MI355X)", "",
            "Command (repository root, on the GPU box), then "

@@ -196,7 +196,10 @@ int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int 
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Sets every gradient to zero on `stream`.  Replaces Tensor::zero_grad
- * (utils/Tensor.cpp:181-187) over this layer's parameters. */
+ * (utils/Tensor.cpp:181-187) over this layer's parameters.  No memory is
+ * written: the gradients are marked zero, the next mgpt_moe_backward stores
+ * them instead of adding, and a read before that (get / accumulate) clears
+ * the buffer first. */
 int mgpt_moe_zero_grad(mgpt_moe* h, void* stream);
 
 /* Copies the 2 + 6E fp32 gradients to grads[i] in get_parameters() order
