@@ -435,12 +435,15 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
     e = hipDeviceGetAttribute(&h->num_cus, hipDeviceAttributeMultiprocessorCount, h->device);
   if (e == hipSuccess && h->num_cus <= 0) e = hipErrorInvalidDevice;
   if (e == hipSuccess) {
+    // Stage events only time: without the system-scope fence their record
+    // does not write back and invalidate the caches, which otherwise leaves
+    // a gap of several microseconds before the next launch.
     for (auto& slot : h->ev)
       for (auto& ev : slot)
-        if (e == hipSuccess) e = hipEventCreate(&ev);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableSystemFence);
     for (auto& slot : h->evb)
       for (auto& ev : slot)
-        if (e == hipSuccess) e = hipEventCreate(&ev);
+        if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableSystemFence);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&h->done, hipEventDisableTiming);
   }
   if (e != hipSuccess) {
