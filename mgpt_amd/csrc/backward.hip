@@ -124,7 +124,7 @@ constexpr int kDxTokens = 8;   // tokens per token_dx wave
 // dx of kDxTokens tokens x 512 columns per wave (8 columns per lane):
 // the sum of the tokens' slot rows of dX_e in ascending slot order (the
 // gather backward) plus dL . W_r^T (wrt = W_r as [E][C]; experts in
-// ascending order, 4 experts' weights loaded at a time).
+// ascending order, 4 experts' weights loaded at a time, fused multiply-adds).
 template <typename ActT>
 __global__ __launch_bounds__(64) void token_dx_kernel(const ActT* __restrict__ dxe,
                                                       const int32_t* __restrict__ slot_of,
@@ -182,7 +182,7 @@ __global__ __launch_bounds__(64) void token_dx_kernel(const ActT* __restrict__ d
       for (int u = 0; u < 4; ++u) {
         const float g = s_dl[r][e0 + u];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) acc[r][q] += g * w[u][q];
+        for (int q = 0; q < 8; ++q) acc[r][q] = __builtin_fmaf(g, w[u][q], acc[r][q]);
       }
   }
 #pragma unroll
