@@ -1113,9 +1113,9 @@ int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
   if (!trainable(h))
     return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   HIP_TRY(hipSetDevice(h->device));
-  hipStream_t st = (hipStream_t)stream;
+  (void)stream;   // nothing is enqueued: the next backward stores instead of adding
   if (int rc = ensure_grad(h)) return rc;
-  h->grad_zero = true;   // the next backward stores instead of adding
+  h->grad_zero = true;
   return MGPT_OK;
 }
 

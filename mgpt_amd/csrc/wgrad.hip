@@ -44,7 +44,7 @@ constexpr int kRowBytes = 128;        // LDS row: one feature's slab of rows
 constexpr int kOpBytes = 256 * kRowBytes;   // one operand tile (32 KB)
 
 template <typename T> struct WgT;
-template <> struct WgT<bf16_t> { static constexpr int BK = 64, EPV = 8; };
+template <> struct WgT<bf16_t> { static constexpr int EPV = 8; };   // (wgrad_tr_kernel)
 template <> struct WgT<float> { static constexpr int BK = 32, EPV = 4; };
 
 // 16-byte chunk c of LDS row r sits at slot c ^ swz(r).  (r >> 1) spreads
