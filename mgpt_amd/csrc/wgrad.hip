@@ -80,11 +80,13 @@ __device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, in
     const int ch_incl = wave_incl_scan(nch);
     const int xtra = nch > 0 ? nch - 1 : 0;                     // partial slots of expert l
     const int x_incl = wave_incl_scan(xtra);
-    const int V = __shfl(ch_incl, kWave - 1, kWave);
+    // (reads of one lane's value at a wave-uniform lane index are v_readlane,
+    // not an LDS permute round trip per step)
+    const int V = __builtin_amdgcn_readlane(ch_incl, kWave - 1);
     // virtual expert l: chunk c of expert ve (ve = experts whose chunks all
     // precede l); lanes l >= V describe nothing
     int ve = 0;
-    for (int e2 = 0; e2 < E; ++e2) ve += __shfl(ch_incl, e2, kWave) <= l;
+    for (int e2 = 0; e2 < E; ++e2) ve += __builtin_amdgcn_readlane(ch_incl, e2) <= l;
     const int src = ve < E ? ve : 0;
     const int c = l - (__shfl(ch_incl, src, kWave) - __shfl(nch, src, kWave));
     const int cnt_e = __shfl(cnt, src, kWave);
@@ -98,7 +100,7 @@ __device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, in
     // rank of virtual expert l in (rows descending, index ascending)
     int rank = 0;
     for (int v2 = 0; v2 < V; ++v2) {
-      const int c2 = __shfl(vcnt, v2, kWave);
+      const int c2 = __builtin_amdgcn_readlane(vcnt, v2);
       rank += (c2 > vcnt) || (c2 == vcnt && v2 < l);
     }
     const int ngx = (Jx + gx - 1) / gx;
