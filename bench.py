@@ -76,7 +76,7 @@ def stage_of(kernel_name: str):
     m = re.search(r"wgrad(?:_tr)?_kernel<(?:[^,>]*, )?(\d)>", short)
     if m:
         return ("wgrad_down", "wgrad_gateup")[int(m.group(1))]
-    if re.search(r"router_(?:topk|logits|softmax)", short):
+    if re.search(r"router_(?:topk|logits|softmax|decode)", short):
         return "router_topk"
     if "permute_kernel" in short:
         return "permute"

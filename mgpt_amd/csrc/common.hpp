@@ -26,6 +26,10 @@ constexpr int kMaxTopK = 8;
 constexpr int kRouterTokens = 64;
 __host__ __device__ inline int router_tokens_per_block(int /*E*/) { return kRouterTokens; }
 
+// Widest row the one-launch decode router takes (x[t] is widened into LDS as
+// fp32, 32 KB at this width).
+constexpr int kDecodeRouterMaxC = 8192;
+
 // Router experts per wave (the router block has ceil(E / RE) <= 16 waves);
 // router weights are packed [ceil(E/RE)][C][RE], zero-padded.  Two experts
 // per wave share the activation loads and conversions of their chains:

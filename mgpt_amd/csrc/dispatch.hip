@@ -151,6 +151,18 @@ __global__ __launch_bounds__(256) void permute_kernel(
       s_pre[tid] = base[(size_t)tid * nb + b];
       s_tot[tid] = counts[tid];
     }
+  } else if (!hist) {
+    // a single router block routed without a histogram (nb == 1): count its
+    // ids (LDS integer atomics; counts do not depend on their order)
+    if (tid < E) {
+      s_pre[tid] = 0;
+      s_tot[tid] = 0;
+    }
+    __syncthreads();
+    for (int f = tid; f < nflat; f += 256) {
+      const int e = topk_idx[flat0 + f];
+      if (e >= 0 && e < E) atomicAdd(&s_tot[e], 1);
+    }
   } else {
     // Per expert: the assignments of the router blocks before this one and
     // of all blocks.  G consecutive lanes of one wave share an expert (G =
@@ -304,6 +316,7 @@ hipError_t launch_permute(const InT* x, const int32_t* topk_idx, const int32_t* 
   const int nb = (N + TB - 1) / TB;
   if (nb == 0) return hipSuccess;
   const bool fold = E * nb <= kFoldScan;
+  if (!hist && nb != 1) return hipErrorInvalidValue;   // counting the ids needs one block
   if (!fold)
     hipLaunchKernelGGL(expert_scan_kernel, dim3(E), dim3(256), 0, stream, hist, nb, base, counts);
   // Column slices: enough blocks for ~512 in all, each slice >= 8 chunks

@@ -36,9 +36,9 @@
 namespace mgpt {
 // kernels (router.hip, dispatch.hip, gemm.hip, combine.hip, pack.hip)
 template <typename ActT>
-hipError_t launch_router(const ActT*, const float*, const float*, const float*, int, int, int,
-                         int, int32_t*, float*, int32_t*, float*, float*, const float*, float, int,
-                         float*, hipStream_t);
+hipError_t launch_router(const ActT*, const float*, const float*, const float*, const float*, int,
+                         int, int, int, int32_t*, float*, int32_t*, float*, float*, const float*,
+                         float, int, float*, hipStream_t);
 hipError_t launch_expf_probe(const float*, float*, int, hipStream_t);
 template <typename InT, typename ActT>
 hipError_t launch_permute(const InT*, const int32_t*, const int32_t*, int32_t*, int, int, int,
@@ -59,6 +59,7 @@ hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hip
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
 hipError_t launch_pack_router(const float*, int, int, int, int, float*, hipStream_t);
+hipError_t launch_pack_router_quads(const float*, int, int, int, float*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_dma(const bf16_t*, const bf16_t*, const float*, const float*,
                            const int32_t*, int, int, int, int, int, bf16_t*, int, int, float*, int,
@@ -192,6 +193,7 @@ struct mgpt_moe {
   int gemm_tile = 256;     // block tile of the large-M bf16 GEMMs (256 or 128)
   float* wr_g = nullptr;   // router weights [G][C][RE] (router_experts_per_wave)
   float* wr1 = nullptr;    // router weights [E][C] (split decode router, E > 16)
+  float* wr4 = nullptr;    // router weights [C/4][E][4] (one-launch decode router, E > 16)
   float* br = nullptr;     // [E]
   void* wgu = nullptr;     // [E][2Hp][C] of bf16 / fp8 / f32
   void* wd = nullptr;      // [E][Cp][Hp]
@@ -241,6 +243,11 @@ struct mgpt_moe {
   // Few tokens and many experts: the router's logits are spread over more
   // blocks (one expert per wave) instead of one block per 64 tokens.
   bool router_split(int N) const { return E > 16 && N < 4096; }
+  // one router block of tokens: logits and softmax in one launch, and the
+  // permute counts the ids itself (no histogram)
+  bool router_one_launch(int N, bool norm) const {
+    return wr4 && N <= kRouterTokens && !norm && C % 64 == 0 && C <= kDecodeRouterMaxC;
+  }
   // The bf16 large-M path (gemm_dma.hip), which may split its last round.
   // bias partials of the weight gradients' row chunks: at most 64 chunks of
   // the wider tile row (2Hp gate/up columns or C down columns) of
@@ -329,11 +336,11 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_g, h->wr1, h->br,  h->wgu,  h->wd,   h->sgu,  h->sd, h->bg,
-                  h->bu,   h->bd,  h->wdb, h->wgub, h->wrt, h->wgu_t, h->wd_t};
+  void* ptrs[] = {h->wr_g, h->wr1, h->wr4, h->br,  h->wgu,  h->wd,   h->sgu,  h->sd,
+                  h->bg,   h->bu,  h->bd,  h->wdb, h->wgub, h->wrt, h->wgu_t, h->wd_t};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
-  h->wr_g = h->wr1 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = h->wrt = nullptr;
+  h->wr_g = h->wr1 = h->wr4 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = h->wrt = nullptr;
   h->wgu = h->wd = h->wdb = h->wgub = h->wgu_t = h->wd_t = nullptr;
   h->loaded = false;
   h->bwd_ready = false;
@@ -487,6 +494,8 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
   const int RE = router_experts_per_wave(E);
   HIP_TRY(hipMalloc(&h->wr_g, sizeof(float) * ((E + RE - 1) / RE) * RE * C));
   if (E > 16) HIP_TRY(hipMalloc(&h->wr1, sizeof(float) * E * C));
+  if (E > 16 && C % 64 == 0 && C <= kDecodeRouterMaxC)
+    HIP_TRY(hipMalloc(&h->wr4, sizeof(float) * E * C));
   HIP_TRY(hipMalloc(&h->br, sizeof(float) * E));
   HIP_TRY(hipMalloc(&h->wgu, wb * E * 2 * Hp * C));
   HIP_TRY(hipMalloc(&h->wd, wb * E * Cp * Hp));
@@ -536,7 +545,8 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
     const float* s = src(0, (size_t)Cx * E);
     if (!s) break;
     if (launch_pack_router(s, Cx, C, E, RE, h->wr_g, st) != hipSuccess ||
-        (h->wr1 && launch_pack_router(s, Cx, C, E, 1, h->wr1, st) != hipSuccess)) {
+        (h->wr1 && launch_pack_router(s, Cx, C, E, 1, h->wr1, st) != hipSuccess) ||
+        (h->wr4 && launch_pack_router_quads(s, Cx, C, E, h->wr4, st) != hipSuccess)) {
       rc = fail(MGPT_ERR_HIP, "router pack failed");
       break;
     }
@@ -710,10 +720,13 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
   float* probs = train ? (float*)(ws + L.probs) : nullptr;
   ActT* gu = train ? (ActT*)(ws + L.gu) : nullptr;
   float* rstd = gamma ? (float*)(ws + L.rstd) : nullptr;
-  HIP_TRY(launch_router<IoT>(xi, h->wr_g, h->wr1, h->br, N, C, E, k, idx, topp, hist, logits,
+  const bool one_launch = h->router_one_launch(N, gamma != nullptr);
+  HIP_TRY(launch_router<IoT>(xi, h->wr_g, h->wr1, one_launch ? h->wr4 : nullptr, h->br, N, C, E,
+                             k, idx, topp, hist, logits,
                              probs, gamma, blk.eps, Cx, rstd, st));
   HIP_TRY(mark(1));
-  HIP_TRY((launch_permute<IoT, ActT>(xi, idx, hist, base, N, C, E, k, counts, perm, slot_of, xg,
+  HIP_TRY((launch_permute<IoT, ActT>(xi, idx, one_launch ? nullptr : hist, base, N, C, E, k,
+                                     counts, perm, slot_of, xg,
                                      rstd, gamma, st)));
   HIP_TRY(mark(2));
   if constexpr (sizeof(ActT) == 4) {

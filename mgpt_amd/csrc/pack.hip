@@ -179,6 +179,26 @@ hipError_t launch_pack_router(const float* wr, int Cx, int C, int E, int RE, flo
   return hipGetLastError();
 }
 
+// W_r [Cx][E] -> column quads [C/4][E][4] (zero past Cx): expert e's
+// columns 4q .. 4q+3 are one 16-byte entry, and the E entries of a quad are
+// contiguous.
+__global__ void pack_router_quads_kernel(const float* __restrict__ wr, int Cx, int C, int E,
+                                         float* __restrict__ out, int total) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int r = i % 4, e = (i / 4) % E, c = (i / (4 * E)) * 4 + r;
+  out[i] = c < Cx ? wr[(size_t)c * E + e] : 0.0f;
+}
+
+hipError_t launch_pack_router_quads(const float* wr, int Cx, int C, int E, float* out,
+                                    hipStream_t stream) {
+  if (C % 4) return hipErrorInvalidValue;
+  const int total = C * E;
+  hipLaunchKernelGGL(pack_router_quads_kernel, dim3((total + 255) / 256), dim3(256), 0, stream, wr,
+                     Cx, C, E, out, total);
+  return hipGetLastError();
+}
+
 // rows x nfill block: copy ncopy columns, zero the rest (pad), or copy
 // ncopy = nfill columns of a wider source (unpad).
 template <typename T>

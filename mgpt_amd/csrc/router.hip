@@ -20,6 +20,8 @@
 // expert-major as hist[e][block] for the per-expert scan of dispatch.hip.
 // Decode shapes (few tokens, E > 16) split phase 1 over more blocks, one
 // expert per wave, through a logits buffer.
+#include <type_traits>
+
 #include "common.hpp"
 #include "glibc_expf.hpp"
 
@@ -686,51 +688,292 @@ __global__ __launch_bounds__(256) void router_logits_pc_kernel(
 // and counted into hist[e][token / 64] with integer atomics
 // (router_logits_pc_kernel cleared those entries).  No shuffles or merge
 // rounds: four passes over the row in LDS, latency hidden across lanes.
+// The softmax / top-k of one token on one wave (lane e = expert e, l its
+// logit), with the row in LDS (row[e] = l for every lane already stored and
+// visible to the wave).  hist == nullptr: no histogram (the caller's
+// permute counts the ids itself).
+// The softmax / top-k of one token on one wave (lane e = expert e, l its
+// logit), with the row in LDS: row[e] = l for e < E and -inf for the lanes
+// past E, stored by every lane and visible to the wave.  hist == nullptr: no
+// histogram (the caller's permute counts the ids itself).
+//
+// Every pass reads the whole row (kMaxExperts floats, 16-byte aligned) as
+// quads, all reads before the arithmetic, and runs over all kMaxExperts
+// entries without branches: the lanes past E store neutral entries (-inf
+// for the running max, which '>' never takes; +0 for the sum, which is
+// never -0 and so is unchanged by adding +0; 0 for the ranks, below every
+// clamped probability), and the reductions keep the reference's order.
+__device__ __forceinline__ void softmax_topk_wave(float l, bool valid, int t, int e, int E,
+                                                  int k, float* row, const uint64_t* tab,
+                                                  int32_t* __restrict__ topk_idx,
+                                                  float* __restrict__ topk_p,
+                                                  int32_t* __restrict__ hist, int nb,
+                                                  float* __restrict__ probs) {
+  constexpr int kQ = kMaxExperts / 4;
+  const float4* row4 = reinterpret_cast<const float4*>(row);
+  auto load_row = [&](float (&r)[kMaxExperts]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kQ; ++q) {
+      const float4 v = row4[q];
+      r[4 * q] = v.x;
+      r[4 * q + 1] = v.y;
+      r[4 * q + 2] = v.z;
+      r[4 * q + 3] = v.w;
+    }
+  };
+  const bool mine = e < E;
+  float r[kMaxExperts];
+  load_row(r);
+  float m = r[0];
+#pragma unroll
+  for (int v = 1; v < kMaxExperts; ++v)
+    if (r[v] > m) m = r[v];
+  const float ex = mgpt_expf::expf_glibc(l - m, tab);
+  __builtin_amdgcn_wave_barrier();   // every lane has read the logits
+  row[e] = mine ? ex : 0.0f;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  load_row(r);
+  float sum = 0.0f;
+#pragma unroll
+  for (int v = 0; v < kMaxExperts; ++v) sum = sum + r[v];
+  const float inv = 1.0f / fmaxf(sum, 1e-15f);
+  const float p = fminf(fmaxf(ex * inv, 1e-7f), 1.0f);
+  __builtin_amdgcn_wave_barrier();
+  row[e] = mine ? p : 0.0f;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (!valid || !mine) return;
+  if (probs) probs[(size_t)t * E + e] = p;   // kept for the backward pass
+  load_row(r);
+  int rank = 0;
+#pragma unroll
+  for (int v = 0; v < kMaxExperts; ++v) rank += (r[v] > p) || (r[v] == p && v < e);
+  if (rank < k) {
+    topk_idx[(size_t)t * k + rank] = e;
+    topk_p[(size_t)t * k + rank] = p;
+    if (hist) atomicAdd(&hist[(size_t)e * nb + t / kRT], 1);
+  }
+}
+
 constexpr int kSoftmaxWaves = 4;   // tokens per block
 __global__ __launch_bounds__(kSoftmaxWaves * 64) void router_softmax_wave_kernel(
     const float* __restrict__ logits, int N, int E, int k, int32_t* __restrict__ topk_idx,
     float* __restrict__ topk_p, int32_t* __restrict__ hist, int nb, float* __restrict__ probs) {
-  __shared__ float s_row[kSoftmaxWaves][kMaxExperts];
+  __shared__ __align__(16) float s_row[kSoftmaxWaves][kMaxExperts];
   __shared__ uint64_t s_tab[32];
   const int w = threadIdx.x / kWave, e = lane_id();
   const int t = blockIdx.x * kSoftmaxWaves + w;
   if (threadIdx.x < 32) s_tab[threadIdx.x] = c_exp2_tab[threadIdx.x];
   float* row = s_row[w];
   const bool valid = t < N;   // wave-uniform
-  const bool mine = e < E;
-  const float l = (valid && mine) ? logits[(size_t)t * E + e] : 0.0f;
-  row[e] = l;
+  const float l = (valid && e < E) ? logits[(size_t)t * E + e] : 0.0f;
+  row[e] = e < E ? l : -INFINITY;
   __syncthreads();
-  float m = row[0];
-  for (int v = 1; v < E; ++v) {
-    const float lv = row[v];
-    if (lv > m) m = lv;
+  softmax_topk_wave(l, valid, t, e, E, k, row, s_tab, topk_idx, topk_p, hist, nb, probs);
+}
+
+// Decode router for a single block of tokens (N <= 64, E > 16, no
+// normalisation), logits and softmax in one launch.  A block owns one token
+// t: wave 0 runs the 64 chains acc = acc + p[c] (lane e = expert e, columns
+// ascending, then the bias: the reference's rounding sequence, as in the
+// other router kernels) and then the softmax / top-k of the token with
+// softmax_topk_wave; waves 1-3 (the other SIMDs) form the products p[e][c] =
+// x[t][c] * W_r[c][e] of step s + 2 into a triple-buffered LDS array while
+// the chain wave adds step s's.  No histogram: with one router block the
+// permute counts the ids itself.
+//
+// A wave issues about one vector instruction per four cycles, so a chain
+// wave that also formed its products took two issue slots per column (9-10
+// cycles per column at cfg5, against 3.7 for the adds alone); here it
+// issues one add and a quarter of an LDS read per column.  W_r comes from
+// its column-quad copy wr4 = [C/4][E][4] (lane e's 16 bytes of quad q at
+// (q*E + e)*16, so one load instruction reads 1 KB contiguous), requested
+// kDrPS - 1 steps ahead into the producers' registers with buffer loads
+// (scalar step offset, loop-invariant lane offsets); x[t] is widened into
+// LDS once and read as 16-byte broadcasts.
+constexpr int kDrCols = 64;               // columns per step
+constexpr int kDrQ = kDrCols / 4;         // column quads per step
+constexpr int kDrPLD = kDrCols + 4;       // floats per LDS product row
+constexpr int kDrPS = 4;                  // producer register stages
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename ActT>
+__global__ __launch_bounds__(256) void router_decode_kernel(
+    const ActT* __restrict__ x, const float4* __restrict__ wr4, const float* __restrict__ br,
+    int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
+    float* __restrict__ probs) {
+  __shared__ float4 s_x[kDecodeRouterMaxC / 4];          // x[t] widened to fp32
+  __shared__ float4 s_p[3][kMaxExperts * kDrPLD / 4];    // products [e][column]
+  __shared__ __align__(16) float s_row[kMaxExperts];
+  __shared__ uint64_t s_tab[32];
+  const int tid = threadIdx.x;
+  const int e = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int t = blockIdx.x;
+  const int ee = min(e, E - 1);   // lanes past E repeat the last expert
+  const int nst = C / kDrCols;    // steps (C is a multiple of 64)
+  // the step barrier: this wave's LDS writes and reads are complete
+  auto barrier = [&]() __attribute__((always_inline)) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+  if (w == 0 && e < 32) s_tab[e] = c_exp2_tab[e];
+  // W_r for the producers: wave w owns quads [q0, q0 + nq) of every step
+  // (6 + 5 + 5; waves 2 and 3 load a sixth quad, quad 15 again, in bounds,
+  // and skip it), in kDrPS register stages requested kDrPS - 1 steps ahead
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float4*>(wr4), (short)0, C * E * (int)sizeof(float), 0x00020000);
+  float4 wv[kDrPS][6];
+  uint32_t off[6];
+  int q0 = 0, nq = 6;
+  if (w == 2) { q0 = 6; nq = 5; }
+  if (w == 3) { q0 = 11; nq = 5; }
+#pragma unroll
+  for (int q = 0; q < 6; ++q) off[q] = (uint32_t)((min(q0 + q, kDrQ - 1)) * E + ee) * 16u;
+  auto load = [&](int j, float4 (&v)[6]) __attribute__((always_inline)) {
+    const int so = min(j, nst - 1) * kDrQ * E * 16;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(wrs, off[q], so, 0);
+      v[q] = make_float4(__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z),
+                         __uint_as_float(r.w));
+    }
+  };
+  {
+    // x[t] into LDS as fp32 by all 256 threads, 8 columns per thread and
+    // pass: every pass's load first, then the producers' first kDrPS - 1
+    // W_r requests (so that both latencies overlap and the wait for x does
+    // not wait for W_r), then the widened stores
+    constexpr int kXP = kDecodeRouterMaxC / (8 * 256);   // passes at the widest row
+    const ActT* xr = x + (size_t)t * C;
+    using XPiece = typename std::conditional<sizeof(ActT) == 2, uint4, float4>::type;
+    XPiece xv[kXP], xv2[kXP];
+#pragma unroll
+    for (int pp = 0; pp < kXP; ++pp) {
+      const int c = min(8 * tid + 8 * 256 * pp, C - 8);   // in bounds; stored only if < C
+      xv[pp] = *reinterpret_cast<const XPiece*>(xr + c);
+      if constexpr (sizeof(ActT) == 4) xv2[pp] = *reinterpret_cast<const XPiece*>(xr + c + 4);
+    }
+    if (w > 0) {
+#pragma unroll
+      for (int j = 0; j < kDrPS - 1; ++j) load(j, wv[j]);
+    }
+#pragma unroll
+    for (int pp = 0; pp < kXP; ++pp) {
+      const int c = 8 * tid + 8 * 256 * pp;
+      if (c < C) {
+        float4 lo, hi;
+        if constexpr (sizeof(ActT) == 2) {
+          const uint4 v = xv[pp];
+          lo = make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                           __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+          hi = make_float4(__uint_as_float(v.z << 16), __uint_as_float(v.z & 0xFFFF0000u),
+                           __uint_as_float(v.w << 16), __uint_as_float(v.w & 0xFFFF0000u));
+        } else {
+          lo = xv[pp];
+          hi = xv2[pp];
+        }
+        s_x[c / 4] = lo;
+        s_x[c / 4 + 1] = hi;
+      }
+    }
   }
-  const float ex = mgpt_expf::expf_glibc(l - m, s_tab);
-  __builtin_amdgcn_wave_barrier();   // every lane has read the logits
-  row[e] = ex;
+  barrier();   // x[t] and the table are in LDS
+
+  if (w > 0) {
+    // step j: request W_r of step j + kDrPS - 1 into its stage, then form
+    // step j's products from stage j % kDrPS into buffer j % 3 (row e,
+    // columns 4 * (q0 + q) ..)
+    auto produce = [&](int j, auto st_c) __attribute__((always_inline)) {
+      constexpr int st = decltype(st_c)::value;
+      constexpr int ahead = (st + kDrPS - 1) % kDrPS;
+      load(j + kDrPS - 1, wv[ahead]);
+      if (j >= nst) return;
+      float4* prow = s_p[j % 3] + (e * kDrPLD) / 4;
+      const float4* xs = s_x + (size_t)j * kDrQ;
+#pragma unroll
+      for (int q = 0; q < 6; ++q) {
+        if (q < nq) {
+          const float4 xv = xs[q0 + q];
+          const float4 wq = wv[st][q];
+          prow[q0 + q] = make_float4(xv.x * wq.x, xv.y * wq.y, xv.z * wq.z, xv.w * wq.w);
+        }
+      }
+    };
+    produce(0, IntC<0>{});
+    produce(1, IntC<1>{});
+    barrier();   // steps 0 and 1 are in LDS
+    for (int s = 0; s < nst; s += kDrPS) {
+      // iteration s: form step s + 2 (buffer (s + 2) % 3, last read during
+      // step s - 2's iteration, before the barrier just passed), then meet
+      // the chain wave, which adds step s meanwhile
+      produce(s + 2, IntC<2>{});
+      barrier();
+      if (s + 1 >= nst) break;
+      produce(s + 3, IntC<3>{});
+      barrier();
+      if (s + 2 >= nst) break;
+      produce(s + 4, IntC<0>{});
+      barrier();
+      if (s + 3 >= nst) break;
+      produce(s + 5, IntC<1>{});
+      barrier();
+    }
+    static_assert(kDrPS == 4, "the unrolled producer loop assumes 4 stages");
+    // drain the requests of steps past the end before the wave ends
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    return;
+  }
+
+  // the chain wave
+  // The compiler does not read the waits in inline asm: it would still count
+  // the products read a step earlier as pending where they are used and wait
+  // there for all reads, the ones just issued included.  Passing the
+  // registers through an empty asm after the barrier makes them that asm's
+  // results, with nothing left to wait for.
+  auto settle = [&](float4 (&v)[kDrQ]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < kDrQ; ++q)
+      asm volatile("" : "+v"(v[q].x), "+v"(v[q].y), "+v"(v[q].z), "+v"(v[q].w));
+  };
+  auto read = [&](int j, float4 (&v)[kDrQ]) __attribute__((always_inline)) {
+    const float4* prow = s_p[min(j, nst - 1) % 3] + (e * kDrPLD) / 4;
+#pragma unroll
+    for (int q = 0; q < kDrQ; ++q) v[q] = prow[q];
+  };
+  float acc = 0.0f;
+  float4 pa[kDrQ], pb[kDrQ];
+  barrier();   // steps 0 and 1 are in LDS
+  read(0, pa);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  settle(pa);
+  // step s: read step s + 1's products (formed before the last barrier),
+  // add step s's, meet the producers
+  auto step = [&](int s, float4 (&pc)[kDrQ], float4 (&pn)[kDrQ]) __attribute__((always_inline)) {
+    read(s + 1, pn);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < kDrQ; ++q) {
+      acc = acc + pc[q].x;
+      acc = acc + pc[q].y;
+      acc = acc + pc[q].z;
+      acc = acc + pc[q].w;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    barrier();
+    settle(pn);
+  };
+  for (int s = 0; s < nst; s += 2) {
+    step(s, pa, pb);
+    if (s + 1 >= nst) break;
+    step(s + 1, pb, pa);
+  }
+  const bool mine = e < E;
+  const float l = mine ? acc + br[ee] : 0.0f;
+  s_row[e] = mine ? l : -INFINITY;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float sum = 0.0f;
-  for (int v = 0; v < E; ++v) sum = sum + row[v];
-  const float inv = 1.0f / fmaxf(sum, 1e-15f);
-  const float p = fminf(fmaxf(ex * inv, 1e-7f), 1.0f);
-  __builtin_amdgcn_wave_barrier();
-  row[e] = p;
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (!valid || !mine) return;
-  if (probs) probs[(size_t)t * E + e] = p;   // kept for the backward pass
-  int rank = 0;
-  for (int v = 0; v < E; ++v) {
-    const float pv = row[v];
-    rank += (pv > p) || (pv == p && v < e);
-  }
-  if (rank < k) {
-    topk_idx[(size_t)t * k + rank] = e;
-    topk_p[(size_t)t * k + rank] = p;
-    atomicAdd(&hist[(size_t)e * nb + t / kRT], 1);
-  }
+  softmax_topk_wave(l, t < N, t, e, E, k, s_row, s_tab, topk_idx, topk_p, nullptr, 1, probs);
 }
 
 
@@ -742,14 +985,26 @@ __global__ __launch_bounds__(kSoftmaxWaves * 64) void router_softmax_wave_kernel
 // gamma (nullable): route on RMSNorm(x) * gamma instead of x, writing each
 // token's 1/rms to rstd [N]; cn: the mean's divisor (C, or the caller's width
 // when x's rows are zero-padded to C).
+//
+// wr4 (W_r as column quads [C/4][E][4]) set: the one-launch decode router,
+// for N <= 64, E > 16, no normalisation and C a multiple of 64 up to
+// kDecodeRouterMaxC; it writes no histogram (hist is unused).
 template <typename ActT>
-hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, const float* br,
-                         int N, int C, int E, int k, int32_t* topk_idx, float* topk_p,
-                         int32_t* hist, float* logits, float* probs, const float* gamma,
-                         float eps, int cn, float* rstd, hipStream_t stream) {
+hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, const float* wr4,
+                         const float* br, int N, int C, int E, int k, int32_t* topk_idx,
+                         float* topk_p, int32_t* hist, float* logits, float* probs,
+                         const float* gamma, float eps, int cn, float* rstd, hipStream_t stream) {
   const RowNorm nrm{gamma, eps, cn};
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
+  if (wr4) {
+    if (N > kRT || E <= 16 || E > kMaxExperts || gamma || C % 64 || C > kDecodeRouterMaxC)
+      return hipErrorInvalidValue;
+    hipLaunchKernelGGL((router_decode_kernel<ActT>), dim3(N), dim3(256), 0, stream, x,
+                       reinterpret_cast<const float4*>(wr4), br, N, C, E, k, topk_idx, topk_p,
+                       probs);
+    return hipGetLastError();
+  }
   if (logits && !gamma) {
     // decode shapes without normalisation: products and chains on separate
     // waves, then the softmax / top-k with one wave per token
@@ -790,12 +1045,13 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
 }
 
 template hipError_t launch_router<float>(const float*, const float*, const float*, const float*,
-                                         int, int, int, int, int32_t*, float*, int32_t*, float*,
-                                         float*, const float*, float, int, float*, hipStream_t);
+                                         const float*, int, int, int, int, int32_t*, float*,
+                                         int32_t*, float*, float*, const float*, float, int,
+                                         float*, hipStream_t);
 template hipError_t launch_router<bf16_t>(const bf16_t*, const float*, const float*,
-                                          const float*, int, int, int, int, int32_t*, float*,
-                                          int32_t*, float*, float*, const float*, float, int,
-                                          float*, hipStream_t);
+                                          const float*, const float*, int, int, int, int,
+                                          int32_t*, float*, int32_t*, float*, float*,
+                                          const float*, float, int, float*, hipStream_t);
 
 // Device expf over a buffer (tests compare it with the host's glibc expf).
 __global__ void expf_probe_kernel(const float* __restrict__ in, float* __restrict__ out, int n) {

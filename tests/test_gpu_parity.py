@@ -215,6 +215,50 @@ def test_router_shapes_against_oracle(E, k, tweak):
     check_close(y, ref["y"], TOL["f32"], cfg.name)
 
 
+ONE_LAUNCH_ROUTER_SHAPES = [
+    # (N, C, E, k, act, tweak): one router block of tokens with E > 16, the
+    # one-launch decode router (logits and softmax on one wave per token, no
+    # histogram: the permute counts the ids); widths of one step pair up to
+    # cfg5's 2048, single tokens, and ties decided by id
+    (1, 64, 17, 5, "f32", ""),
+    (37, 128, 33, 7, "f32", "tie_router"),
+    (64, 64, 64, 8, "f32", "tie_router"),
+    (64, 256, 40, 6, "f32", "wide_router"),
+    (50, 2048, 64, 8, "bf16", ""),
+    (64, 2048, 64, 2, "bf16", ""),
+    # a NaN logit in every token: expert 0's (the running max starts there,
+    # so it is NaN) and expert 3's (skipped by the strict '>')
+    (64, 128, 33, 4, "f32", "nan_w0"),
+    (64, 128, 33, 4, "f32", "nan_w3"),
+]
+
+
+@pytest.mark.parametrize("N,Cm,E,k,act,tweak", ONE_LAUNCH_ROUTER_SHAPES)
+def test_one_launch_router_against_oracle(N, Cm, E, k, act, tweak):
+    """Routing bit for bit (counts, ids, probabilities, slots) and outputs
+    against the oracle where a single block of tokens takes the one-launch
+    decode router."""
+    cfg = wl.MoEConfig(f"router1_{N}_{Cm}_E{E}_k{k}", N, Cm, E, k, 64, act, act, "normal")
+    inp = wl.make_inputs(cfg, C.SEED + N + E * 10 + k, bias_std=0.05)
+    if act == "bf16":
+        inp.x[:] = wl.bf16_round(inp.x)
+        inp.Wr[:] = wl.bf16_round(inp.Wr)
+    if tweak == "tie_router":
+        inp.Wr[:] = inp.Wr[:, :1]
+        inp.br[:] = 0.0
+    elif tweak == "wide_router":
+        inp.Wr[:] = inp.Wr * np.float32(100.0)
+    elif tweak.startswith("nan_w"):
+        inp.Wr[:, int(tweak[5:])] = np.float32(np.nan)
+    layer, y, r, _, _ = run_gpu(inp)
+    ref = O.forward(inp)
+    assert np.array_equal(r["counts"], ref["counts"]), "counts"
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["topk_p"].view(np.uint32), ref["topp"].view(np.uint32)), "topk_p"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    check_close(y, ref["y"], TOL[act], cfg.name)
+
+
 GEMM_SHAPES = [
     # (N, C, H, E, k): bf16 prefill shapes on the direct-to-LDS GEMM with
     # padded hidden (H % 128 != 0) and padded output features (C % 256 != 0),
