@@ -98,7 +98,7 @@ struct DItem {
 // within an m-tile.
 struct DScan {
   int cnt, rows_incl, tiles_incl, tiles_excl, tm;
-  __device__ __forceinline__ void init(const int32_t* __restrict__ counts, int E) {
+  __device__ __forceinline__ void init(const int32_t* counts, int E) {   // global or LDS
     const int l = lane_id();
     cnt = (l < E) ? counts[l] : 0;
     const int tiles = (cnt + kDBM - 1) / kDBM;
@@ -123,17 +123,101 @@ struct DScan {
   }
 };
 
-template <int EPI>
+// The routing of a single router block of tokens (nflat = N * k <= 512
+// flat ids), computed by each block of the gathering gate/up kernel instead
+// of a separate permute launch: per-expert counts, expert-major slots in
+// flat order within each expert (the permute's assignment, dispatch.hip),
+// and the slot -> token map s_tok.  Ids outside [0, E) get no slot, as in
+// the permute.  With publish set the block also writes counts, perm and
+// slot_of for the down GEMM, the combine and the caller.  All threads call
+// it; wave 0 does the work.
+constexpr int kGatherFlat = kRouterTokens * kMaxTopK;
+__device__ __forceinline__ void decode_rank(const int32_t* __restrict__ topk_idx, int nflat,
+                                            int k, int E, int* s_cnt, int* s_base, int* s_run,
+                                            int* s_tok, bool publish,
+                                            int32_t* __restrict__ counts,
+                                            int32_t* __restrict__ perm,
+                                            int32_t* __restrict__ slot_of) {
+  const int tid = threadIdx.x;
+  if (tid < kWave) {
+    const int l = tid;
+    constexpr int kIdPerLane = kGatherFlat / kWave;
+    int ids[kIdPerLane];
+#pragma unroll
+    for (int u = 0; u < kIdPerLane; ++u) {
+      const int f = u * kWave + l;
+      ids[u] = f < nflat ? topk_idx[f] : -1;
+    }
+    s_cnt[l] = 0;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+    for (int u = 0; u < kIdPerLane; ++u)
+      if (ids[u] >= 0 && ids[u] < E) atomicAdd(&s_cnt[ids[u]], 1);
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const int cnt = l < E ? s_cnt[l] : 0;
+    s_base[l] = wave_incl_scan(cnt) - cnt;
+    s_run[l] = 0;
+    if (publish && l < E) counts[l] = cnt;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (kWave - l));
+#pragma unroll
+    for (int u = 0; u < kIdPerLane; ++u) {
+      const int f0 = u * kWave;
+      if (f0 >= nflat) break;
+      const int f = f0 + l;
+      int e = ids[u];
+      const bool valid = e >= 0 && e < E;
+      if (!valid) e = 0;
+      unsigned long long match = __ballot(valid);
+#pragma unroll
+      for (int bit = 0; bit < 6; ++bit) {
+        const unsigned long long on = __ballot(valid && ((e >> bit) & 1));
+        match &= ((e >> bit) & 1) ? on : ~on;
+      }
+      if (valid) {
+        const int run = s_run[e];
+        const int slot = s_base[e] + run + __popcll(match & lt);
+        s_tok[slot] = f / k;
+        if (publish) {
+          perm[slot] = f;
+          slot_of[f] = slot;
+        }
+        // the highest lane of each expert group advances the running count
+        if ((match >> l) == 1ull) s_run[e] = run + __popcll(match);
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// GATHER (gate/up of a single router block, bf16 rows): the activation rows
+// come straight from the caller's x through s_tok instead of from the
+// gathered copy A, and the routing is computed in the block (decode_rank).
+template <int EPI, bool GATHER>
 __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
     const bf16_t* __restrict__ A, const fp8_t* __restrict__ B, const float* __restrict__ wscale,
     const float* __restrict__ bias0, const float* __restrict__ bias1,
     const int32_t* __restrict__ counts, int E, int K, int Npad, int n_store, int bias_ld,
-    bf16_t* __restrict__ out, int ldo) {
+    bf16_t* __restrict__ out, int ldo, const int32_t* __restrict__ topk_idx, int nflat, int k,
+    int32_t* __restrict__ counts_out, int32_t* __restrict__ perm,
+    int32_t* __restrict__ slot_of) {
   __shared__ __attribute__((aligned(1024))) char smem[kDStages * kDStage];
+  __shared__ int s_tok[GATHER ? kGatherFlat : 1];
+  __shared__ int s_cnt[GATHER ? kMaxExperts : 1], s_base[GATHER ? kMaxExperts : 1],
+      s_run[GATHER ? kMaxExperts : 1];
   const int nbx = Npad / kDBN;
   const int G = gridDim.x;
+  const int32_t* cnts = counts;
+  if constexpr (GATHER) {
+    decode_rank(topk_idx, nflat, k, E, s_cnt, s_base, s_run, s_tok, blockIdx.x == 0, counts_out,
+                perm, slot_of);
+    cnts = s_cnt;
+  }
   DScan sc;
-  sc.init(counts, E);
+  sc.init(cnts, E);
   int v = blockIdx.x;
   DItem cur;
   if (!sc.locate(E, nbx, v, &cur)) return;
@@ -171,9 +255,10 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
 #pragma unroll
     for (int i = 0; i < kDmaA; ++i) {
       const int r = 8 * w + 4 * i + lane / 16;            // activation row in the tile
-      const int tok = min(it.row0 + r, it.row_end - 1);
+      const int tok = min(it.row0 + r, it.row_end - 1);   // a slot
       const int chunk = (lane % 16) ^ (r & 15);
-      const char* ag = reinterpret_cast<const char*>(A) + (size_t)tok * arow_g +
+      const int src_row = GATHER ? s_tok[tok] : tok;
+      const char* ag = reinterpret_cast<const char*>(A) + (size_t)src_row * arow_g +
                        (size_t)kt * kDBK * 2 + chunk * 16;
       dma16(ag, st + (uint32_t)(kWBytes + (w * kDmaA + i) * 1024));
     }
@@ -311,15 +396,14 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
   }
 }
 
-}  // namespace
-
 // Persistent launch, one block per CU.  Requires K % 128 == 0, Npad % 256 ==
 // 0 and n_store % 64 == 0; max_mtiles bounds sum_e ceil(count_e / 32).
-template <int EPI>
-hipError_t launch_gemm_decode(const bf16_t* A, const fp8_t* B, const float* wscale,
-                              const float* bias0, const float* bias1, const int32_t* counts, int E,
-                              int K, int Npad, int n_store, int bias_ld, bf16_t* out, int ldo,
-                              int max_mtiles, hipStream_t stream) {
+template <int EPI, bool GATHER>
+hipError_t launch_decode(const bf16_t* A, const fp8_t* B, const float* wscale, const float* bias0,
+                         const float* bias1, const int32_t* counts, int E, int K, int Npad,
+                         int n_store, int bias_ld, bf16_t* out, int ldo, int max_mtiles,
+                         const int32_t* topk_idx, int nflat, int k, int32_t* counts_out,
+                         int32_t* perm, int32_t* slot_of, hipStream_t stream) {
   if (max_mtiles <= 0) return hipSuccess;
   if (K % kDBK != 0 || Npad % kDBN != 0 || n_store % 64 != 0) return hipErrorInvalidValue;
   static int num_cus = 0;
@@ -335,9 +419,22 @@ hipError_t launch_gemm_decode(const bf16_t* A, const fp8_t* B, const float* wsca
   const int items = max_mtiles * (Npad / kDBN);
   const int slots = MGPT_DECODE_BLOCKS_PER_CU * num_cus;
   const int grid = items < slots ? items : slots;
-  hipLaunchKernelGGL((gemm_decode_kernel<EPI>), dim3(grid), dim3(kDThreads), 0, stream, A, B,
-                     wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo);
+  hipLaunchKernelGGL((gemm_decode_kernel<EPI, GATHER>), dim3(grid), dim3(kDThreads), 0, stream, A,
+                     B, wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
+                     topk_idx, nflat, k, counts_out, perm, slot_of);
   return hipGetLastError();
+}
+
+}  // namespace
+
+template <int EPI>
+hipError_t launch_gemm_decode(const bf16_t* A, const fp8_t* B, const float* wscale,
+                              const float* bias0, const float* bias1, const int32_t* counts, int E,
+                              int K, int Npad, int n_store, int bias_ld, bf16_t* out, int ldo,
+                              int max_mtiles, hipStream_t stream) {
+  return launch_decode<EPI, false>(A, B, wscale, bias0, bias1, counts, E, K, Npad, n_store,
+                                   bias_ld, out, ldo, max_mtiles, nullptr, 0, 0, nullptr, nullptr,
+                                   nullptr, stream);
 }
 
 template hipError_t launch_gemm_decode<kEpiGateUp>(const bf16_t*, const fp8_t*, const float*,
@@ -348,5 +445,21 @@ template hipError_t launch_gemm_decode<kEpiDown>(const bf16_t*, const fp8_t*, co
                                                  const float*, const float*, const int32_t*, int,
                                                  int, int, int, int, bf16_t*, int, int,
                                                  hipStream_t);
+
+// The gate/up GEMM of a single router block of tokens (nflat = N * k <=
+// 512) with bf16 rows x [N][K]: routes the block itself (the permute's
+// counts, perm and slot_of, written by block 0) and reads the activation
+// rows from x, so no permute kernel runs and no gathered copy is written.
+hipError_t launch_gemm_decode_gather(const bf16_t* x, const fp8_t* B, const float* wscale,
+                                     const float* bias0, const float* bias1, const int32_t* topk_idx,
+                                     int nflat, int k, int E, int K, int Npad, int n_store,
+                                     int bias_ld, bf16_t* out, int ldo, int max_mtiles,
+                                     int32_t* counts, int32_t* perm, int32_t* slot_of,
+                                     hipStream_t stream) {
+  if (nflat > kGatherFlat || E > kMaxExperts || k < 1) return hipErrorInvalidValue;
+  return launch_decode<kEpiGateUp, true>(x, B, wscale, bias0, bias1, nullptr, E, K, Npad, n_store,
+                                         bias_ld, out, ldo, max_mtiles, topk_idx, nflat, k, counts,
+                                         perm, slot_of, stream);
+}
 
 }  // namespace mgpt

@@ -27,6 +27,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/mgpt_moe.h"
@@ -58,6 +59,10 @@ template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
+hipError_t launch_gemm_decode_gather(const bf16_t*, const fp8_t*, const float*, const float*,
+                                     const float*, const int32_t*, int, int, int, int, int, int,
+                                     int, bf16_t*, int, int, int32_t*, int32_t*, int32_t*,
+                                     hipStream_t);
 hipError_t launch_pack_router(const float*, int, int, int, int, float*, hipStream_t);
 hipError_t launch_pack_router_quads(const float*, int, int, int, float*, hipStream_t);
 template <int EPI>
@@ -725,9 +730,15 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
                              k, idx, topp, hist, logits,
                              probs, gamma, blk.eps, Cx, rstd, st));
   HIP_TRY(mark(1));
-  HIP_TRY((launch_permute<IoT, ActT>(xi, idx, one_launch ? nullptr : hist, base, N, C, E, k,
-                                     counts, perm, slot_of, xg,
-                                     rstd, gamma, st)));
+  // A decode step of one router block with bf16 rows and fp8 weights (no
+  // training caches): the gate/up weight-streaming GEMM routes the block
+  // itself and reads the rows of x, so no permute runs.
+  const bool gather_decode = !train && !gamma && std::is_same<IoT, bf16_t>::value &&
+                             h->wdt == MGPT_DTYPE_FP8_E4M3 && h->wgu_t && small_m(h, N) &&
+                             A <= (size_t)kRouterTokens * kMaxTopK;
+  if (!gather_decode)
+    HIP_TRY((launch_permute<IoT, ActT>(xi, idx, one_launch ? nullptr : hist, base, N, C, E, k,
+                                       counts, perm, slot_of, xg, rstd, gamma, st)));
   HIP_TRY(mark(2));
   if constexpr (sizeof(ActT) == 4) {
     const int mt = (int)((A + 63) / 64) + E;
@@ -745,8 +756,15 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
       if (fp8 && h->wgu_t) {
         // weight streaming: the persistent direct-to-LDS decode kernel on the
         // tiled copies
-        HIP_TRY(launch_gemm_decode<kEpiGateUp>(xg, (const fp8_t*)h->wgu_t, h->sgu, h->bg, h->bu,
-                                               counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt, st));
+        if (gather_decode)
+          HIP_TRY(launch_gemm_decode_gather(reinterpret_cast<const bf16_t*>(xi),
+                                            (const fp8_t*)h->wgu_t, h->sgu, h->bg, h->bu, idx,
+                                            (int)A, k, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt, counts,
+                                            perm, slot_of, st));
+        else
+          HIP_TRY(launch_gemm_decode<kEpiGateUp>(xg, (const fp8_t*)h->wgu_t, h->sgu, h->bg, h->bu,
+                                                 counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt,
+                                                 st));
         HIP_TRY(mark(3));
         HIP_TRY(launch_gemm_decode<kEpiDown>(hb, (const fp8_t*)h->wd_t, h->sd, h->bd, nullptr,
                                              counts, E, Hp, Cp, C, Cp, ob, C, mt, st));
