@@ -797,6 +797,10 @@ constexpr int kDrQ = kDrCols / 4;         // column quads per step
 constexpr int kDrPLD = kDrCols + 4;       // floats per LDS product row
 constexpr int kDrPS = 4;                  // producer register stages
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+// Word 3 of a raw buffer descriptor: DATA_FORMAT (bits 15-18) = 4, 32-bit
+// elements, no swizzle; offsets are bytes, and reads past num_records
+// return zeros (none are issued here).
+constexpr int kBufWord3 = 0x00020000;
 
 template <typename ActT>
 __global__ __launch_bounds__(256) void router_decode_kernel(
@@ -822,7 +826,7 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   // (6 + 5 + 5; waves 2 and 3 load a sixth quad, quad 15 again, in bounds,
   // and skip it), in kDrPS register stages requested kDrPS - 1 steps ahead
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float4*>(wr4), (short)0, C * E * (int)sizeof(float), 0x00020000);
+      const_cast<float4*>(wr4), (short)0, C * E * (int)sizeof(float), kBufWord3);
   float4 wv[kDrPS][6];
   uint32_t off[6];
   int q0 = 0, nq = 6;
