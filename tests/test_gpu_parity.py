@@ -314,6 +314,26 @@ def test_fp8_decode_shapes(N, Cm, H, E, k):
     check_close(y, ref["y"], TOL["fp8"], cfg.name)
 
 
+def test_fp8_decode_step_at_the_gather_limit():
+    """A decode step of one router block at the most flat ids the gathering
+    gate/up GEMM routes itself (N * k = 512) with Zipf-skewed routing, so the
+    large experts span several 32-row m-tiles: routing bit for bit and
+    outputs against the oracle."""
+    cfg = wl.MoEConfig("decode_gather_512", 64, 256, 17, 8, 256, "bf16", "fp8", "zipf")
+    inp = wl.make_inputs(cfg, C.SEED + 512, bias_std=0.02)
+    inp.x[:] = wl.bf16_round(inp.x)
+    inp.Wr[:] = wl.bf16_round(inp.Wr)
+    layer, y, r, _, _ = run_gpu(inp)
+    ref = O.forward(inp)
+    print(f"{cfg.name}: counts {ref['counts'].tolist()}", flush=True)
+    assert max(ref["counts"]) > 32, "expected an expert with several m-tiles"
+    assert np.array_equal(r["counts"], ref["counts"]), "counts"
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    assert np.array_equal(r["slot_of"][r["perm"]], np.arange(512, dtype=np.int32)), "slot_of"
+    check_close(y, ref["y"], TOL["fp8"], cfg.name)
+
+
 def test_deterministic_and_repeatable():
     case = C.ALL_CASES["bf16_e64_k6"]
     inp = C.build_inputs(case)
