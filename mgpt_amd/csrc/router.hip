@@ -372,6 +372,77 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
   drain_barrier();   // the block may reuse the LDS after this
 }
 
+// Softmax, top-k and histogram of the block's kRT tokens for E <= 32, with
+// no cross-lane traffic: each wave takes 64 / EP tokens at a time (EP = E
+// rounded up to a power of two), lane e of a token's group of EP lanes
+// holding expert e, and every lane runs the token's reductions itself over
+// the row in LDS, in the reference's order: the running max from element 0
+// with a strict '>' (NaN handling as the reference's), the glibc expf, the
+// sequential sum and clamp, and its rank under (p descending, id
+// ascending), which is the insertion top-k's order.  The entries past E
+// are made neutral (-inf for the max, +0 for the sum, which is never -0, 0
+// for the ranks, below every clamped probability), so every pass runs over
+// EP entries without branches.  The choices are counted into s_hist with
+// LDS atomics.  (The layout used for E > 32, L lanes per token merging
+// partial maxima and top-k lists with shuffles, took 8.2 k cycles per block
+// at cfg3 against 6.2 k here, barriers included.)
+template <int EP>
+__device__ __forceinline__ void softmax_topk_group(float (*s_l)[kMaxExperts + 1], int* s_hist,
+                                                   const uint64_t* tab, int tok0, int N, int E,
+                                                   int k, int32_t* __restrict__ topk_idx,
+                                                   float* __restrict__ topk_p,
+                                                   float* __restrict__ probs) {
+  constexpr int G = kWave / EP;   // tokens per wave and pass
+  const int lane = lane_id();
+  const int w = (int)threadIdx.x / kWave, nw = (int)blockDim.x / kWave;
+  const int e = lane % EP;
+  const bool mine = e < E;
+  for (int r0 = w * G; r0 < kRT; r0 += nw * G) {
+    const int r = r0 + lane / EP;
+    float* row = s_l[r];
+    float v[EP];
+    auto load_row = [&]() __attribute__((always_inline)) {
+#pragma unroll
+      for (int i = 0; i < EP; ++i) v[i] = row[i];
+    };
+    auto publish = [&](float value) __attribute__((always_inline)) {
+      __builtin_amdgcn_wave_barrier();   // every lane has read the row
+      row[e] = value;
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    const float l = row[e];
+    publish(mine ? l : -INFINITY);
+    load_row();
+    float m = v[0];
+#pragma unroll
+    for (int i = 1; i < EP; ++i)
+      if (v[i] > m) m = v[i];
+    const float ex = mgpt_expf::expf_glibc(l - m, tab);
+    publish(mine ? ex : 0.0f);
+    load_row();
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EP; ++i) sum = sum + v[i];
+    const float inv = 1.0f / fmaxf(sum, 1e-15f);
+    const float p = fminf(fmaxf(ex * inv, 1e-7f), 1.0f);
+    publish(mine ? p : 0.0f);
+    load_row();
+    int rank = 0;
+#pragma unroll
+    for (int i = 0; i < EP; ++i) rank += (v[i] > p) || (v[i] == p && i < e);
+    const int t = tok0 + r;
+    if (mine && t < N) {
+      if (probs) probs[(size_t)t * E + e] = p;   // kept for the backward pass
+      if (rank < k) {
+        topk_idx[(size_t)t * k + rank] = e;
+        topk_p[(size_t)t * k + rank] = p;
+        atomicAdd(&s_hist[e], 1);
+      }
+    }
+  }
+}
+
 // Softmax, top-k and the block histogram of kRT tokens whose logits are in
 // s_l (all threads of the block call it).  Per token (L lanes): the
 // max as the reference's strict '>' scan from element 0 computes it (so NaN
@@ -386,6 +457,24 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
                                                    int32_t* __restrict__ hist, int num_blocks,
                                                    float* __restrict__ probs) {
   const int tid = threadIdx.x;
+  if (E <= 32) {
+    __shared__ uint64_t s_tab32[32];
+    if (tid < 32) s_tab32[tid] = c_exp2_tab[tid];
+    __syncthreads();   // the table, and the logits the caller wrote
+    if (E <= 2)
+      softmax_topk_group<2>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+    else if (E <= 4)
+      softmax_topk_group<4>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+    else if (E <= 8)
+      softmax_topk_group<8>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+    else if (E <= 16)
+      softmax_topk_group<16>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+    else
+      softmax_topk_group<32>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+    __syncthreads();
+    if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
+    return;
+  }
   // L lanes per token: the largest power of two <= min(16, blockDim / 64),
   // so that the kRT tokens use (most of) the block
   int L = 1;
