@@ -868,8 +868,10 @@ __global__ __launch_bounds__(kSoftmaxWaves * 64) void router_softmax_wave_kernel
 // ascending, then the bias: the reference's rounding sequence, as in the
 // other router kernels) and then the softmax / top-k of the token with
 // softmax_topk_wave; waves 1-3 (the other SIMDs) form the products p[e][c] =
-// x[t][c] * W_r[c][e] of step s + 2 into a triple-buffered LDS array while
-// the chain wave adds step s's.  No histogram: with one router block the
+// x[t][c] * W_r[c][e] of 15 of each step's 16 column quads (5 each) for step
+// s + 2 into a triple-buffered LDS array while the chain wave adds step s's
+// (the chain wave forms the 16th quad's products itself: with 6 + 5 + 5 the
+// 6-quad wave set the pace).  No histogram: with one router block the
 // permute counts the ids itself.
 //
 // A wave issues about one vector instruction per four cycles, so a chain
@@ -885,6 +887,7 @@ constexpr int kDrCols = 64;               // columns per step
 constexpr int kDrQ = kDrCols / 4;         // column quads per step
 constexpr int kDrPLD = kDrCols + 4;       // floats per LDS product row
 constexpr int kDrPS = 4;                  // producer register stages
+constexpr int kDrPQ = 5;                  // column quads per producer wave and step
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Word 3 of a raw buffer descriptor: DATA_FORMAT (bits 15-18) = 4, 32-bit
 // elements, no swizzle; offsets are bytes, and reads past num_records
@@ -911,22 +914,21 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
   if (w == 0 && e < 32) s_tab[e] = c_exp2_tab[e];
-  // W_r for the producers: wave w owns quads [q0, q0 + nq) of every step
-  // (6 + 5 + 5; waves 2 and 3 load a sixth quad, quad 15 again, in bounds,
-  // and skip it), in kDrPS register stages requested kDrPS - 1 steps ahead
+  // W_r for the producers: wave w owns quads [q0, q0 + kDrPQ) of every step
+  // (5 + 5 + 5; the chain wave forms the last quad's products itself, which
+  // balances the three), in kDrPS register stages requested kDrPS - 1 steps
+  // ahead
   const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<float4*>(wr4), (short)0, C * E * (int)sizeof(float), kBufWord3);
-  float4 wv[kDrPS][6];
-  uint32_t off[6];
-  int q0 = 0, nq = 6;
-  if (w == 2) { q0 = 6; nq = 5; }
-  if (w == 3) { q0 = 11; nq = 5; }
+  float4 wv[kDrPS][kDrPQ];
+  uint32_t off[kDrPQ];
+  const int q0 = w > 0 ? (w - 1) * kDrPQ : 0;
 #pragma unroll
-  for (int q = 0; q < 6; ++q) off[q] = (uint32_t)((min(q0 + q, kDrQ - 1)) * E + ee) * 16u;
-  auto load = [&](int j, float4 (&v)[6]) __attribute__((always_inline)) {
+  for (int q = 0; q < kDrPQ; ++q) off[q] = (uint32_t)((q0 + q) * E + ee) * 16u;
+  auto load = [&](int j, float4 (&v)[kDrPQ]) __attribute__((always_inline)) {
     const int so = min(j, nst - 1) * kDrQ * E * 16;
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
+    for (int q = 0; q < kDrPQ; ++q) {
       const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(wrs, off[q], so, 0);
       v[q] = make_float4(__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z),
                          __uint_as_float(r.w));
@@ -985,12 +987,10 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
       float4* prow = s_p[j % 3] + (e * kDrPLD) / 4;
       const float4* xs = s_x + (size_t)j * kDrQ;
 #pragma unroll
-      for (int q = 0; q < 6; ++q) {
-        if (q < nq) {
-          const float4 xv = xs[q0 + q];
-          const float4 wq = wv[st][q];
-          prow[q0 + q] = make_float4(xv.x * wq.x, xv.y * wq.y, xv.z * wq.z, xv.w * wq.w);
-        }
+      for (int q = 0; q < kDrPQ; ++q) {
+        const float4 xv = xs[q0 + q];
+        const float4 wq = wv[st][q];
+        prow[q0 + q] = make_float4(xv.x * wq.x, xv.y * wq.y, xv.z * wq.z, xv.w * wq.w);
       }
     };
     produce(0, IntC<0>{});
@@ -1024,43 +1024,63 @@ __global__ __launch_bounds__(256) void router_decode_kernel(
   // there for all reads, the ones just issued included.  Passing the
   // registers through an empty asm after the barrier makes them that asm's
   // results, with nothing left to wait for.
-  auto settle = [&](float4 (&v)[kDrQ]) __attribute__((always_inline)) {
+  constexpr int kPQ = kDrQ - 1;   // product quads in LDS; the last is the chain wave's
+  auto settle = [&](float4 (&v)[kPQ]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < kDrQ; ++q)
+    for (int q = 0; q < kPQ; ++q)
       asm volatile("" : "+v"(v[q].x), "+v"(v[q].y), "+v"(v[q].z), "+v"(v[q].w));
   };
-  auto read = [&](int j, float4 (&v)[kDrQ]) __attribute__((always_inline)) {
+  auto read = [&](int j, float4 (&v)[kPQ]) __attribute__((always_inline)) {
     const float4* prow = s_p[min(j, nst - 1) % 3] + (e * kDrPLD) / 4;
 #pragma unroll
-    for (int q = 0; q < kDrQ; ++q) v[q] = prow[q];
+    for (int q = 0; q < kPQ; ++q) v[q] = prow[q];
   };
+  // W_r's last quad of each step, for the chain wave's own products,
+  // requested two steps ahead
+  const uint32_t off_c = (uint32_t)(kPQ * E + ee) * 16u;
+  auto load_c = [&](int j) __attribute__((always_inline)) -> float4 {
+    const u32x4 r = __builtin_amdgcn_raw_buffer_load_b128(wrs, off_c, min(j, nst - 1) * kDrQ * E * 16, 0);
+    return make_float4(__uint_as_float(r.x), __uint_as_float(r.y), __uint_as_float(r.z),
+                       __uint_as_float(r.w));
+  };
+  float4 wca = load_c(0), wcb = load_c(1);
   float acc = 0.0f;
-  float4 pa[kDrQ], pb[kDrQ];
+  float4 pa[kPQ], pb[kPQ];
   barrier();   // steps 0 and 1 are in LDS
   read(0, pa);
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   settle(pa);
-  // step s: read step s + 1's products (formed before the last barrier),
-  // add step s's, meet the producers
-  auto step = [&](int s, float4 (&pc)[kDrQ], float4 (&pn)[kDrQ]) __attribute__((always_inline)) {
+  // step s: read x's last quad of step s and step s + 1's products (formed
+  // before the last barrier), add step s's 15 quads from LDS and then its
+  // last quad from products formed here, request W_r's last quad of step
+  // s + 2, meet the producers
+  auto step = [&](int s, float4 (&pc)[kPQ], float4 (&pn)[kPQ], float4& wc)
+      __attribute__((always_inline)) {
+    const float4 xq = s_x[(size_t)s * kDrQ + kPQ];
     read(s + 1, pn);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int q = 0; q < kDrQ; ++q) {
+    for (int q = 0; q < kPQ; ++q) {
       acc = acc + pc[q].x;
       acc = acc + pc[q].y;
       acc = acc + pc[q].z;
       acc = acc + pc[q].w;
     }
+    acc = acc + xq.x * wc.x;
+    acc = acc + xq.y * wc.y;
+    acc = acc + xq.z * wc.z;
+    acc = acc + xq.w * wc.w;
+    wc = load_c(s + 2);
     __builtin_amdgcn_sched_barrier(0);
     barrier();
     settle(pn);
   };
   for (int s = 0; s < nst; s += 2) {
-    step(s, pa, pb);
+    step(s, pa, pb, wca);
     if (s + 1 >= nst) break;
-    step(s + 1, pb, pa);
+    step(s + 1, pb, pa, wcb);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the requests past the last step
   const bool mine = e < E;
   const float l = mine ? acc + br[ee] : 0.0f;
   s_row[e] = mine ? l : -INFINITY;
