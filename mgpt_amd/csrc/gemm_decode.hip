@@ -123,9 +123,9 @@ struct DScan {
   }
 };
 
-// The routing of a single router block of tokens (nflat = N * k <= 512
-// flat ids), computed by each block of the gathering gate/up kernel instead
-// of a separate permute launch: per-expert counts, expert-major slots in
+// The routing of at most 512 flat ids (nflat = N * k), computed by each
+// block of the gathering gate/up kernel instead of a separate permute
+// launch: per-expert counts, expert-major slots in
 // flat order within each expert (the permute's assignment, dispatch.hip),
 // and the slot -> token map s_tok.  Ids outside [0, E) get no slot, as in
 // the permute.  With publish set the block also writes counts, perm and
@@ -193,7 +193,7 @@ __device__ __forceinline__ void decode_rank(const int32_t* __restrict__ topk_idx
   __syncthreads();
 }
 
-// GATHER (gate/up of a single router block, bf16 rows): the activation rows
+// GATHER (gate/up of at most 512 flat ids, bf16 rows): the activation rows
 // come straight from the caller's x through s_tok instead of from the
 // gathered copy A, and the routing is computed in the block (decode_rank).
 template <int EPI, bool GATHER>
@@ -446,8 +446,8 @@ template hipError_t launch_gemm_decode<kEpiDown>(const bf16_t*, const fp8_t*, co
                                                  int, int, int, int, bf16_t*, int, int,
                                                  hipStream_t);
 
-// The gate/up GEMM of a single router block of tokens (nflat = N * k <=
-// 512) with bf16 rows x [N][K]: routes the block itself (the permute's
+// The gate/up GEMM of at most 512 flat ids (nflat = N * k) with bf16 rows
+// x [N][K]: routes the ids itself (the permute's
 // counts, perm and slot_of, written by block 0) and reads the activation
 // rows from x, so no permute kernel runs and no gathered copy is written.
 hipError_t launch_gemm_decode_gather(const bf16_t* x, const fp8_t* B, const float* wscale,

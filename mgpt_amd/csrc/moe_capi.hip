@@ -730,9 +730,9 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
                              k, idx, topp, hist, logits,
                              probs, gamma, blk.eps, Cx, rstd, st));
   HIP_TRY(mark(1));
-  // A decode step of one router block with bf16 rows and fp8 weights (no
-  // training caches): the gate/up weight-streaming GEMM routes the block
-  // itself and reads the rows of x, so no permute runs.
+  // A decode step of at most 512 flat ids (N * k) with bf16 rows and fp8
+  // weights (no training caches): the gate/up weight-streaming GEMM routes
+  // the ids itself and reads the rows of x, so no permute runs.
   const bool gather_decode = !train && !gamma && std::is_same<IoT, bf16_t>::value &&
                              h->wdt == MGPT_DTYPE_FP8_E4M3 && h->wgu_t && small_m(h, N) &&
                              A <= (size_t)kRouterTokens * kMaxTopK;

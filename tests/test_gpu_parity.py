@@ -294,6 +294,9 @@ DECODE_SHAPES = [
     (200, 512, 384, 16, 4),
     (8, 256, 256, 64, 2),
     (33, 1024, 640, 32, 8),
+    # two router blocks (N > 64) with N * k <= 512: the gate/up GEMM still
+    # routes all the flat ids itself
+    (100, 256, 256, 32, 4),
     # C % 128 == 64: no tiled weight copy, the register-staged fp8 path
     (40, 192, 256, 16, 4),
 ]
