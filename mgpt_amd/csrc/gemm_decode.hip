@@ -35,11 +35,7 @@ constexpr int kDBK = 128;                    // columns per stage
 #endif
 constexpr int kDStages = MGPT_DECODE_STAGES;   // ring depth (LDS: 40 KB a stage)
 constexpr int kWBytes = kDBN * kDBK;         // 32 KB of fp8 weights
-constexpr int kABytes = kDBM * kDBK * 2;     // 8 KB of bf16 activations
-constexpr int kDStage = kWBytes + kABytes;   // 40 KB
 constexpr int kDmaW = kWBytes / 1024 / 4;    // 8 weight blocks per wave
-constexpr int kDmaA = kABytes / 1024 / 4;    // 2 activation blocks per wave
-constexpr int kDma = kDmaW + kDmaA;
 
 typedef __attribute__((address_space(3))) char lds_char;
 
@@ -196,15 +192,27 @@ __device__ __forceinline__ void decode_rank(const int32_t* __restrict__ topk_idx
 // GATHER (gate/up of at most 512 flat ids, bf16 rows): the activation rows
 // come straight from the caller's x through s_tok instead of from the
 // gathered copy A, and the routing is computed in the block (decode_rank).
-template <int EPI, bool GATHER>
+template <int EPI, bool GATHER, typename XT>
 __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
-    const bf16_t* __restrict__ A, const fp8_t* __restrict__ B, const float* __restrict__ wscale,
+    const XT* __restrict__ A, const fp8_t* __restrict__ B, const float* __restrict__ wscale,
     const float* __restrict__ bias0, const float* __restrict__ bias1,
     const int32_t* __restrict__ counts, int E, int K, int Npad, int n_store, int bias_ld,
     bf16_t* __restrict__ out, int ldo, const int32_t* __restrict__ topk_idx, int nflat, int k,
     int32_t* __restrict__ counts_out, int32_t* __restrict__ perm,
     int32_t* __restrict__ slot_of) {
-  __shared__ __attribute__((aligned(1024))) char smem[kDStages * kDStage];
+  // Activation rows of XT (bf16, or the caller's fp32 rows when gathering):
+  // kRowB bytes per stage row, staged as they are and converted to bf16 when
+  // the fragments are read.
+  constexpr int kXS = (int)sizeof(XT);
+  constexpr int kAB = kDBM * kDBK * kXS;       // activation bytes per stage
+  constexpr int kStage = kWBytes + kAB;
+  constexpr int kDA = kAB / 1024 / 4;          // activation blocks per wave
+  constexpr int kDm = kDmaW + kDA;             // loads per wave and stage
+  constexpr int kRowB = kDBK * kXS;            // LDS bytes per activation row
+  constexpr int kRowsPerBlk = 1024 / kRowB;
+  constexpr int kChunks = kRowB / 16;          // 16-byte chunks per row
+  static_assert(kXS == 2 || kXS == 4, "bf16 or fp32 rows");
+  __shared__ __attribute__((aligned(1024))) char smem[kDStages * kStage];
   __shared__ int s_tok[GATHER ? kGatherFlat : 1];
   __shared__ int s_cnt[GATHER ? kMaxExperts : 1], s_base[GATHER ? kMaxExperts : 1],
       s_run[GATHER ? kMaxExperts : 1];
@@ -230,14 +238,15 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
 
   // DMA lane mapping.  Weights: 128-byte rows, wave w fills rows 64w ..
   // 64w+63 in 8 blocks of 8 rows; lane l covers row 8i + l/8, slot l%8 =
-  // chunk ^ ((row >> 1) & 7).  Activations: 256-byte rows, wave w fills rows
-  // 8w .. 8w+7 in 2 blocks of 4 rows; lane l covers row 4i + l/16, slot
-  // l%16 = chunk ^ (row & 15).  Activation rows past the item's last token
-  // re-read that token (in bounds, never stored).
+  // chunk ^ ((row >> 1) & 7).  Activations: kRowB-byte rows (256 for bf16,
+  // 512 for fp32), wave w fills rows 8w .. 8w+7 in kDA blocks of
+  // kRowsPerBlk rows; lane l covers row kRowsPerBlk*i + l/kChunks, slot
+  // l%kChunks = chunk ^ (row & (kChunks - 1)).  Activation rows past the
+  // item's last token re-read that token (in bounds, never stored).
   // Weights are in the tiled layout [E][Npad/256][K/128][256][128]: a
   // stage is one contiguous 32 KB block, rows 128 bytes apart.
   const size_t wrow_g = (size_t)kDBK;       // fp8 bytes between weight rows of a stage
-  const size_t arow_g = (size_t)K * 2;      // bf16 bytes per activation row
+  const size_t arow_g = (size_t)K * kXS;    // bytes per activation row
   uint32_t woff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
@@ -245,7 +254,7 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
     woff[i] = (uint32_t)(lane / 8) * (uint32_t)wrow_g + (uint32_t)(((lane % 8) ^ ((r >> 1) & 7)) * 16);
   }
   auto dma_stage = [&](const DItem& it, int kt, int stage) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + (uint32_t)(stage * kDStage);
+    const uint32_t st = lds0 + (uint32_t)(stage * kStage);
     const char* wg = reinterpret_cast<const char*>(B) +
                      (((size_t)it.expert * nbx + it.n0 / kDBN) * KT + kt) * (size_t)kWBytes +
                      (size_t)(64 * w) * wrow_g;
@@ -253,14 +262,14 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
     for (int i = 0; i < kDmaW; ++i)
       dma16(wg + (size_t)(8 * i) * wrow_g + woff[i & 1], st + (uint32_t)((w * kDmaW + i) * 1024));
 #pragma unroll
-    for (int i = 0; i < kDmaA; ++i) {
-      const int r = 8 * w + 4 * i + lane / 16;            // activation row in the tile
-      const int tok = min(it.row0 + r, it.row_end - 1);   // a slot
-      const int chunk = (lane % 16) ^ (r & 15);
+    for (int i = 0; i < kDA; ++i) {
+      const int r = 8 * w + kRowsPerBlk * i + lane / kChunks;   // activation row in the tile
+      const int tok = min(it.row0 + r, it.row_end - 1);         // a slot
+      const int chunk = (lane % kChunks) ^ (r & (kChunks - 1));
       const int src_row = GATHER ? s_tok[tok] : tok;
       const char* ag = reinterpret_cast<const char*>(A) + (size_t)src_row * arow_g +
-                       (size_t)kt * kDBK * 2 + chunk * 16;
-      dma16(ag, st + (uint32_t)(kWBytes + (w * kDmaA + i) * 1024));
+                       (size_t)kt * kRowB + chunk * 16;
+      dma16(ag, st + (uint32_t)(kWBytes + (w * kDA + i) * 1024));
     }
   };
 
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
   // done with stage c-1, which the DMA issued right after refills.
   auto next_stage_barrier = [&]() __attribute__((always_inline)) {
     --ahead;
-    if (ahead >= kDStages - 2) stage_barrier<(kDStages - 2) * kDma>();
+    if (ahead >= kDStages - 2) stage_barrier<(kDStages - 2) * kDm>();
     else stage_barrier<0>();
     advance();
   };
@@ -301,9 +310,20 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
     return *reinterpret_cast<const uint4*>(st + row * kDBK + ((chunk ^ wswz) << 4));
   };
   auto afrag = [&](const char* st, int ks) -> bf16x8 {
-    const int chunk = 8 * lhalf + ks;
-    return *reinterpret_cast<const bf16x8*>(st + kWBytes + lrow * (kDBK * 2) +
-                                            ((chunk ^ (lrow & 15)) << 4));
+    const int c = 8 * lhalf + ks;   // columns 8c .. 8c+7 of the stage
+    const char* row = st + kWBytes + lrow * kRowB;
+    if constexpr (kXS == 2) {
+      return *reinterpret_cast<const bf16x8*>(row + ((c ^ (lrow & 15)) << 4));
+    } else {
+      // two 16-byte chunks of fp32 rounded to bf16 by v_cvt_pk_bf16_f32
+      // (nearest even, fp32 denormals kept: the rounding f32_to_bf16 does in
+      // software for the permute's gather, at 4 instructions a fragment)
+      typedef float f32x8 __attribute__((ext_vector_type(8)));
+      const float4 a = *reinterpret_cast<const float4*>(row + (((2 * c) ^ (lrow & 31)) << 4));
+      const float4 b = *reinterpret_cast<const float4*>(row + (((2 * c + 1) ^ (lrow & 31)) << 4));
+      const f32x8 v = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      return __builtin_convertvector(v, bf16x8);
+    }
   };
 
 #pragma unroll
@@ -320,7 +340,7 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[j][e] = 0.0f;
     for (int kt = 0; kt < KT; ++kt) {
-      const char* st = smem + cstage * kDStage;
+      const char* st = smem + cstage * kStage;
       // 8 k-steps: weights as 4 chunks of 16 fp8 per row (2 k-steps each)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -398,8 +418,8 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
 
 // Persistent launch, one block per CU.  Requires K % 128 == 0, Npad % 256 ==
 // 0 and n_store % 64 == 0; max_mtiles bounds sum_e ceil(count_e / 32).
-template <int EPI, bool GATHER>
-hipError_t launch_decode(const bf16_t* A, const fp8_t* B, const float* wscale, const float* bias0,
+template <int EPI, bool GATHER, typename XT>
+hipError_t launch_decode(const XT* A, const fp8_t* B, const float* wscale, const float* bias0,
                          const float* bias1, const int32_t* counts, int E, int K, int Npad,
                          int n_store, int bias_ld, bf16_t* out, int ldo, int max_mtiles,
                          const int32_t* topk_idx, int nflat, int k, int32_t* counts_out,
@@ -419,7 +439,7 @@ hipError_t launch_decode(const bf16_t* A, const fp8_t* B, const float* wscale, c
   const int items = max_mtiles * (Npad / kDBN);
   const int slots = MGPT_DECODE_BLOCKS_PER_CU * num_cus;
   const int grid = items < slots ? items : slots;
-  hipLaunchKernelGGL((gemm_decode_kernel<EPI, GATHER>), dim3(grid), dim3(kDThreads), 0, stream, A,
+  hipLaunchKernelGGL((gemm_decode_kernel<EPI, GATHER, XT>), dim3(grid), dim3(kDThreads), 0, stream, A,
                      B, wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
                      topk_idx, nflat, k, counts_out, perm, slot_of);
   return hipGetLastError();
@@ -432,7 +452,7 @@ hipError_t launch_gemm_decode(const bf16_t* A, const fp8_t* B, const float* wsca
                               const float* bias0, const float* bias1, const int32_t* counts, int E,
                               int K, int Npad, int n_store, int bias_ld, bf16_t* out, int ldo,
                               int max_mtiles, hipStream_t stream) {
-  return launch_decode<EPI, false>(A, B, wscale, bias0, bias1, counts, E, K, Npad, n_store,
+  return launch_decode<EPI, false, bf16_t>(A, B, wscale, bias0, bias1, counts, E, K, Npad, n_store,
                                    bias_ld, out, ldo, max_mtiles, nullptr, 0, 0, nullptr, nullptr,
                                    nullptr, stream);
 }
@@ -446,20 +466,32 @@ template hipError_t launch_gemm_decode<kEpiDown>(const bf16_t*, const fp8_t*, co
                                                  int, int, int, int, bf16_t*, int, int,
                                                  hipStream_t);
 
-// The gate/up GEMM of at most 512 flat ids (nflat = N * k) with bf16 rows
-// x [N][K]: routes the ids itself (the permute's
+// The gate/up GEMM of at most 512 flat ids (nflat = N * k) with the
+// caller's rows x [N][K] (bf16, or fp32 rounded to bf16 as the permute
+// would): routes the ids itself (the permute's
 // counts, perm and slot_of, written by block 0) and reads the activation
 // rows from x, so no permute kernel runs and no gathered copy is written.
-hipError_t launch_gemm_decode_gather(const bf16_t* x, const fp8_t* B, const float* wscale,
+template <typename XT>
+hipError_t launch_gemm_decode_gather(const XT* x, const fp8_t* B, const float* wscale,
                                      const float* bias0, const float* bias1, const int32_t* topk_idx,
                                      int nflat, int k, int E, int K, int Npad, int n_store,
                                      int bias_ld, bf16_t* out, int ldo, int max_mtiles,
                                      int32_t* counts, int32_t* perm, int32_t* slot_of,
                                      hipStream_t stream) {
   if (nflat > kGatherFlat || E > kMaxExperts || k < 1) return hipErrorInvalidValue;
-  return launch_decode<kEpiGateUp, true>(x, B, wscale, bias0, bias1, nullptr, E, K, Npad, n_store,
+  return launch_decode<kEpiGateUp, true, XT>(x, B, wscale, bias0, bias1, nullptr, E, K, Npad, n_store,
                                          bias_ld, out, ldo, max_mtiles, topk_idx, nflat, k, counts,
                                          perm, slot_of, stream);
 }
+template hipError_t launch_gemm_decode_gather<bf16_t>(const bf16_t*, const fp8_t*, const float*,
+                                                       const float*, const float*, const int32_t*,
+                                                       int, int, int, int, int, int, int, bf16_t*,
+                                                       int, int, int32_t*, int32_t*, int32_t*,
+                                                       hipStream_t);
+template hipError_t launch_gemm_decode_gather<float>(const float*, const fp8_t*, const float*,
+                                                      const float*, const float*, const int32_t*,
+                                                      int, int, int, int, int, int, int, bf16_t*,
+                                                      int, int, int32_t*, int32_t*, int32_t*,
+                                                      hipStream_t);
 
 }  // namespace mgpt

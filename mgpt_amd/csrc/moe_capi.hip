@@ -59,7 +59,8 @@ template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
 hipError_t launch_pad_row(const float*, int, float*, int, hipStream_t);
-hipError_t launch_gemm_decode_gather(const bf16_t*, const fp8_t*, const float*, const float*,
+template <typename XT>
+hipError_t launch_gemm_decode_gather(const XT*, const fp8_t*, const float*, const float*,
                                      const float*, const int32_t*, int, int, int, int, int, int,
                                      int, bf16_t*, int, int, int32_t*, int32_t*, int32_t*,
                                      hipStream_t);
@@ -730,12 +731,12 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
                              k, idx, topp, hist, logits,
                              probs, gamma, blk.eps, Cx, rstd, st));
   HIP_TRY(mark(1));
-  // A decode step of at most 512 flat ids (N * k) with bf16 rows and fp8
-  // weights (no training caches): the gate/up weight-streaming GEMM routes
-  // the ids itself and reads the rows of x, so no permute runs.
-  const bool gather_decode = !train && !gamma && std::is_same<IoT, bf16_t>::value &&
-                             h->wdt == MGPT_DTYPE_FP8_E4M3 && h->wgu_t && small_m(h, N) &&
-                             A <= (size_t)kRouterTokens * kMaxTopK;
+  // A decode step of at most 512 flat ids (N * k) with fp8 weights (no
+  // training caches): the gate/up weight-streaming GEMM routes the ids
+  // itself and reads the caller's rows of x (bf16, or fp32 rounded as the
+  // permute would), so no permute runs.
+  const bool gather_decode = !train && !gamma && h->wdt == MGPT_DTYPE_FP8_E4M3 && h->wgu_t &&
+                             small_m(h, N) && A <= (size_t)kRouterTokens * kMaxTopK;
   if (!gather_decode)
     HIP_TRY((launch_permute<IoT, ActT>(xi, idx, one_launch ? nullptr : hist, base, N, C, E, k,
                                        counts, perm, slot_of, xg, rstd, gamma, st)));
@@ -757,8 +758,7 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
         // weight streaming: the persistent direct-to-LDS decode kernel on the
         // tiled copies
         if (gather_decode)
-          HIP_TRY(launch_gemm_decode_gather(reinterpret_cast<const bf16_t*>(xi),
-                                            (const fp8_t*)h->wgu_t, h->sgu, h->bg, h->bu, idx,
+          HIP_TRY(launch_gemm_decode_gather<IoT>(xi, (const fp8_t*)h->wgu_t, h->sgu, h->bg, h->bu, idx,
                                             (int)A, k, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp, mt, counts,
                                             perm, slot_of, st));
         else

@@ -47,8 +47,11 @@ class MoELayer:
 
     def __del__(self):
         h = getattr(self, "_h", None)
-        if h is not None and h.value:
-            capi.lib().mgpt_moe_destroy(h)
+        # at interpreter exit the module's globals may already be gone; the
+        # process then releases the device memory itself
+        lib = getattr(capi, "lib", None) if capi is not None else None
+        if h is not None and h.value and lib is not None:
+            lib().mgpt_moe_destroy(h)
             self._h = None
 
     # ---------------------------------------------------------------- params

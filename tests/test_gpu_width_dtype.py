@@ -15,6 +15,8 @@ reference bit for bit by tests/test_oracle.py): routing bit for bit, outputs
 and gradients normwise and elementwise within 1e-5 (fp32), 2e-2 (bf16
 products), 6e-2 (fp8 weights).
 """
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -192,6 +194,66 @@ def test_f32_tensors_low_precision_weights(name, shape):
     rows = C.sample_rows(cfg.N, 256) if cfg.N > 4096 else np.arange(cfg.N)
     yref = ref["y"] if ref["y"] is not None else O.tokens(inp, ref["idx"], ref["topp"], rows)
     check_close(y[rows], yref if ref["y"] is None else yref[rows], TOL[cfg.weights], name)
+
+
+# fp8 decode steps whose gate/up GEMM reads the caller's rows itself (no
+# permute): the cfg5 shape at the 512-id limit, a ragged one and one with
+# C = 2048 (several K stages).
+GATHERED = [
+    (64, 1024, 64, 8, 256),
+    (37, 512, 40, 4, 320),
+    (16, 2048, 32, 2, 128),
+]
+
+
+@pytest.mark.parametrize("shape", GATHERED)
+def test_f32_rows_gathered_like_bf16_rows(shape):
+    """The same bf16-representable rows as fp32 and as bf16 tensors: the
+    fp32 step routes identically and its outputs, rounded to bf16, equal the
+    bf16 step's bit for bit (the gathered fp32 rows are rounded to the same
+    bf16 products the bf16 rows hold); both within the fp8 bar of the
+    oracle."""
+    N, Cm, E, k, H = shape
+    inp = make_case("gath", N, Cm, E, k, H, "bf16", "fp8")
+    print(f"case {inp.cfg}", flush=True)
+    y16, r16 = forward(layer_for(inp), inp)
+    cfg32 = dataclasses.replace(inp.cfg, name="gath_f32io", act="f32")
+    inp32 = dataclasses.replace(inp, cfg=cfg32)
+    y32, r32 = forward(layer_for(inp32), inp32)
+    for key in r16:
+        np.testing.assert_array_equal(r32[key], r16[key], err_msg=key)
+    y32b = torch.from_numpy(y32).bfloat16().float().numpy()
+    np.testing.assert_array_equal(y32b, y16)
+    ref = O.forward(inp32, with_y=True)
+    check_routing(r32, ref)
+    check_close(y32, ref["y"], TOL["fp8"], "gath_f32io")
+
+
+def test_f32_rows_rounded_to_nearest_even():
+    """Every fp32 element sits a quarter, half or three quarters of a bf16
+    step above a bf16 value (or one unit either side of the half).  With a
+    zero router weight both steps route on the bias alone, so the fp32 step
+    and the bf16 step on the host's nearest-even rounding of the rows
+    (ties to even) agree bit for bit only if the decode GEMM rounds the
+    gathered fp32 rows the same way; truncation or ties away from zero
+    would move about half of the elements by one step."""
+    N, Cm, E, k, H = 64, 1024, 64, 8, 256
+    inp = make_case("rne", N, Cm, E, k, H, "f32", "fp8")
+    inp.Wr[:] = 0.0
+    rng = np.random.default_rng(11)
+    hi = wl.bf16_round(inp.x).view(np.uint32) & np.uint32(0xFFFF0000)
+    lo = rng.choice(np.array([0x4000, 0x8000, 0x8000, 0xC000, 0x7FFF, 0x8001], np.uint32),
+                    size=hi.shape)
+    inp.x[:] = (hi | lo).view(np.float32)
+    print(f"case {inp.cfg}", flush=True)
+    y32, r32 = forward(layer_for(inp), inp)
+    cfg16 = dataclasses.replace(inp.cfg, name="rne_bf16", act="bf16")
+    inp16 = dataclasses.replace(inp, cfg=cfg16, x=wl.bf16_round(inp.x))
+    y16, r16 = forward(layer_for(inp16), inp16)
+    for key in r16:
+        np.testing.assert_array_equal(r32[key], r16[key], err_msg=key)
+    y32b = torch.from_numpy(y32).bfloat16().float().numpy()
+    np.testing.assert_array_equal(y32b, y16)
 
 
 def test_f32_tensors_low_precision_weights_do_not_train():
