@@ -232,9 +232,9 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
  * in ms over the recorded forwards: [0] router+top-k+histogram, [1] dispatch
  * (count scan + permutation), [2] gate/up GEMM + SwiGLU, [3] down GEMM,
  * [4] combine; if n > 5, ms[5] receives the number of forwards averaged.
- * (Decode steps of at most 512 flat ids with bf16 rows and fp8 weights route
- * inside the gate/up GEMM: [1] is then only the gap between two events and
- * [2] includes the routing.)
+ * (Inference steps with fp8 weights, no gamma, bf16 or fp32 rows and at most
+ * 512 flat ids N*k, below 64*E, route inside the gate/up GEMM: [1] is then
+ * only the gap between two events and [2] includes the routing.)
  * enable: 0 off, 1 every stage boundary, 2 only the two boundaries of the
  * gate/up GEMM (the other launches keep their spacing; stage_times then
  * returns -1 for the other stages).  The backward records its stages
