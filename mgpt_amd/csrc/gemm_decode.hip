@@ -33,7 +33,7 @@ constexpr int kDBK = 128;                    // columns per stage
 #ifndef MGPT_DECODE_STAGES
 #define MGPT_DECODE_STAGES 3
 #endif
-constexpr int kDStages = MGPT_DECODE_STAGES;   // ring depth (LDS: 40 KB a stage)
+constexpr int kDStages = MGPT_DECODE_STAGES;   // ring depth (LDS: 40 KB a stage, 48 KB for fp32 rows)
 constexpr int kWBytes = kDBN * kDBK;         // 32 KB of fp8 weights
 constexpr int kDmaW = kWBytes / 1024 / 4;    // 8 weight blocks per wave
 
@@ -212,6 +212,8 @@ __global__ __launch_bounds__(kDThreads) void gemm_decode_kernel(
   constexpr int kRowsPerBlk = 1024 / kRowB;
   constexpr int kChunks = kRowB / 16;          // 16-byte chunks per row
   static_assert(kXS == 2 || kXS == 4, "bf16 or fp32 rows");
+  static_assert(kDStages * kStage + kGatherFlat * 4 <= 160 * 1024,
+                "the ring does not fit in LDS at this MGPT_DECODE_STAGES");
   __shared__ __attribute__((aligned(1024))) char smem[kDStages * kStage];
   __shared__ int s_tok[GATHER ? kGatherFlat : 1];
   __shared__ int s_cnt[GATHER ? kMaxExperts : 1], s_base[GATHER ? kMaxExperts : 1],
