@@ -197,12 +197,14 @@ def test_f32_tensors_low_precision_weights(name, shape):
 
 
 # fp8 decode steps whose gate/up GEMM reads the caller's rows itself (no
-# permute): the cfg5 shape at the 512-id limit, a ragged one and one with
-# C = 2048 (several K stages).
+# permute): the cfg5 shape at the 512-id limit, a ragged one, one with
+# C = 2048 (several K stages) and one whose rows are zero-padded from C = 200
+# to 256 before the GEMM reads them.
 GATHERED = [
     (64, 1024, 64, 8, 256),
     (37, 512, 40, 4, 320),
     (16, 2048, 32, 2, 128),
+    (24, 200, 16, 4, 192),
 ]
 
 
