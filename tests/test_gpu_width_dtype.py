@@ -231,6 +231,28 @@ def test_f32_rows_gathered_like_bf16_rows(shape):
     check_close(y32, ref["y"], TOL["fp8"], "gath_f32io")
 
 
+def test_f32_rows_gathered_nonfinite_stay_in_their_token():
+    """A NaN and an infinity in two fp32 rows of a permute-free decode step:
+    the fp32 step still matches the bf16 step on the same rows bit for bit
+    (NaN where the bf16 step has NaN), and every other token's output is
+    finite, so the gathered rows (and the padding rows of a tile, which
+    re-read a segment's last token) reach no other token's output."""
+    N, Cm, E, k, H = 64, 1024, 64, 8, 256
+    inp = make_case("nonfin", N, Cm, E, k, H, "bf16", "fp8")
+    inp.x[5, 17] = np.nan
+    inp.x[9, 3] = np.inf
+    print(f"case {inp.cfg}", flush=True)
+    y16, r16 = forward(layer_for(inp), inp)
+    inp32 = dataclasses.replace(inp, cfg=dataclasses.replace(inp.cfg, name="nonfin_f32io",
+                                                              act="f32"))
+    y32, r32 = forward(layer_for(inp32), inp32)
+    for key in r16:
+        np.testing.assert_array_equal(r32[key], r16[key], err_msg=key)
+    np.testing.assert_array_equal(torch.from_numpy(y32).bfloat16().float().numpy(), y16)
+    others = np.setdiff1d(np.arange(N), [5, 9])
+    assert np.isfinite(y32[others]).all()
+
+
 def test_f32_rows_rounded_to_nearest_even():
     """Every fp32 element sits a quarter, half or three quarters of a bf16
     step above a bf16 value (or one unit either side of the half).  With a
