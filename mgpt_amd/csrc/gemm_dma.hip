@@ -31,6 +31,8 @@
 //    together (16 rows of one logical chunk) hit 16 distinct bank groups.
 //  * SwiGLU in the epilogue uses the hardware exp/reciprocal (well inside
 //    the bf16 tolerance).
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace mgpt {
@@ -200,12 +202,10 @@ __device__ __forceinline__ void store_group32(bf16_t* base, const uint2 (&q)[4],
 // token column lane%32.  Biases are read at wave-uniform addresses (scalar
 // loads): a vector load here would make the compiler wait for the DMA loads
 // it does not track as well.
-template <int EPI, int NW>
+template <int EPI, int NW, bool kSave>
 __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Waves<NW>::TM],
                                            const Tile& cur, int wn, int wm, int lrow, int lhalf,
-                                           const float* __restrict__ bias0,
-                                           const float* __restrict__ bias1, int n_store,
-                                           int bias_ld, bf16_t* out, int ldo, bf16_t* save,
+                                           int n_store, bf16_t* out, int ldo, bf16_t* save,
                                            int save_ld) {
   using W = Waves<NW>;
   const int tok_base = cur.row0 + wm * W::WTM + lrow;
@@ -214,18 +214,6 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
 #pragma unroll
     for (int gi = 0; gi < W::TN / 2; ++gi) {
       const int hb = (cur.n0 + wn * W::WTN) / 2 + 32 * gi;
-      const float* bgp = bias0 + (size_t)cur.expert * bias_ld + hb;
-      const float* bup = bias1 + (size_t)cur.expert * bias_ld + hb;
-      float bg[16], bu[16];
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float g0 = uniform_load(bgp + 8 * g + q), g1 = uniform_load(bgp + 8 * g + 4 + q);
-          const float u0 = uniform_load(bup + 8 * g + q), u1 = uniform_load(bup + 8 * g + 4 + q);
-          bg[4 * g + q] = lhalf ? g1 : g0;
-          bu[4 * g + q] = lhalf ? u1 : u0;
-        }
 #pragma unroll
       for (int i = 0; i < W::TM; ++i) {
         const int row = tok_base + i * 32;
@@ -235,23 +223,19 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int v = 4 * g;
-          q[g] = pack4_bf16(silu_mul_fast(ga[v + 0] + bg[v + 0], ua[v + 0] + bu[v + 0]),
-                            silu_mul_fast(ga[v + 1] + bg[v + 1], ua[v + 1] + bu[v + 1]),
-                            silu_mul_fast(ga[v + 2] + bg[v + 2], ua[v + 2] + bu[v + 2]),
-                            silu_mul_fast(ga[v + 3] + bg[v + 3], ua[v + 3] + bu[v + 3]));
+          q[g] = pack4_bf16(silu_mul_fast(ga[v + 0], ua[v + 0]), silu_mul_fast(ga[v + 1], ua[v + 1]),
+                            silu_mul_fast(ga[v + 2], ua[v + 2]), silu_mul_fast(ga[v + 3], ua[v + 3]));
         }
         store_group32(out + (size_t)row * ldo + hb, q, lhalf, row < cur.row_end);
-        if (save) {
+        if constexpr (kSave) {
           // pre-activations for the backward pass, in the packed column order
           const int pc = cur.n0 + wn * W::WTN + 64 * gi;
           uint2 sg[4], su[4];
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const int v = 4 * g;
-            sg[g] = pack4_bf16(ga[v] + bg[v], ga[v + 1] + bg[v + 1], ga[v + 2] + bg[v + 2],
-                               ga[v + 3] + bg[v + 3]);
-            su[g] = pack4_bf16(ua[v] + bu[v], ua[v + 1] + bu[v + 1], ua[v + 2] + bu[v + 2],
-                               ua[v + 3] + bu[v + 3]);
+            sg[g] = pack4_bf16(ga[v], ga[v + 1], ga[v + 2], ga[v + 3]);
+            su[g] = pack4_bf16(ua[v], ua[v + 1], ua[v + 2], ua[v + 3]);
           }
           store_group32(save + (size_t)row * save_ld + pc, sg, lhalf, row < cur.row_end);
           store_group32(save + (size_t)row * save_ld + pc + 32, su, lhalf, row < cur.row_end);
@@ -322,20 +306,6 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
     for (int j = 0; j < W::TN; ++j) {
       const int cb = cur.n0 + wn * W::WTN + j * 32;
       if (cb >= n_store) continue;   // n_store is a multiple of 64
-      float b[16];
-      if (bias0) {
-        const float* bdp = bias0 + (size_t)cur.expert * bias_ld + cb;
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float b0 = uniform_load(bdp + 8 * g + q), b1 = uniform_load(bdp + 8 * g + 4 + q);
-            b[4 * g + q] = lhalf ? b1 : b0;
-          }
-      } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) b[v] = 0.0f;
-      }
 #pragma unroll
       for (int i = 0; i < W::TM; ++i) {
         const int row = tok_base + i * 32;
@@ -343,8 +313,7 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
         uint2 q[4];
 #pragma unroll
         for (int g = 0; g < 4; ++g)
-          q[g] = pack4_bf16(a[4 * g + 0] + b[4 * g + 0], a[4 * g + 1] + b[4 * g + 1],
-                            a[4 * g + 2] + b[4 * g + 2], a[4 * g + 3] + b[4 * g + 3]);
+          q[g] = pack4_bf16(a[4 * g + 0], a[4 * g + 1], a[4 * g + 2], a[4 * g + 3]);
         store_group32(out + (size_t)row * ldo + cb, q, lhalf, row < cur.row_end);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -404,6 +373,52 @@ __device__ __forceinline__ bool locate_work(const SegScan& sc, const SplitPlan& 
   return locate_tile(sc, E, nbx, tv, &wk->tile);
 }
 
+// The accumulators of a work item start from the biases of its features
+// (the same for every token), or from zero for split-K parts (the reduce
+// kernel adds the bias), the SwiGLU backward and a down product without
+// bias.  Register v of a 32x32 tile holds feature 8*(v/4) + 4*(lane/32) +
+// v%4.  The biases are read at wave-uniform addresses (scalar loads): a
+// vector load would make the compiler wait for the ring's DMA loads, which
+// it does not track, as well.
+template <int EPI, int NW>
+__device__ __forceinline__ void init_acc(f32x16 (&acc)[Waves<NW>::TN][Waves<NW>::TM],
+                                         const Work& wk, int wn, int lhalf,
+                                         const float* __restrict__ bias0,
+                                         const float* __restrict__ bias1, int bias_ld) {
+  using W = Waves<NW>;
+  const bool has_bias = EPI != kEpiSwigluBwd && wk.sidx < 0 && bias0 != nullptr;
+#pragma unroll
+  for (int j = 0; j < W::TN; ++j) {
+    f32x16 b;
+    if (has_bias) {
+      const float* src;
+      if constexpr (EPI == kEpiGateUp) {
+        // packed rows: each 64 of them are [32 gate | 32 up] of hidden units hb..hb+31
+        const int hb = (wk.tile.n0 + wn * W::WTN) / 2 + 32 * (j / 2);
+        src = ((j & 1) ? bias1 : bias0) + (size_t)wk.tile.expert * bias_ld + hb;
+      } else {
+        src = bias0 + (size_t)wk.tile.expert * bias_ld + wk.tile.n0 + wn * W::WTN + 32 * j;
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 v = *reinterpret_cast<const float4*>(src + 8 * g + 4 * lhalf);
+        b[4 * g] = v.x;
+        b[4 * g + 1] = v.y;
+        b[4 * g + 2] = v.z;
+        b[4 * g + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) b[v] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < W::TM; ++i) acc[j][i] = b;
+    // one feature group at a time: keeps the scheduler from hoisting all
+    // TN * 32 scalar loads together (SGPR pressure)
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Partial sums of one work item, a whole 256 x 256 fp32 tile, stored as
 // [TN*TM*4 float4 slots q][threads] so that every store and load is a
 // coalesced row.  q = (j * kTM + i) * 4 + v4 holds acc[j][i][4v4 ..].
@@ -417,7 +432,7 @@ constexpr int kPartialFloats = 256 * 256;
 // and refills them with units 2s+3 (weights of slab s+1) and 2s+4
 // (activations of slab s+2): the activations are requested two slabs ahead
 // and the weights one (a 2-stage ring of 64 KB slabs manages one for both).
-template <int EPI, int NW>
+template <int EPI, int NW, bool kSave>
 __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
     const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
@@ -557,12 +572,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     Work nxt;
     const bool have_next = locate_work(sc, plan, E, nbx, KT, t + G, &nxt);
     f32x16 acc[kTN][kTM];
-#pragma unroll
-    for (int j = 0; j < kTN; ++j)
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[j][i][v] = 0.0f;
+    init_acc<EPI, NW>(acc, cur, wn, lhalf, bias0, bias1, bias_ld);
 
     // The k loop for MT live 32-token sub-tiles of this wave (the rest of
     // its 128 tokens lie past the segment: their MFMAs would only multiply
@@ -616,8 +626,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     }
     mfma_drain<NW>();
     if (cur.sidx < 0) {
-      store_tile<EPI, NW>(acc, cur.tile, wn, wm, lrow, lhalf, bias0, bias1, n_store, bias_ld, out,
-                          ldo, save, save_ld);
+      store_tile<EPI, NW, kSave>(acc, cur.tile, wn, wm, lrow, lhalf, n_store, out, ldo, save,
+                                 save_ld);
     } else {
       float4* P = reinterpret_cast<float4*>(partials + (size_t)cur.sidx * kPartialFloats) + tid;
 #pragma unroll
@@ -754,12 +764,28 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                (reinterpret_cast<uintptr_t>(save) & 15) != 0))
     return hipErrorInvalidValue;
   if (EPI == kEpiSwigluBwd && !save) return hipErrorInvalidValue;
+  // the accumulators start from the biases, read as 16-byte vectors
+  if (((reinterpret_cast<uintptr_t>(bias0) | reinterpret_cast<uintptr_t>(bias1)) & 15) != 0 ||
+      bias_ld % 4 != 0)
+    return hipErrorInvalidValue;
   if (K / 64 < kMinSplitSlabs) partials = nullptr;   // no split, no reduce launch
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
-  hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves>), dim3(grid), dim3(kRingWaves * kWave), 0,
-                     stream, A, B, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out, ldo,
-                     partials, save, save_ld);
+  // the gate/up epilogue's pre-activation stores are compiled only into
+  // the training instance (fewer live registers in the inference one)
+  auto launch = [&](auto save_c) {
+    hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves, decltype(save_c)::value>), dim3(grid),
+                       dim3(kRingWaves * kWave), 0, stream, A, B, bias0, bias1, counts, E, K, Npad,
+                       n_store, bias_ld, out, ldo, partials, save, save_ld);
+  };
+  if constexpr (EPI == kEpiGateUp) {
+    if (save)
+      launch(std::true_type{});
+    else
+      launch(std::false_type{});
+  } else {
+    launch(std::false_type{});
+  }
   if constexpr (EPI != kEpiSwigluBwd) {
     if (partials)
       hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256), 0,
