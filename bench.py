@@ -295,10 +295,16 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
                 f"device, enqueued by the host in {b['growing_phase_host_enqueue_ms']} ms; "
                 f"{rf['kernel']}: {rf['achieved']} GB/s = {100 * rf['frac']:.1f}% of "
                 f"{rf['peak']} GB/s."]
+    elif rf["unit"] == "GB/s":
+        # weight-streaming decode shapes: an HBM roofline
+        out += ["", f"bench.py: {b['value']:.0f} tokens/s, {b['ms_per_step']} ms/step; "
+                f"{rf['kernel']}: {rf['achieved']} GB/s of weights = {100 * rf['frac']:.1f}% of "
+                f"{rf['peak']} GB/s HBM; both expert GEMMs {b['expert_gemm_tflops']} TFLOP/s."]
     else:
         out += ["", f"bench.py: {b['value']:.0f} tokens/s, {b['ms_per_step']} ms/step; gate/up GEMM "
                 f"{rf['achieved']} TFLOP/s = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s dense "
-                f"bf16; both expert GEMMs {b['expert_gemm_tflops']} TFLOP/s."]
+                f"{'fp32' if rf['peak'] == PEAK_F32_TFLOPS else 'bf16'}; both expert GEMMs "
+                f"{b['expert_gemm_tflops']} TFLOP/s."]
         if mode == "block":
             out += [f"Unfused (torch RMSNorm, the layer forward, torch add) on the same inputs: "
                     f"{b['unfused_ms_per_step']} ms/step."]
@@ -520,9 +526,15 @@ def main() -> int:
         "expert_gemm_mfma_frac": round(gemm_tflops / peak_mm, 4),
         "stage_ms": {kk: round(v, 4) for kk, v in stages.items()},
         "stage_ms_forwards_averaged": n_prof,
-        "hbm_frac": {kk.replace("_GBs", ""): round(v / PEAK_HBM_GBS, 4) for kk, v in hbm.items()},
-        "hbm_frac_moved_bytes": {kk: round(v / (stages[kk] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
-                                 for kk, v in moved.items()},
+        # achieved HBM bandwidth over peak, by the bytes each kernel must move
+        "hbm_frac": {kk: round(v / (stages[kk] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)
+                     for kk, v in moved.items()},
+        # the per-unit byte formulas of the scope table (router N*C*a + C*E*4 + 8A,
+        # permute 2*A*C*a + 8A, combine A*C*a + N*C*a + 8A) over the stage time and
+        # HBM peak: the permute's formula counts k reads of each row, which the
+        # kernel does not make, so this is a ratio, not a bandwidth
+        "formula_bytes_ratio": {kk.replace("_GBs", ""): round(v / PEAK_HBM_GBS, 4)
+                                for kk, v in hbm.items()},
         "expert_counts_max_over_mean": round(max(counts) / (sum(counts) / len(counts)), 3),
         "roofline": ({
             "kernel": "gate/up fp8 weight-streaming GEMM + SwiGLU epilogue",
