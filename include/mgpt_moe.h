@@ -82,7 +82,12 @@ int mgpt_moe_destroy(mgpt_moe* h);
  * The library copies and packs them (transposed tiles; bf16 rounding or
  * per-output-channel e4m3 quantisation for the expert weights; the router
  * stays fp32).  Replaces Layer::to(Device::CUDA) (layers/Layer.h:46-51) for
- * this layer.  Synchronous with respect to `stream`'s prior work. */
+ * this layer.  The first load allocates the packed buffers and returns once
+ * the packs are done; later loads re-pack into the same buffers.  Host
+ * parameters are always waited for (they are staged through one device
+ * buffer); a re-pack of device parameters is stream-ordered on `stream`,
+ * with no allocation and no host wait (a training loop re-packs after every
+ * optimizer step). */
 int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params,
                              int num_params, int params_on_device, void* stream);
 
@@ -191,15 +196,22 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens,
  * Experts no token chose get no gradient, as in the reference.  x, dy, dx
  * are act_dtype, device memory; dx must not overlap x or dy.  The workspace
  * is consumed (a second backward needs a new training forward).  Replaces
- * MoELayer::backward_into (layers/MoELayer.cpp:130-223) on the device. */
+ * MoELayer::backward_into (layers/MoELayer.cpp:130-223) on the device.
+ * Under HIP graph capture the backward always adds into the gradients (a
+ * graph replays the mode it was captured in): zeros still pending from an
+ * eager mgpt_moe_zero_grad are written into the graph first, so each replay
+ * of a graph captured right after zero_grad starts from zero. */
 int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
                       void* workspace, size_t workspace_bytes, void* stream);
 
 /* Sets every gradient to zero on `stream`.  Replaces Tensor::zero_grad
- * (utils/Tensor.cpp:181-187) over this layer's parameters.  No memory is
- * written: the gradients are marked zero, the next mgpt_moe_backward stores
- * them instead of adding, and a read before that (get / accumulate) clears
- * the buffer first. */
+ * (utils/Tensor.cpp:181-187) over this layer's parameters.  Eagerly, before
+ * any backward has been captured, no memory is written: the gradients are
+ * marked zero on the host, the next mgpt_moe_backward stores them instead of
+ * adding, and a read before that (get / accumulate) clears the buffer first.
+ * On a capturing stream, or once a backward has been captured into a graph
+ * (whose replays add), it enqueues a fill kernel on `stream` that clears the
+ * gradients, so zero_grad between graph replays takes effect. */
 int mgpt_moe_zero_grad(mgpt_moe* h, void* stream);
 
 /* Copies the 2 + 6E fp32 gradients to grads[i] in get_parameters() order
@@ -232,9 +244,12 @@ int mgpt_moe_expert_counts(mgpt_moe* h, int32_t* host_counts, int num_experts);
  * in ms over the recorded forwards: [0] router+top-k+histogram, [1] dispatch
  * (count scan + permutation), [2] gate/up GEMM + SwiGLU, [3] down GEMM,
  * [4] combine; if n > 5, ms[5] receives the number of forwards averaged.
- * (Inference steps with fp8 weights, no gamma, bf16 or fp32 rows and at most
- * 512 flat ids N*k, below 64*E, route inside the gate/up GEMM: [1] is then
- * only the gap between two events and [2] includes the routing.)
+ * (Inference steps with fp8 weights, no gamma, bf16 or fp32 rows, an
+ * embed_dim padded to a multiple of 128 (its tiled weight copy exists only
+ * then) and at most 512 flat ids N*k, below 64*E, route inside the gate/up
+ * GEMM: [1] is then only the gap between two events and [2] includes the
+ * routing.  Other decode steps run the permute and split their stages as
+ * usual.)
  * enable: 0 off, 1 every stage boundary, 2 only the two boundaries of the
  * gate/up GEMM (the other launches keep their spacing; stage_times then
  * returns -1 for the other stages).  The backward records its stages

@@ -90,6 +90,7 @@ hipError_t launch_wgrad(const T*, int, int, const T*, int, int, const int32_t*, 
                         float*, int, size_t, int, int, float*, float*, size_t, int, float*,
                         size_t, float*, size_t, int, bool, hipStream_t);
 hipError_t launch_zero_idle_experts(const int32_t*, int, const IdleSlices&, hipStream_t);
+hipError_t launch_fill_zero(float* p, size_t n, hipStream_t stream);
 hipError_t launch_tile_fp8(const uint8_t*, int, int, int, uint8_t*, hipStream_t);
 template <int EPI>
 hipError_t launch_gemm_decode(const bf16_t*, const fp8_t*, const float*, const float*,
@@ -161,7 +162,8 @@ std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
 // Device address of `scratch` on `device`, looked up once per device with
-// that device current.
+// that device current (mgpt_moe_create does it for the handle's device, so
+// the noalloc forward only reads the cached address).
 int scratch_address(int device, void** out) {
   if (device < 0 || device >= kMaxDevices)
     return fail(MGPT_ERR_UNSUPPORTED, "device %d beyond the %d the library tracks", device,
@@ -212,6 +214,10 @@ struct mgpt_moe {
   float* bg = nullptr;     // [E][Hp]
   float* bu = nullptr;     // [E][Hp]
   float* bd = nullptr;     // [E][Cp]
+  // staging of host parameters (one of the largest size) and, for fp8, the
+  // packed fp32 rows before quantisation; kept for later loads
+  float* stage = nullptr;
+  float* stage_tmp = nullptr;
   bool loaded = false;
   // Backward: the weights in the layouts the data-gradient products read,
   // derived from the forward packs on the first backward after a load
@@ -230,6 +236,10 @@ struct mgpt_moe {
   // zero_grad and at allocation): the next backward writes every gradient
   // instead of adding to it, and a read clears the buffer first.
   bool grad_zero = false;
+  // Set once a backward has been captured into a HIP graph: a graph keeps
+  // the add mode it was captured in, so zero_grad then clears the buffer
+  // (stream-ordered) instead of only marking it.
+  bool bwd_captured = false;
   // Profiling ring: forward i records its stage boundaries into slot
   // i % kProfSlots; stage_times averages over the recorded slots.
   static constexpr int kProfSlots = 64;
@@ -342,11 +352,12 @@ int check_config(const mgpt_moe_config* c) {
 }
 
 void free_weights(mgpt_moe* h) {
-  void* ptrs[] = {h->wr_g, h->wr1, h->wr4, h->br,  h->wgu,  h->wd,   h->sgu,  h->sd,
-                  h->bg,   h->bu,  h->bd,  h->wdb, h->wgub, h->wrt, h->wgu_t, h->wd_t};
+  void* ptrs[] = {h->wr_g, h->wr1, h->wr4,  h->br,  h->wgu,  h->wd,    h->sgu,  h->sd,    h->bg,
+                  h->bu,   h->bd,  h->wdb,  h->wgub, h->wrt, h->wgu_t, h->wd_t, h->stage, h->stage_tmp};
   for (void* p : ptrs)
     if (p) (void)hipFree(p);
   h->wr_g = h->wr1 = h->wr4 = h->br = h->sgu = h->sd = h->bg = h->bu = h->bd = h->wrt = nullptr;
+  h->stage = h->stage_tmp = nullptr;
   h->wgu = h->wd = h->wdb = h->wgub = h->wgu_t = h->wd_t = nullptr;
   h->loaded = false;
   h->bwd_ready = false;
@@ -378,7 +389,7 @@ int ensure_grad(mgpt_moe* h) {
 int materialize_grad(mgpt_moe* h, hipStream_t st) {
   if (int rc = ensure_grad(h)) return rc;
   if (h->grad_zero) {
-    HIP_TRY(hipMemsetAsync(h->grad, 0, sizeof(float) * h->g_total, st));
+    HIP_TRY(launch_fill_zero(h->grad, h->g_total, st));
     h->grad_zero = false;
   }
   return MGPT_OK;
@@ -463,6 +474,14 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
     mgpt_moe_destroy(h);
     return fail(MGPT_ERR_HIP, "device setup failed: %s", hipGetErrorString(e));
   }
+  // The noalloc forward's scratch address on this device, looked up here
+  // (once per device) so that a later mgpt_moe_forward_noalloc, possibly
+  // under graph capture, makes no runtime call to find it.
+  void* scratch_ptr = nullptr;
+  if (int rc2 = scratch_address(h->device, &scratch_ptr)) {
+    mgpt_moe_destroy(h);
+    return rc2;
+  }
   *out = h;
   return MGPT_OK;
 }
@@ -492,43 +511,45 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
     if (!params[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "parameter %d is null", i);
   hipStream_t st = (hipStream_t)stream_ptr;
   HIP_TRY(hipSetDevice(h->device));
-  free_weights(h);
   const int C = h->C, Cx = h->Cx, H = h->H, E = h->E, Hp = h->Hp, Cp = h->Cp;
   const size_t wb = h->w_bytes();
   const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
   const bool bf = h->wdt == MGPT_DTYPE_BF16;
   const int RE = router_experts_per_wave(E);
-  HIP_TRY(hipMalloc(&h->wr_g, sizeof(float) * ((E + RE - 1) / RE) * RE * C));
-  if (E > 16) HIP_TRY(hipMalloc(&h->wr1, sizeof(float) * E * C));
-  if (E > 16 && C % 64 == 0 && C <= kDecodeRouterMaxC)
-    HIP_TRY(hipMalloc(&h->wr4, sizeof(float) * E * C));
-  HIP_TRY(hipMalloc(&h->br, sizeof(float) * E));
-  HIP_TRY(hipMalloc(&h->wgu, wb * E * 2 * Hp * C));
-  HIP_TRY(hipMalloc(&h->wd, wb * E * Cp * Hp));
-  HIP_TRY(hipMalloc(&h->bg, sizeof(float) * E * Hp));
-  HIP_TRY(hipMalloc(&h->bu, sizeof(float) * E * Hp));
-  HIP_TRY(hipMalloc(&h->bd, sizeof(float) * E * Cp));
-  if (fp8) {
-    HIP_TRY(hipMalloc(&h->sgu, sizeof(float) * E * 2 * Hp));
-    HIP_TRY(hipMalloc(&h->sd, sizeof(float) * E * Cp));
+  // The packed buffers depend only on the handle's shape: the first load
+  // allocates them (and zeroes the padding the packs never write), later
+  // loads re-pack into them, stream-ordered, with no allocation.  The
+  // backward's transposed copies are rebuilt from the new packs.
+  h->loaded = false;
+  h->bwd_ready = false;
+  const bool first = h->wgu == nullptr;
+  if (first) {
+    HIP_TRY(hipMalloc(&h->wr_g, sizeof(float) * ((E + RE - 1) / RE) * RE * C));
+    if (E > 16) HIP_TRY(hipMalloc(&h->wr1, sizeof(float) * E * C));
+    if (E > 16 && C % 64 == 0 && C <= kDecodeRouterMaxC)
+      HIP_TRY(hipMalloc(&h->wr4, sizeof(float) * E * C));
+    HIP_TRY(hipMalloc(&h->br, sizeof(float) * E));
+    HIP_TRY(hipMalloc(&h->bg, sizeof(float) * E * Hp));
+    HIP_TRY(hipMalloc(&h->bu, sizeof(float) * E * Hp));
+    HIP_TRY(hipMalloc(&h->bd, sizeof(float) * E * Cp));
+    if (fp8) {
+      HIP_TRY(hipMalloc(&h->sgu, sizeof(float) * E * 2 * Hp));
+      HIP_TRY(hipMalloc(&h->sd, sizeof(float) * E * Cp));
+    }
+    HIP_TRY(hipMalloc(&h->wd, wb * E * Cp * Hp));
+    HIP_TRY(hipMemsetAsync(h->wd, 0, wb * E * Cp * Hp, st));
+    HIP_TRY(hipMalloc(&h->wgu, wb * E * 2 * Hp * C));
+    HIP_TRY(hipMemsetAsync(h->wgu, 0, wb * E * 2 * Hp * C, st));
   }
-  HIP_TRY(hipMemsetAsync(h->wgu, 0, wb * E * 2 * Hp * C, st));
-  HIP_TRY(hipMemsetAsync(h->wd, 0, wb * E * Cp * Hp, st));
 
   // Host parameters are staged through one device buffer of the largest size.
-  struct DevBuf {
-    float* p = nullptr;
-    ~DevBuf() {
-      if (p) (void)hipFree(p);
-    }
-  } stage_buf, tmp_buf;
   const size_t max_elems = std::max<size_t>((size_t)Cx * std::max(H, E), (size_t)H * Cx);
-  HIP_TRY(hipMalloc(&stage_buf.p, sizeof(float) * max_elems));
-  if (fp8)
-    HIP_TRY(hipMalloc(&tmp_buf.p,
+  if (!params_on_device && !h->stage) HIP_TRY(hipMalloc(&h->stage, sizeof(float) * max_elems));
+  if (fp8 && !h->stage_tmp)
+    HIP_TRY(hipMalloc(&h->stage_tmp,
                       sizeof(float) * std::max<size_t>((size_t)2 * Hp * C, (size_t)Cp * Hp)));
-  float* stage = stage_buf.p;
-  float* fp32tmp = tmp_buf.p;   // fp8: packed fp32 before quantisation
+  float* stage = h->stage;
+  float* fp32tmp = h->stage_tmp;   // fp8: packed fp32 before quantisation
   int rc = MGPT_OK;
   auto src = [&](int i, size_t n) -> const float* {
     if (params_on_device) return params[i];
@@ -598,20 +619,25 @@ int mgpt_moe_load_parameters(mgpt_moe* h, const float* const* params, int num_pa
     }
     if (rc == MGPT_OK && fp8 && C % 128 == 0 && Hp % 128 == 0 && Cp % 256 == 0) {
       // the decode stream's contiguous 32 KB stage tiles (a second copy)
-      HIP_TRY(hipMalloc(&h->wgu_t, (size_t)E * 2 * Hp * C));
-      HIP_TRY(hipMalloc(&h->wd_t, (size_t)E * Cp * Hp));
+      if (!h->wgu_t) HIP_TRY(hipMalloc(&h->wgu_t, (size_t)E * 2 * Hp * C));
+      if (!h->wd_t) HIP_TRY(hipMalloc(&h->wd_t, (size_t)E * Cp * Hp));
       HIP_TRY(launch_tile_fp8((const uint8_t*)h->wgu, E, 2 * Hp, C, (uint8_t*)h->wgu_t, st));
       HIP_TRY(launch_tile_fp8((const uint8_t*)h->wd, E, Cp, Hp, (uint8_t*)h->wd_t, st));
     }
   } while (0);
-  hipError_t se = hipStreamSynchronize(st);
   if (rc) {
+    (void)hipStreamSynchronize(st);
     free_weights(h);
     return rc;
   }
-  if (se != hipSuccess) {
-    free_weights(h);
-    return fail(MGPT_ERR_HIP, "parameter packing failed: %s", hipGetErrorString(se));
+  // A first load (new allocations) and host sources finish before the call
+  // returns; a re-pack of device parameters stays stream-ordered.
+  if (first || !params_on_device) {
+    const hipError_t se = hipStreamSynchronize(st);
+    if (se != hipSuccess) {
+      free_weights(h);
+      return fail(MGPT_ERR_HIP, "parameter packing failed: %s", hipGetErrorString(se));
+    }
   }
   h->loaded = true;
   return MGPT_OK;
@@ -869,7 +895,10 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   float* g = h->grad;
   const ActT* wdb = (const ActT*)h->wdb;
   const ActT* wgub = (const ActT*)h->wgub;
-  const bool prof = h->profiling && !h->prof_gemm_only;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(st, &cap));
+  // no stage events inside a captured graph (as in the forward)
+  const bool prof = h->profiling && !h->prof_gemm_only && cap == hipStreamCaptureStatusNone;
   hipEvent_t* evs = h->evb[h->prof_b_count % mgpt_moe::kProfSlots];
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
@@ -1132,6 +1161,15 @@ int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int 
     return fail(MGPT_ERR_INVALID_ARGUMENT, "dx must not overlap x or dy");
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(st, &cap));
+  if (cap != hipStreamCaptureStatusNone) {
+    // A graph replays the mode it was captured in, so a captured backward
+    // always adds: zeros still pending from zero_grad are written first
+    // (into the graph), and later zero_grads clear the buffer on the stream.
+    if (int rc = materialize_grad(h, st)) return rc;
+    h->bwd_captured = true;
+  }
   if (h->act == MGPT_DTYPE_BF16)
     return backward_impl<bf16_t>(h, (const bf16_t*)x, (const bf16_t*)dy, (bf16_t*)dx,
                                  num_tokens, (char*)workspace, st);
@@ -1144,8 +1182,18 @@ int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
   if (!trainable(h))
     return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   HIP_TRY(hipSetDevice(h->device));
-  (void)stream;   // nothing is enqueued: the next backward stores instead of adding
   if (int rc = ensure_grad(h)) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(st, &cap));
+  if (cap != hipStreamCaptureStatusNone || h->bwd_captured) {
+    // under capture, or once a captured (adding) backward exists: clear the
+    // buffer on the stream, a fill kernel (graph-safe)
+    HIP_TRY(launch_fill_zero(h->grad, h->g_total, st));
+    h->grad_zero = false;
+    return MGPT_OK;
+  }
+  // eager: nothing is enqueued, the next backward stores instead of adding
   h->grad_zero = true;
   return MGPT_OK;
 }
@@ -1192,17 +1240,25 @@ int mgpt_moe_accumulate_gradients(mgpt_moe* h, float* const* grads, int num_para
     }
     return MGPT_OK;
   }
-  // host destinations: through one host buffer, added in place
+  // host destinations: the whole gradient buffer in one copy and one wait,
+  // then each piece added in place from its place in that copy
   std::vector<float> tmp;
+  try {
+    tmp.resize(h->g_total);
+  } catch (const std::bad_alloc&) {
+    return fail(MGPT_ERR_OUT_OF_MEMORY, "host buffer of %zu floats", h->g_total);
+  }
+  HIP_TRY(hipMemcpyAsync(tmp.data(), h->grad, sizeof(float) * h->g_total, hipMemcpyDeviceToHost,
+                         st));
+  HIP_TRY(hipStreamSynchronize(st));
   for (int i = 0; i < num_params; ++i) {
     const GradPiece g = grad_piece(h, i);
-    tmp.resize((size_t)g.rows * g.cols);
-    HIP_TRY(hipMemcpy2DAsync(tmp.data(), sizeof(float) * g.cols, h->grad + g.off,
-                             sizeof(float) * g.ld, sizeof(float) * g.cols, g.rows,
-                             hipMemcpyDeviceToHost, st));
-    HIP_TRY(hipStreamSynchronize(st));
     float* d = grads[i];
-    for (size_t q = 0; q < tmp.size(); ++q) d[q] = d[q] + tmp[q];
+    for (int r = 0; r < g.rows; ++r) {
+      const float* srow = tmp.data() + g.off + (size_t)r * g.ld;
+      float* drow = d + (size_t)r * g.cols;
+      for (int c = 0; c < g.cols; ++c) drow[c] = drow[c] + srow[c];
+    }
   }
   return MGPT_OK;
 }

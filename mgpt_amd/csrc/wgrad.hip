@@ -748,7 +748,28 @@ __global__ __launch_bounds__(256) void zero_idle_experts_kernel(const int32_t* _
   }
 }
 
+// n floats of p (16-byte aligned) set to zero: a kernel, so that a HIP graph
+// captures a kernel node and not a memset node.
+__global__ __launch_bounds__(256) void fill_zero_kernel(float4* __restrict__ p, size_t n4,
+                                                        float* __restrict__ tail, int ntail) {
+  const size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  for (size_t i = t0; i < n4; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if (t0 < (size_t)ntail) tail[t0] = 0.0f;
+}
+
 }  // namespace
+
+hipError_t launch_fill_zero(float* p, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  if ((reinterpret_cast<uintptr_t>(p) & 15) != 0) return hipErrorInvalidValue;
+  const size_t n4 = n / 4;
+  const size_t want = (n4 + 255) / 256;
+  const int blocks = (int)std::max<size_t>(1, std::min<size_t>(want, 2048));
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0, stream,
+                     reinterpret_cast<float4*>(p), n4, p + 4 * n4, (int)(n - 4 * n4));
+  return hipGetLastError();
+}
 
 // The store-mode companion of launch_wgrad: clears the slices of every
 // expert with counts[e] == 0, which the weight-gradient launches leave as

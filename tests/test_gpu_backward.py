@@ -250,3 +250,82 @@ def test_fp8_handle_has_no_backward():
     with pytest.raises(capi.MoEError) as ei:
         layer.forward(x, train=True)
     assert ei.value.status == capi.MGPT_ERR_UNSUPPORTED
+
+
+def _collect(layer, cfg, dx):
+    g = [t.cpu().numpy() for t in layer.get_gradients()]
+    out = {"dx": dx.float().cpu().numpy(), "dWr": g[0], "dbr": g[1].reshape(-1)}
+    for i, n in enumerate(NAMES[2:]):
+        arr = np.stack([g[2 + 6 * e + i] for e in range(cfg.E)])
+        out[n] = arr.reshape(cfg.E, -1) if n.startswith("db") else arr
+    return out
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_graph_captured_training_step(act):
+    """forward_train + backward captured into one HIP graph.  A captured
+    backward always adds.  Captured right after zero_grad, the pending zeros
+    are part of the graph: every replay equals an eager zero_grad + step, bit
+    for bit.  Captured with nothing pending, replays accumulate (2x after two),
+    and zero_grad between replays (now a fill on the stream) restarts the
+    sum.  Eager steps between replays leave the replays unchanged."""
+    from mgpt_amd import workload as wl
+    cfg = wl.MoEConfig("cap", 300, 128, 6, 2, 192, act, act, "normal")
+    inp = wl.make_inputs(cfg, seed=11, bias_std=0.05)
+    if act == "bf16":
+        inp.x[:] = wl.bf16_round(inp.x)
+    dy = np.random.default_rng(5).standard_normal((cfg.N, cfg.C)).astype(np.float32)
+    if act == "bf16":
+        dy = wl.bf16_round(dy)
+    layer = make_layer(inp)
+    eager = run_backward(layer, inp, dy)          # allocates the workspace and gradients
+    dt = _dt(cfg)
+    x = torch.from_numpy(np.ascontiguousarray(inp.x)).to("cuda").to(dt)
+    d = torch.from_numpy(np.ascontiguousarray(dy)).to("cuda").to(dt)
+    y = torch.empty_like(x)
+    dx = torch.empty_like(x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                 # warm-up off the capture
+        layer.forward_into(x, y, train=True)
+        layer.backward_into(d, dx)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+
+    def same(got, ref, mult=1):
+        for n in ("dx",) + NAMES:
+            want = ref[n] if n == "dx" else mult * ref[n]
+            assert np.array_equal(got[n], want), (n, mult)
+
+    layer.zero_grad()                             # eager: zeros pending at capture
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        layer.forward_into(x, y, train=True)
+        layer.backward_into(d, dx)
+    torch.cuda.synchronize()
+    for r in range(2):
+        g1.replay()
+        torch.cuda.synchronize()
+        same(_collect(layer, cfg, dx), eager)
+        run_backward(layer, inp, dy)              # eager work between replays
+        print(f"{act}: graph with the pending zeros, replay {r} equals the eager step",
+              flush=True)
+
+    layer.zero_grad()                             # a fill now: nothing pending at capture
+    g2 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g2):
+        layer.forward_into(x, y, train=True)
+        layer.backward_into(d, dx)
+    torch.cuda.synchronize()
+    layer.zero_grad()
+    g2.replay()
+    torch.cuda.synchronize()
+    same(_collect(layer, cfg, dx), eager, 1)
+    g2.replay()
+    torch.cuda.synchronize()
+    same(_collect(layer, cfg, dx), eager, 2)
+    layer.zero_grad()
+    g2.replay()
+    torch.cuda.synchronize()
+    same(_collect(layer, cfg, dx), eager, 1)
+    print(f"{act}: adding graph accumulates 1x, 2x, then 1x after zero_grad", flush=True)

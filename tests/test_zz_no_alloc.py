@@ -104,3 +104,42 @@ def test_noalloc_refuses_beyond_its_scratch():
     y_ref = layer.forward(x)
     y2, _ = _noalloc(layer, x)
     assert torch.equal(y2.view(torch.int16), y_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("N,Cm,E,k,H,act,weights", SHAPES[:2])
+def test_noalloc_captured_graph_replays(N, Cm, E, k, H, act, weights):
+    """The use the entry point is for: mgpt_moe_forward_noalloc captured into
+    a HIP graph (its scratch address was looked up at handle creation, so
+    the capture records only kernels).  Each replay on new inputs equals an
+    eager noalloc forward of the same inputs bit for bit, with eager work
+    between the replays."""
+    from mgpt_amd import capi
+    cfg = wl.MoEConfig(f"noalloc_graph_{Cm}", N, Cm, E, k, H, act, weights, "normal")
+    layer, x = _layer(cfg, C.SEED + 7 * N)
+    print(f"noalloc graph case {cfg}", flush=True)
+    static_x = x.clone()
+    static_y = torch.empty_like(x)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):                 # warm-up off the capture
+        capi.check(capi.lib().mgpt_moe_forward_noalloc(layer._h, static_x.data_ptr(),
+                                                       static_y.data_ptr(), N,
+                                                       side.cuda_stream))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        capi.check(capi.lib().mgpt_moe_forward_noalloc(
+            layer._h, static_x.data_ptr(), static_y.data_ptr(), N,
+            torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    iv = torch.int16 if x.dtype == torch.bfloat16 else torch.int32
+    for r in range(3):
+        ctx = torch.roll(x, shifts=-5 * r, dims=0).contiguous()
+        static_x.copy_(ctx)
+        g.replay()
+        torch.cuda.synchronize()
+        got = static_y.clone()
+        want, _ = _noalloc(layer, ctx)            # eager work between replays
+        assert torch.equal(got.view(iv), want.view(iv)), f"replay {r} differs"
+    print(f"3 replays at N = {N} equal the eager noalloc forward", flush=True)
