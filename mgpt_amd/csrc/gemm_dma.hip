@@ -110,14 +110,16 @@ constexpr int kGroupM = 4;   // m-tiles per group of the tile order
 // e holds expert e; E <= 64), so that locating a tile needs no memory access
 // and no barrier.
 struct SegScan {
-  int cnt, rows_incl, tiles_incl, tiles_excl, tm;
+  // (the exclusive counts are recomputed where needed: the kernel runs at
+  // the register limit, and these live in every lane throughout)
+  int cnt, rows_incl, tiles_incl, tm;
+  __device__ __forceinline__ int tiles_excl() const { return tiles_incl - (cnt + kBM - 1) / kBM; }
   __device__ __forceinline__ void init(const int32_t* __restrict__ counts, int E) {
     const int l = lane_id();
     cnt = (l < E) ? counts[l] : 0;
     const int tiles = (cnt + kBM - 1) / kBM;
     rows_incl = wave_incl_scan(cnt);
     tiles_incl = wave_incl_scan(tiles);
-    tiles_excl = tiles_incl - tiles;
     tm = __builtin_amdgcn_readfirstlane(__shfl(tiles_incl, kWave - 1, kWave));   // all m-tiles
   }
 };
@@ -134,12 +136,13 @@ __device__ __forceinline__ bool locate_tile(const SegScan& sc, int E, int nbx, i
   const int idx = v - g * kGroupM * nbx;
   const int mt = g * kGroupM + idx % gsize;
   const int l = lane_id();
-  const bool mine = (l < E) && (mt >= sc.tiles_excl) && (mt < sc.tiles_incl);
+  const int texcl = sc.tiles_excl();
+  const bool mine = (l < E) && (mt >= texcl) && (mt < sc.tiles_incl);
   const unsigned long long m = __ballot(mine);
   const int owner = __ffsll((long long)m) - 1;   // exists: mt < tm
   out->expert = __builtin_amdgcn_readfirstlane(owner);
   out->row0 = __builtin_amdgcn_readfirstlane(
-      __shfl((sc.rows_incl - sc.cnt) + (mt - sc.tiles_excl) * kBM, owner, kWave));
+      __shfl((sc.rows_incl - sc.cnt) + (mt - texcl) * kBM, owner, kWave));
   out->row_end = __builtin_amdgcn_readfirstlane(__shfl(sc.rows_incl, owner, kWave));
   out->n0 = (idx / gsize) * kBN;
   return true;
@@ -194,6 +197,29 @@ __device__ __forceinline__ void store_group32(bf16_t* base, const uint2 (&q)[4],
     *reinterpret_cast<uint4*>(base + 8 * lhalf) = w0;
     *reinterpret_cast<uint4*>(base + 16 + 8 * lhalf) = w1;
   }
+}
+
+// The inverse of store_group32: loads the 32 bf16 values (features base ..
+// base+31) of one token as two 16-byte vectors per lane (lane half h takes
+// features 8h..8h+7 and 16+8h..16+8h+7) and swaps quads with the partner
+// lane, so that q[g] of lane half h holds features 8g+4h .. 8g+4h+3, the
+// accumulator layout.  Rows past the segment read zeros (no access); every
+// lane of the pair runs the swaps.
+__device__ __forceinline__ void load_group32(const bf16_t* base, uint2 (&q)[4], int lhalf,
+                                             bool load) {
+  uint4 w0 = make_uint4(0u, 0u, 0u, 0u), w1 = w0;
+  if (load) {
+    w0 = *reinterpret_cast<const uint4*>(base + 8 * lhalf);
+    w1 = *reinterpret_cast<const uint4*>(base + 16 + 8 * lhalf);
+  }
+  const auto s0 = __builtin_amdgcn_permlane32_swap(w0.x, w0.z, false, false);
+  const auto s1 = __builtin_amdgcn_permlane32_swap(w0.y, w0.w, false, false);
+  const auto s2 = __builtin_amdgcn_permlane32_swap(w1.x, w1.z, false, false);
+  const auto s3 = __builtin_amdgcn_permlane32_swap(w1.y, w1.w, false, false);
+  q[0] = make_uint2(s0[0], s1[0]);
+  q[1] = make_uint2(s0[1], s1[1]);
+  q[2] = make_uint2(s2[0], s3[0]);
+  q[3] = make_uint2(s2[1], s3[1]);
 }
 
 // Epilogue straight from the accumulators of a wave's WTN-feature x
@@ -254,8 +280,9 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
       const int hb = cur.n0 + wn * W::WTN + j * 32;
       if (hb >= n_store) continue;
       const int pc = packed_gate_col(hb);
-      // the loads of two 32-token sub-tiles at a time: half the memory
-      // round trips of one at a time, within the register budget
+      // the g and u loads of two 32-token sub-tiles at a time, as 16-byte
+      // vectors: half the memory round trips of one at a time, within the
+      // register budget (four at a time spill)
       constexpr int kPair = 2;
 #pragma unroll
       for (int i2 = 0; i2 < W::TM; i2 += kPair) {
@@ -264,12 +291,9 @@ __device__ __forceinline__ void store_tile(const f32x16 (&acc)[Waves<NW>::TN][Wa
         for (int ii = 0; ii < kPair; ++ii) {
           const int row = tok_base + (i2 + ii) * 32;
           const bool ok = row < cur.row_end;
-          const bf16_t* src = save + (size_t)row * save_ld + pc + 4 * lhalf;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            gq[ii][g] = ok ? *reinterpret_cast<const uint2*>(src + 8 * g) : make_uint2(0u, 0u);
-            uq[ii][g] = ok ? *reinterpret_cast<const uint2*>(src + 32 + 8 * g) : make_uint2(0u, 0u);
-          }
+          const bf16_t* src = save + (size_t)row * save_ld + pc;
+          load_group32(src, gq[ii], lhalf, ok);
+          load_group32(src + 32, uq[ii], lhalf, ok);
         }
 #pragma unroll
         for (int ii = 0; ii < kPair; ++ii) {
@@ -411,6 +435,11 @@ __device__ __forceinline__ void init_acc(f32x16 (&acc)[Waves<NW>::TN][Waves<NW>:
 #pragma unroll
       for (int v = 0; v < 16; ++v) b[v] = 0.0f;
     }
+    // The wait for these loads happens here, at the item's start: past this
+    // point the values count as computed, so sub-tiles that no MFMA
+    // touches (MT < 4) do not make the epilogue wait for the loads and,
+    // with them, for the ring's DMA.
+    if constexpr (EPI != kEpiSwigluBwd) asm volatile("" : "+v"(b));
 #pragma unroll
     for (int i = 0; i < W::TM; ++i) acc[j][i] = b;
     // one feature group at a time: keeps the scheduler from hoisting all
@@ -626,8 +655,15 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     }
     mfma_drain<NW>();
     if (cur.sidx < 0) {
-      store_tile<EPI, NW, kSave>(acc, cur.tile, wn, wm, lrow, lhalf, n_store, out, ldo, save,
-                                 save_ld);
+      // The lane's row and half recomputed here rather than kept live from
+      // the start: the kernel runs at the register limit, and a value held
+      // across the k loop gets spilled (its reload then waits for the
+      // ring's DMA loads as well).
+      int lane_now;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0"
+                   : "=v"(lane_now));
+      store_tile<EPI, NW, kSave>(acc, cur.tile, wn, wm, lane_now & 31, lane_now >> 5, n_store,
+                                 out, ldo, save, save_ld);
     } else {
       float4* P = reinterpret_cast<float4*>(partials + (size_t)cur.sidx * kPartialFloats) + tid;
 #pragma unroll
