@@ -144,6 +144,37 @@ __global__ __launch_bounds__(256) void permute_kernel(
   const int nflat = ntok * k;
   const size_t flat0 = (size_t)tok0 * k;
 
+  // Row copy geometry (used below): this slice's 16-byte chunks [q0, q1);
+  // thread t takes chunk q0 + t % W of tokens t / W, t / W + R, ...
+  // (W = min(slice width, 256) consecutive threads per row, R = 256 / W
+  // rows per step), four tokens in flight before their k stores each.
+  using Chunk = RowChunk<InT, ActT>;
+  constexpr int U = 4;
+  const int chunks = C * (int)sizeof(ActT) / 16;
+  const int q0 = (int)((long)blockIdx.y * chunks / gridDim.y);
+  const int q1 = (int)((long)(blockIdx.y + 1) * chunks / gridDim.y);
+  const int W = min(q1 - q0, 256);
+  const int R = 256 / W;
+  const int rr = tid / W;
+  const int qf = q0 + tid % W;
+  // The rows do not depend on the slots: the first batch is loaded before
+  // the ranking, so its latency overlaps the histogram and id loads.
+  const bool have_pre = rr < R && qf < q1 && rr < ntok;
+  Chunk pre[U];
+  if (have_pre) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) pre[u].load(x + (size_t)(tok0 + min(rr + R * u, ntok - 1)) * C, qf);
+  }
+  // every id of the block, for the ranking wave, loaded up front as well
+  constexpr int kIdPerLane = kRouterTokens * kMaxTopK / kWave;
+  int ids[kIdPerLane];
+  if (tid < kWave) {
+#pragma unroll
+    for (int u = 0; u < kIdPerLane; ++u) {
+      const int f = u * kWave + tid;
+      ids[u] = f < nflat ? topk_idx[flat0 + f] : -1;
+    }
+  }
   for (int f = tid; f < kRouterTokens * kMaxTopK; f += 256) s_slot[f] = -1;
   if (base) {
     // scanned by expert_scan_kernel
@@ -218,14 +249,6 @@ __global__ __launch_bounds__(256) void permute_kernel(
   if (tid < kWave) {
     const int l = tid;
     const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (kWave - l));
-    // every id of the block loaded before the ranking uses any
-    constexpr int kIdPerLane = kRouterTokens * kMaxTopK / kWave;
-    int ids[kIdPerLane];
-#pragma unroll
-    for (int u = 0; u < kIdPerLane; ++u) {
-      const int f = u * kWave + l;
-      ids[u] = f < nflat ? topk_idx[flat0 + f] : -1;
-    }
 #pragma unroll
     for (int u = 0; u < kIdPerLane; ++u) {
       const int f0 = u * kWave;
@@ -257,27 +280,20 @@ __global__ __launch_bounds__(256) void permute_kernel(
     }
   }
   __syncthreads();
-  // Row copy of this slice's 16-byte chunks [q0, q1): thread t takes chunk
-  // q0 + t % W of tokens t / W, t / W + R, ... (W = min(slice width, 256)
-  // consecutive threads per row, R = 256 / W rows per step), four tokens in
-  // flight before their k stores each.  A narrow slice still keeps (nearly)
-  // every lane busy.
-  const int chunks = C * (int)sizeof(ActT) / 16;
-  const int q0 = (int)((long)blockIdx.y * chunks / gridDim.y);
-  const int q1 = (int)((long)(blockIdx.y + 1) * chunks / gridDim.y);
-  const int W = min(q1 - q0, 256);
-  const int R = 256 / W;
-  const int rr = tid / W;
-  constexpr int U = 4;
+  // Row copy (a narrow slice still keeps nearly every lane busy).
   if (rr < R) {
-    for (int q = q0 + tid % W; q < q1; q += W) {
+    for (int q = qf; q < q1; q += W) {
       for (int r0 = rr; r0 < ntok; r0 += R * U) {
-        using Chunk = RowChunk<InT, ActT>;
         Chunk in[U];
+        if (q == qf && r0 == rr) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int r = min(r0 + R * u, ntok - 1);
-          in[u].load(x + (size_t)(tok0 + r) * C, q);
+          for (int u = 0; u < U; ++u) in[u] = pre[u];
+        } else {
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int r = min(r0 + R * u, ntok - 1);
+            in[u].load(x + (size_t)(tok0 + r) * C, q);
+          }
         }
         V16 v[U];
 #pragma unroll

@@ -32,6 +32,9 @@
 // d_gate = (d*u)*(sig*(1+g*(1-sig))), written to out in the interleaved
 // layout (out may equal aux: each element is read before it is written by
 // the same thread).
+#include <algorithm>
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace mgpt {
@@ -62,7 +65,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
     const AT* __restrict__ A, const WT* __restrict__ B, const float* __restrict__ wscale,
     const float* __restrict__ bias0, const float* __restrict__ bias1,
     const int32_t* __restrict__ counts, int E, int K, int Npad, int n_store, int bias_ld,
-    OutT* out, int ldo, OutT* aux, int aux_ld) {
+    OutT* out, int ldo, OutT* aux, int aux_ld, float* __restrict__ partials) {
   constexpr int BK = KSlab<AT>::BK;
   constexpr int PAD = 16 / (int)sizeof(AT);
   constexpr int LDK = BK + PAD;
@@ -158,7 +161,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int KT = K / BK;
+  // Split K (DOWN only, gridDim.z parts): part z takes slabs
+  // [z*KT/S, (z+1)*KT/S) and stores its fp32 partial tile for
+  // split_reduce_kernel instead of running the epilogue.
+  const int S = gridDim.z, z = blockIdx.z;
+  const int KT = K / BK / S;
+  Ablk += (size_t)z * KT * BK;
+  Bblk += (size_t)z * KT * BK;
   gload(0);
   sstore(0);
   __syncthreads();
@@ -214,6 +223,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
   // Epilogue.  Accumulator register v of a 32x32 tile holds row
   // 8*(v/4) + 4*(lane/32) + v%4 and column lane%32.
   const int row_base = ti.row0 + wm * WTM;
+  if constexpr (EPI == kEpiDown) {
+    if (S > 1) {
+      // the partial tile [BM][BN] in slot (z, m-tile, n-tile)
+      float* P = partials + ((size_t)(z * gridDim.y + mtile) * gridDim.x + bid % nbx) * (BM * BN);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            P[(wm * WTM + i * 32 + 8 * (v / 4) + 4 * lhalf + (v % 4)) * BN + wn * WTN + j * 32 +
+              lrow] = acc[i][j][v];
+      return;
+    }
+  }
   if constexpr (EPI == kEpiGateUp) {
 #pragma unroll
     for (int q = 0; q < TN / 2; ++q) {
@@ -293,30 +317,99 @@ __global__ __launch_bounds__(256) void grouped_gemm_kernel(
   }
 }
 
+// The epilogue of a split DOWN product: block (n-tile x, m-tile y, slice z)
+// takes every 4 consecutive outputs of its tile's slice z of kSlices, loads
+// the S partial float4s at once, sums them in part order (deterministic),
+// adds the bias and stores.
+constexpr int kReduceSlices = 8;
+#ifndef MGPT_MAX_KSPLIT
+#define MGPT_MAX_KSPLIT 8   // at most 8 parts (the reduce keeps 8 float4s in flight)
+#endif
+template <int BM, int BN, typename OutT>
+__global__ __launch_bounds__(256) void split_reduce_kernel(
+    const float* __restrict__ partials, int S, const float* __restrict__ bias0,
+    const int32_t* __restrict__ counts, int E, int n_store, int bias_ld, OutT* out, int ldo) {
+  static_assert(BM * BN % (4 * 256 * kReduceSlices) == 0, "slices of whole float4 rows");
+  TileInfo ti;
+  if (!find_tile<BM>(counts, E, blockIdx.y, &ti)) return;
+  const int n0 = blockIdx.x * BN;
+  const size_t tile = (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+  const size_t part_stride = (size_t)gridDim.y * gridDim.x * (BM * BN);
+  constexpr int kPer = BM * BN / 4 / kReduceSlices;   // float4s per slice
+  for (int q4 = blockIdx.z * kPer + threadIdx.x; q4 < (blockIdx.z + 1) * kPer; q4 += 256) {
+    const int q = 4 * q4, r = q / BN, c = q % BN;
+    const int row = ti.row0 + r, col = n0 + c;
+    if (row >= ti.row_end || col >= n_store) continue;   // n_store is a multiple of 4
+    const float4* P = reinterpret_cast<const float4*>(partials + tile * (BM * BN) + q);
+    float4 v[8];
+#pragma unroll
+    for (int zz = 0; zz < 8; ++zz)
+      if (zz < S) v[zz] = P[zz * (part_stride / 4)];
+    float4 a = v[0];
+#pragma unroll
+    for (int zz = 1; zz < 8; ++zz)
+      if (zz < S) {
+        a.x += v[zz].x;
+        a.y += v[zz].y;
+        a.z += v[zz].z;
+        a.w += v[zz].w;
+      }
+    const float* bp = bias0 ? bias0 + (size_t)ti.expert * bias_ld + col : nullptr;
+    OutT* o = out + (size_t)row * ldo + col;
+    store_act(o, a.x + (bp ? bp[0] : 0.0f));
+    store_act(o + 1, a.y + (bp ? bp[1] : 0.0f));
+    store_act(o + 2, a.z + (bp ? bp[2] : 0.0f));
+    store_act(o + 3, a.w + (bp ? bp[3] : 0.0f));
+  }
+}
+
 }  // namespace
 
 // Host launcher.  max_mtiles must bound sum_e ceil(count_e / BM) (the
 // caller uses ceil(A / BM) + E); surplus blocks exit after find_tile.
 // aux / aux_ld: the pre-activation save of GATEUP (null: none) or the saved
 // pre-activations SWIGLU_BWD reads (required).
+// DOWN and SWIGLU_BWD cover only the n-tiles that hold stored columns
+// (n_store; Npad is the weights' row stride).  partials (DOWN only, or
+// null): with split_slots > 0 fp32 partial tiles for up to split_slots
+// (part, m-tile, n-tile) items, the K dimension of a product with fewer
+// tiles than that is split into S = 2, 4 or 8 parts (S * tiles <=
+// split_slots), and split_reduce_kernel runs the epilogue.
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT* A, const WT* B, const float* wscale, const float* bias0,
                                const float* bias1, const int32_t* counts, int E, int K, int Npad,
                                int n_store, int bias_ld, OutT* out, int ldo, int max_mtiles,
-                               OutT* aux, int aux_ld, hipStream_t stream) {
+                               OutT* aux, int aux_ld, hipStream_t stream, float* partials,
+                               int split_slots) {
   if (max_mtiles <= 0) return hipSuccess;
   if (EPI == kEpiSwigluBwd && aux == nullptr) return hipErrorInvalidValue;
-  dim3 grid(Npad / BN, max_mtiles);
+  constexpr int BK = KSlab<AT>::BK;
+  const int ntiles = EPI == kEpiGateUp ? Npad / BN : std::min(Npad / BN, (n_store + BN - 1) / BN);
+  int S = 1;
+  if (EPI == kEpiDown && partials && split_slots > 0 && n_store % 4 == 0 &&
+      !std::is_same<WT, fp8_t>::value) {
+    const int KT = K / BK;
+    const long tiles = (long)ntiles * max_mtiles;
+    while (S < MGPT_MAX_KSPLIT && (long)(2 * S) * tiles <= split_slots && KT % (2 * S) == 0)
+      S *= 2;
+  }
+  dim3 grid(ntiles, max_mtiles, S);
   hipLaunchKernelGGL((grouped_gemm_kernel<BM, BN, WM, WN, AT, WT, EPI, OutT>), grid, dim3(256), 0,
                      stream, A, B, wscale, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out,
-                     ldo, aux, aux_ld);
+                     ldo, aux, aux_ld, partials);
+  if constexpr (EPI == kEpiDown) {
+    if (S > 1)
+      hipLaunchKernelGGL((split_reduce_kernel<BM, BN, OutT>), dim3(ntiles, max_mtiles, kReduceSlices),
+                         dim3(256), 0, stream, partials, S, bias0, counts, E, n_store, bias_ld, out,
+                         ldo);
+  }
   return hipGetLastError();
 }
 
 #define MGPT_INST_GEMM(BM, BN, WM, WN, AT, WT, EPI, OT)                                     \
   template hipError_t launch_grouped_gemm<BM, BN, WM, WN, AT, WT, EPI, OT>(                 \
       const AT*, const WT*, const float*, const float*, const float*, const int32_t*, int, int, \
-      int, int, int, OT*, int, int, OT*, int, hipStream_t);
+      int, int, int, OT*, int, int, OT*, int, hipStream_t, float*, int);
 
 // Large-M tiles (prefill-shaped segments).
 MGPT_INST_GEMM(128, 128, 2, 2, bf16_t, bf16_t, kEpiGateUp, bf16_t)

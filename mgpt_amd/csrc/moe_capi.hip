@@ -54,7 +54,7 @@ hipError_t launch_add_jobs(const float*, const AddJobs&, size_t, hipStream_t);
 template <int BM, int BN, int WM, int WN, typename AT, typename WT, int EPI, typename OutT>
 hipError_t launch_grouped_gemm(const AT*, const WT*, const float*, const float*, const float*,
                                const int32_t*, int, int, int, int, int, OutT*, int, int, OutT*,
-                               int, hipStream_t);
+                               int, hipStream_t, float* partials = nullptr, int split_slots = 0);
 template <typename DT>
 hipError_t launch_pack_transpose(const float*, int, int, DT*, int, int, int, hipStream_t);
 hipError_t launch_quantize_rows(const float*, int, int, uint8_t*, float*, hipStream_t);
@@ -128,6 +128,10 @@ namespace {
 
 constexpr size_t kAlign = 256;
 constexpr size_t kGemmPartialBytes = 512 * 128 * 4;   // one 256x256 fp32 tile
+// fp32 handles: one 64x128 fp32 partial tile per CU for the split-K down
+// product of small token counts (a fixed size, so the workspace stays
+// monotonic in N)
+constexpr size_t kF32PartialBytes = 64 * 128 * 4;
 constexpr int kRowPad = 256;   // rows of slack after activation buffers (GEMM tile overrun)
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
@@ -302,7 +306,9 @@ struct mgpt_moe {
     L.hbuf = take((A + kRowPad) * Hp * act_bytes());
     L.obuf = take((A + kRowPad) * C * act_bytes());
     // fp32 partial tiles of the large-M GEMMs' split last round (one per CU)
-    L.partials = take(uses_gemm_dma(N) ? (size_t)num_cus * kGemmPartialBytes : 0);
+    L.partials = take(uses_gemm_dma(N)             ? (size_t)num_cus * kGemmPartialBytes
+                      : act == MGPT_DTYPE_F32 ? (size_t)num_cus * kF32PartialBytes
+                                              : 0);
     L.rstd = take((size_t)N * 4);
     const size_t pad_rows = padded() ? (size_t)N * C * io_bytes() : 0;
     L.xpad = take(pad_rows);
@@ -773,9 +779,10 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
         xg, (const float*)h->wgu, nullptr, h->bg, h->bu, counts, E, C, 2 * Hp, 2 * Hp, Hp, hb, Hp,
         mt, gu, 2 * Hp, st)));
     HIP_TRY(mark(3));
+    // few tiles (small N): split along K over the CUs (fp32 partials, in-order reduce)
     HIP_TRY((launch_grouped_gemm<64, 128, 2, 2, float, float, kEpiDown, float>(
         hb, (const float*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C, mt,
-        nullptr, 0, st)));
+        nullptr, 0, st, (float*)(ws + L.partials), h->num_cus)));
   } else {
     const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
     if (small_m(h, N)) {
