@@ -11,7 +11,8 @@ task states.  Full-size configurations are checked on routing digests, on
 the reference's sampled rows and on every token (cfg2, cfg3) or a row of
 every m-tile (cfg4) of the oracle's per-token forward (each row of the
 reference is an independent sequential sum, so the oracle's per-token rows
-equal the full run's).
+equal the full run's); cfg4's every token also against a plain torch fp32
+forward under the same routing.
 """
 import os
 
@@ -125,7 +126,8 @@ def test_parity_full_size(name):
     routing: every token at cfg2 and cfg3 (so every m-tile and feature tile
     of both expert GEMMs, the down GEMM's split last round included), and at
     cfg4 the tokens of the first and last row of every expert segment and of
-    every 256-row m-tile."""
+    every 256-row m-tile, and all of cfg4's 32768 tokens against a plain
+    torch fp32 forward of the expert products under the same routing."""
     case = C.ALL_CASES[name]
     print(f"case {name}: {case.cfg}", flush=True)
     fx = fixture(name)
@@ -141,6 +143,47 @@ def test_parity_full_size(name):
     print(f"{name}: {dense.size} tokens against the oracle", flush=True)
     ref = O.tokens_parallel(inp, r["topk_idx"], r["topk_p"], dense)
     check_close(y[dense], ref, TOL[case.cfg.weights], f"{name} dense rows")
+    if name == "cfg4":
+        # every one of the 32768 tokens against a plain fp32 reference of the
+        # same expert products under that (bit-checked) routing
+        check_close(y, torch_fp32_forward(inp, r["topk_idx"], r["topk_p"]),
+                    TOL[case.cfg.weights], f"{name} every token (torch fp32)")
+
+
+def torch_fp32_forward(inp, idx, topp):
+    """y[t] = sum over t's choices j, in ascending expert id, of
+    p[t][j] * (silu(x W_g + b_g) * (x W_u + b_u)) W_d + b_d for expert
+    idx[t][j]: the expert products of layers/SwiGLU.cpp:23-50 and the
+    scatter of utils/Tensor.cpp:1385-1408, in fp32 on the GPU with torch's
+    own matmuls (plain 2-D products of contiguous fp32 matrices)."""
+    cfg = inp.cfg
+    dev = torch.device("cuda", 0)
+    x = torch.from_numpy(np.ascontiguousarray(inp.x)).to(dev, torch.float32)
+    idx_t = torch.from_numpy(np.ascontiguousarray(idx)).to(dev).long()
+    p_t = torch.from_numpy(np.ascontiguousarray(topp)).to(dev, torch.float32)
+    N, k = idx_t.shape
+    contrib = torch.zeros((N, k, cfg.C), dtype=torch.float32, device=dev)
+    for e in range(cfg.E):
+        tok, j = torch.nonzero(idx_t == e, as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        xe = x[tok]
+        Wg = torch.from_numpy(inp.Wg[e]).to(dev)
+        Wu = torch.from_numpy(inp.Wu[e]).to(dev)
+        Wd = torch.from_numpy(inp.Wd[e]).to(dev)
+        g = xe @ Wg + torch.from_numpy(inp.bg[e]).to(dev)
+        u = xe @ Wu + torch.from_numpy(inp.bu[e]).to(dev)
+        h = g * torch.sigmoid(g) * u
+        o = h @ Wd + torch.from_numpy(inp.bd[e]).to(dev)
+        contrib[tok, j] = o * p_t[tok, j].unsqueeze(1)
+    # ascending expert id within each token (the slot order the scatter walks)
+    order = torch.argsort(idx_t, dim=1)
+    contrib = torch.gather(contrib, 1, order.unsqueeze(2).expand(-1, -1, cfg.C))
+    y = torch.zeros((N, cfg.C), dtype=torch.float32, device=dev)
+    for j in range(k):
+        y = y + contrib[:, j]
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
 
 
 @pytest.mark.parametrize("tile", ["128", "256"])
@@ -433,3 +476,21 @@ def test_empty_input_and_error_paths():
     y1 = layer.forward(xs)
     y2 = dev.forward(xs)
     assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("N", [150, 700, 1900, 4200])
+def test_f32_down_split_k(N):
+    """fp32 down product with its K split over the CUs: with H = 512 (16
+    slabs of 32) and E = 4, the token counts give about 8, 26, 64 and 135
+    m-tiles of 64 rows, so on 256 CUs the split takes 8, 8, 4 and 1 parts
+    (the last: no split).  Outputs at 1e-5 against the oracle, routing bit
+    for bit (the parts are summed in order, so repeated runs give the same
+    bits)."""
+    cfg = wl.MoEConfig(f"f32split_{N}", N, 128, 4, 2, 512, "f32", "f32", "normal")
+    inp = wl.make_inputs(cfg, C.SEED + N, bias_std=0.05)
+    layer, y, r, _, ys = run_gpu(inp, repeat=2)
+    ref = O.forward(inp)
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    check_close(y, ref["y"], TOL["f32"], f"f32 split N={N}")
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32)), "runs differ"
