@@ -1247,25 +1247,50 @@ int mgpt_moe_accumulate_gradients(mgpt_moe* h, float* const* grads, int num_para
     }
     return MGPT_OK;
   }
-  // host destinations: the whole gradient buffer in one copy and one wait,
-  // then each piece added in place from its place in that copy
-  std::vector<float> tmp;
-  try {
-    tmp.resize(h->g_total);
-  } catch (const std::bad_alloc&) {
-    return fail(MGPT_ERR_OUT_OF_MEMORY, "host buffer of %zu floats", h->g_total);
-  }
-  HIP_TRY(hipMemcpyAsync(tmp.data(), h->grad, sizeof(float) * h->g_total, hipMemcpyDeviceToHost,
-                         st));
-  HIP_TRY(hipStreamSynchronize(st));
-  for (int i = 0; i < num_params; ++i) {
+  // Host destinations: the pieces in buffer order, gathered into windows of
+  // consecutive pieces of at most kWindow floats (a larger piece is a window
+  // of its own); one copy and one wait per window, then each piece of the
+  // window is added in place.  A few waits in all (one at the shapes of the
+  // tests) instead of one per parameter, and a bounded host buffer.
+  constexpr size_t kWindow = (size_t)64 << 20;   // floats (256 MB)
+  std::vector<int> order(num_params);
+  for (int i = 0; i < num_params; ++i) order[i] = i;
+  std::sort(order.begin(), order.end(),
+            [&](int a, int b) { return grad_piece(h, a).off < grad_piece(h, b).off; });
+  auto span = [&](int i) {
     const GradPiece g = grad_piece(h, i);
-    float* d = grads[i];
-    for (int r = 0; r < g.rows; ++r) {
-      const float* srow = tmp.data() + g.off + (size_t)r * g.ld;
-      float* drow = d + (size_t)r * g.cols;
-      for (int c = 0; c < g.cols; ++c) drow[c] = drow[c] + srow[c];
+    return (size_t)(g.rows - 1) * g.ld + g.cols;   // floats from g.off to the piece's end
+  };
+  std::vector<float> tmp;
+  for (int a = 0; a < num_params;) {
+    const size_t w0 = grad_piece(h, order[a]).off;
+    int b = a + 1;
+    size_t w1 = w0 + span(order[a]);
+    while (b < num_params) {
+      const GradPiece g = grad_piece(h, order[b]);
+      const size_t end = g.off + span(order[b]);
+      if (end - w0 > kWindow) break;
+      w1 = std::max(w1, end);
+      ++b;
     }
+    try {
+      tmp.resize(w1 - w0);
+    } catch (const std::bad_alloc&) {
+      return fail(MGPT_ERR_OUT_OF_MEMORY, "host buffer of %zu floats", w1 - w0);
+    }
+    HIP_TRY(hipMemcpyAsync(tmp.data(), h->grad + w0, sizeof(float) * (w1 - w0),
+                           hipMemcpyDeviceToHost, st));
+    HIP_TRY(hipStreamSynchronize(st));
+    for (int q = a; q < b; ++q) {
+      const GradPiece g = grad_piece(h, order[q]);
+      float* d = grads[order[q]];
+      for (int r = 0; r < g.rows; ++r) {
+        const float* srow = tmp.data() + (g.off - w0) + (size_t)r * g.ld;
+        float* drow = d + (size_t)r * g.cols;
+        for (int c = 0; c < g.cols; ++c) drow[c] = drow[c] + srow[c];
+      }
+    }
+    a = b;
   }
   return MGPT_OK;
 }

@@ -329,3 +329,40 @@ def test_graph_captured_training_step(act):
     torch.cuda.synchronize()
     same(_collect(layer, cfg, dx), eager, 1)
     print(f"{act}: adding graph accumulates 1x, 2x, then 1x after zero_grad", flush=True)
+
+
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_accumulate_gradients_host_and_device(act):
+    """mgpt_moe_accumulate_gradients adds the handle's gradients into
+    caller buffers (Tensor::add_grad, utils/Tensor.cpp:638-650): host
+    destinations (copied in windows of whole pieces) and device
+    destinations must both give dest + gradient, one rounded add per
+    element, equal to get_gradients' values added on the host."""
+    from mgpt_amd import capi
+    from mgpt_amd import workload as wl
+    import ctypes
+    cfg = wl.MoEConfig("accum", 200, 64, 5, 2, 96, act, act, "normal")
+    inp = wl.make_inputs(cfg, seed=17, bias_std=0.05)
+    if act == "bf16":
+        inp.x[:] = wl.bf16_round(inp.x)
+    dy = wl.bf16_round(np.random.default_rng(9).standard_normal((cfg.N, cfg.C)).astype(np.float32))
+    layer = make_layer(inp)
+    out = run_backward(layer, inp, dy)
+    grads = [t.cpu().numpy() for t in layer.get_gradients()]
+    rng = np.random.default_rng(3)
+    base = [rng.standard_normal(g.shape).astype(np.float32) for g in grads]
+    # host destinations
+    host = [np.ascontiguousarray(b.copy()) for b in base]
+    ptrs = (ctypes.c_void_p * len(host))(*[h.ctypes.data for h in host])
+    st = torch.cuda.current_stream().cuda_stream
+    capi.check(capi.lib().mgpt_moe_accumulate_gradients(layer._h, ptrs, len(host), 0, st))
+    # device destinations
+    dev = [torch.from_numpy(b.copy()).cuda() for b in base]
+    dptrs = (ctypes.c_void_p * len(dev))(*[t.data_ptr() for t in dev])
+    capi.check(capi.lib().mgpt_moe_accumulate_gradients(layer._h, dptrs, len(dev), 1, st))
+    torch.cuda.synchronize()
+    for i, (b, g) in enumerate(zip(base, grads)):
+        want = (b + g).astype(np.float32)
+        assert np.array_equal(host[i], want), f"host piece {i}"
+        assert np.array_equal(dev[i].cpu().numpy(), want), f"device piece {i}"
+    assert out["dx"].shape == (cfg.N, cfg.C)
