@@ -29,8 +29,9 @@ sampling loop (pipeline/Generator.cpp:13-36: B = 1, no KV cache, the whole
 context re-run every step, cropped to max_seq_len S = cfg.N): the growing
 phase N = 1 .. S enqueued without any host synchronisation, then
 steady-state steps at N = S, eager and replayed from one captured HIP
-graph.  value = steady-state steps/s (graph replay).  The driver's headline
-line is the default forward.
+graph.  value = steady-state steps/s of the faster of the two (named in
+steady_mode; both are reported).  The driver's headline line is the
+default forward.
 """
 from __future__ import annotations
 
@@ -258,7 +259,7 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
                      f"and {w + k} unfused ({w} warmup, {k} timed)",
             "decode": f"{w + 1} growing loops of {b.get('growing_phase_steps')} steps "
                       f"(N = 1 .. {b['config']['N']}), then {k} eager, {k} "
-                      f"profiled, 1 + {w + k} graph-replayed steady-state "
+                      f"profiled, 1 + {max(w, 30) + k} graph-replayed steady-state "
                       "steps (kernel averages mix every N)"}.get(
         mode, f"{w + 2 * k} forwards ({w} warmup, {k} timed, {k} profiled)")
     out = [f"# {b['config']['workload'].split(':')[0]} MoE {what}: rocprofv3 kernel statistics "
@@ -289,8 +290,9 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
                 + ", ".join(f"{k} {v}" for k, v in b["backward_gemm_tflops"].items())
                 + f"; dominant: {rf['kernel']} = {100 * rf['frac']:.1f}% of {rf['peak']} TFLOP/s."]
     elif mode == "decode":
-        out += ["", f"bench.py: {b['value']:.0f} steady-state steps/s ({b['ms_per_step']} ms/step "
-                f"replayed from a HIP graph, {b['steady_eager_ms_per_step']} ms eager); growing "
+        out += ["", f"bench.py: {b['value']:.0f} steady-state steps/s ({b['ms_per_step']} ms/step, "
+                f"{b['steady_graph_ms_per_step']} ms replayed from a HIP graph, "
+                f"{b['steady_eager_ms_per_step']} ms eager); growing "
                 f"loop of {b['growing_phase_steps']} steps {b['growing_phase_ms']} ms on the "
                 f"device, enqueued by the host in {b['growing_phase_host_enqueue_ms']} ms; "
                 f"{rf['kernel']}: {rf['achieved']} GB/s = {100 * rf['frac']:.1f}% of "
@@ -679,7 +681,9 @@ def decode_main(args) -> int:
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         layer.forward_into(x, y)
-    for _ in range(args.warmup):
+    # the first replays of a new graph carry one-time costs (about 0.6 ms over
+    # the first few dozen on MI355X), so the graph warms up longer
+    for _ in range(max(args.warmup, 30)):
         g.replay()
     torch.cuda.synchronize()
     w0 = time.perf_counter()
@@ -696,14 +700,15 @@ def decode_main(args) -> int:
     gu_bytes = used * (2.0 * H * C * w + 2 * H * 4)
     dn_bytes = used * (1.0 * H * C * w + C * 4)
     t_gu = stages["gemm_gateup"] * 1e-3
+    best_ms = min(eager_ms, graph_ms)
     result = {
         "metric": METRIC_DECODE,
-        "value": round(1e3 / graph_ms, 1),
+        "value": round(1e3 / best_ms, 1),
         "unit": "steps/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(graph_ms, 4),
+        "ms_per_step": round(best_ms, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -712,6 +717,7 @@ def decode_main(args) -> int:
         "pass": "decode (sampling loop: growing context, then steady state)",
         "config": {"workload": workload_name(cfg) + f"; sampling loop, max_seq_len S={S}, B=1",
                    "N": S, "C": C, "E": E, "k": k, "H": H, "parallelism": "single GPU"},
+        "steady_mode": "graph" if graph_ms <= eager_ms else "eager",
         "steady_eager_ms_per_step": round(eager_ms, 4),
         "steady_graph_ms_per_step": round(graph_ms, 4),
         "growing_phase_ms": round(grow_ms, 4),
@@ -720,7 +726,7 @@ def decode_main(args) -> int:
         "stage_ms": {kk: round(v, 4) for kk, v in stages.items()},
         "experts_used": used,
         "weight_bytes_per_step": gu_bytes + dn_bytes,
-        "weight_stream_GBs": round((gu_bytes + dn_bytes) / (graph_ms * 1e-3) / 1e9, 1),
+        "weight_stream_GBs": round((gu_bytes + dn_bytes) / (best_ms * 1e-3) / 1e9, 1),
         "roofline": {
             "kernel": "gate/up fp8 weight-streaming GEMM + SwiGLU epilogue (steady-state step)",
             "bound": "hbm", "achieved": round(gu_bytes / t_gu / 1e9, 1), "peak": PEAK_HBM_GBS,

@@ -255,6 +255,12 @@ struct mgpt_moe {
   int prof_b_count = 0;
   hipEvent_t done = nullptr;
   bool done_valid = false;
+  // The backward's second stream (default priority) and its fork / join
+  // events, created with the gradient buffer: the down weight gradient runs
+  // beside the d(act) product.
+  hipStream_t side = nullptr;
+  hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+  int dact_cus = 0;   // persistent blocks of the d(act) product when forked
   const int32_t* last_counts = nullptr;
 
   size_t act_bytes() const { return act == MGPT_DTYPE_BF16 ? 2 : 4; }
@@ -387,6 +393,11 @@ int ensure_grad(mgpt_moe* h) {
   h->g_total = off;
   HIP_TRY(hipMalloc(&h->grad, sizeof(float) * off));
   h->grad_zero = true;
+  if (!h->side) {
+    HIP_TRY(hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking));
+    HIP_TRY(hipEventCreateWithFlags(&h->fork_ev, hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&h->join_ev, hipEventDisableTiming));
+  }
   return MGPT_OK;
 }
 
@@ -464,6 +475,13 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
   if (e == hipSuccess)
     e = hipDeviceGetAttribute(&h->num_cus, hipDeviceAttributeMultiprocessorCount, h->device);
   if (e == hipSuccess && h->num_cus <= 0) e = hipErrorInvalidDevice;
+  // the backward's d(act) product beside the down weight gradient: 5/8 of
+  // the CUs, a multiple of the XCD count (tuning override MGPT_MOE_DACT_CUS;
+  // cfg3 step on MI355X: 2.29 ms at 160 of 256 CUs, 2.33 at 128, 2.34 at 176,
+  // 2.31 at 200 and serial)
+  h->dact_cus = std::max(kNumXcd, h->num_cus * 5 / 8 / kNumXcd * kNumXcd);
+  if (const char* t = std::getenv("MGPT_MOE_DACT_CUS"))
+    h->dact_cus = std::min(h->num_cus, std::max(kNumXcd, std::atoi(t) / kNumXcd * kNumXcd));
   if (e == hipSuccess) {
     // Stage events only time: without the system-scope fence their record
     // does not write back and invalidate the caches, which otherwise leaves
@@ -503,6 +521,9 @@ int mgpt_moe_destroy(mgpt_moe* h) {
     for (auto& ev : slot)
       if (ev) (void)hipEventDestroy(ev);
   if (h->done) (void)hipEventDestroy(h->done);
+  if (h->fork_ev) (void)hipEventDestroy(h->fork_ev);
+  if (h->join_ev) (void)hipEventDestroy(h->join_ev);
+  if (h->side) (void)hipStreamDestroy(h->side);
   delete h;
   return MGPT_OK;
 }
@@ -909,6 +930,37 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   hipEvent_t* evs = h->evb[h->prof_b_count % mgpt_moe::kProfSlots];
   auto mark = [&](int i) -> hipError_t { return prof ? hipEventRecord(evs[i], st) : hipSuccess; };
 
+  // dW_down [H][C] and db_down from (h, dgo); dW_gate/up [C][H] and their
+  // biases from (gathered x, d(gate)/d(up))
+  // (an expert's long contraction is cut into row chunks whose partial
+  // tiles go to the split-K region, free again once the dX product is done)
+  float* wpart = h->uses_gemm_dma(N) ? (float*)(ws + L.partials) : nullptr;
+  const size_t wpart_bytes = wpart ? (size_t)h->num_cus * kGemmPartialBytes : 0;
+  float* wbpart = h->uses_gemm_dma(N) ? (float*)(ws + L.wg_bpart) : nullptr;
+  const size_t wbpart_bytes = wbpart ? h->wg_bpart_bytes() : 0;
+  // After zero_grad the gradients are written, not added to; the experts
+  // without rows are cleared instead (before either weight gradient).
+  const bool store = h->grad_zero;
+  bool down_done = false;
+  auto down_wgrad = [&](hipStream_t s) -> int {
+    if (store) {
+      IdleSlices z{};
+      const size_t lens[6] = {(size_t)C * H, (size_t)H, (size_t)C * H, (size_t)H, (size_t)H * C,
+                              (size_t)C};
+      for (int p = 0; p < 6; ++p) {
+        z.base[p] = g + h->g_off[2 + p];
+        z.len[p] = lens[p];
+      }
+      z.n = 6;
+      HIP_TRY(launch_zero_idle_experts(counts, E, z, s));
+    }
+    HIP_TRY((launch_wgrad<ActT, 0>(hb, Hp, Hp, dgo, C, C, counts, E, g + h->g_off[6], nullptr, C,
+                                   (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, A,
+                                   wpart, wpart_bytes, wbpart, wbpart_bytes, h->num_cus, store,
+                                   s)));
+    return MGPT_OK;
+  };
+
   HIP_TRY(mark(0));
   HIP_TRY(launch_scatter_bwd<ActT>(dy, ob, perm, topp, A, C, k, dgo, dtp, st));
   HIP_TRY(mark(1));
@@ -925,10 +977,26 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
     // prefill-shaped segments: the 256x256 direct-to-LDS kernel; the dX
     // product splits its last round like the forward's down GEMM
     const int mt = (A + 255) / 256 + E;
+    // The d(act) product's epilogue (read g, u; write d(gate), d(up)) keeps
+    // HBM busy while its k loops leave it idle, and on half the CUs it takes
+    // 579 instead of 352 us (cfg3): its epilogues are bound by the chip's
+    // bandwidth more than by the CUs'.  So it runs persistent on part of
+    // them, and the down weight gradient (which does not depend on it) runs
+    // from the second stream on the rest; the dX product waits for both.
+    // Stage timing keeps the launches serial.
+    const bool fork = !prof && h->side != nullptr;
+    if (fork) HIP_TRY(hipEventRecord(h->fork_ev, st));
     HIP_TRY(launch_gemm_dma<kEpiSwigluBwd>((const bf16_t*)dgo, (const bf16_t*)wdb, nullptr,
                                            nullptr, counts, E, C, h->Hq, Hp, 0, (bf16_t*)gu,
-                                           2 * Hp, mt, nullptr, h->num_cus, (bf16_t*)gu, 2 * Hp,
-                                           st));
+                                           2 * Hp, mt, nullptr, fork ? h->dact_cus : h->num_cus,
+                                           (bf16_t*)gu, 2 * Hp, st));
+    if (fork) {
+      HIP_TRY(hipStreamWaitEvent(h->side, h->fork_ev, 0));
+      if (int rc = down_wgrad(h->side)) return rc;
+      HIP_TRY(hipEventRecord(h->join_ev, h->side));
+      HIP_TRY(hipStreamWaitEvent(st, h->join_ev, 0));
+      down_done = true;
+    }
     HIP_TRY(mark(2));
     HIP_TRY(launch_gemm_dma<kEpiDown>((const bf16_t*)gu, (const bf16_t*)wgub, nullptr, nullptr,
                                       counts, E, 2 * Hp, Cp, C, 0, (bf16_t*)ob, C, mt,
@@ -953,32 +1021,8 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
         st)));
   }
   HIP_TRY(mark(3));
-  // dW_down [H][C] and db_down from (h, dgo); dW_gate/up [C][H] and their
-  // biases from (gathered x, d(gate)/d(up))
-  // (an expert's long contraction is cut into row chunks whose partial
-  // tiles go to the split-K region, free again once the dX product is done)
-  float* wpart = h->uses_gemm_dma(N) ? (float*)(ws + L.partials) : nullptr;
-  const size_t wpart_bytes = wpart ? (size_t)h->num_cus * kGemmPartialBytes : 0;
-  float* wbpart = h->uses_gemm_dma(N) ? (float*)(ws + L.wg_bpart) : nullptr;
-  const size_t wbpart_bytes = wbpart ? h->wg_bpart_bytes() : 0;
-  // After zero_grad the gradients are written, not added to; the experts
-  // without rows are cleared instead.
-  const bool store = h->grad_zero;
-  if (store) {
-    IdleSlices z{};
-    const size_t lens[6] = {(size_t)C * H, (size_t)H, (size_t)C * H, (size_t)H, (size_t)H * C,
-                            (size_t)C};
-    for (int p = 0; p < 6; ++p) {
-      z.base[p] = g + h->g_off[2 + p];
-      z.len[p] = lens[p];
-    }
-    z.n = 6;
-    HIP_TRY(launch_zero_idle_experts(counts, E, z, st));
-  }
-  HIP_TRY((launch_wgrad<ActT, 0>(hb, Hp, Hp, dgo, C, C, counts, E, g + h->g_off[6], nullptr, C,
-                                 (size_t)H * C, H, C, g + h->g_off[7], nullptr, (size_t)C, A,
-                                 wpart, wpart_bytes, wbpart, wbpart_bytes, h->num_cus, store,
-                                 st)));
+  if (!down_done)
+    if (int rc = down_wgrad(st)) return rc;
   HIP_TRY(mark(4));
   HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
                                  g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
