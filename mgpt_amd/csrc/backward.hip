@@ -249,8 +249,8 @@ __device__ __forceinline__ void rw_load_cols(const float* p, float (&v)[CPT]) {
 }
 
 // partial[chunk][e][c] = sum over the chunk's tokens of x[t][c] * dL[t][e]
-// (tokens in order, fused multiply-adds).  A thread holds CPT = 64 / EP
-// consecutive columns x EP >= E experts (64 accumulators), reads each
+// (tokens in order, fused multiply-adds).  A thread holds CPT consecutive
+// columns x EP >= E experts (CPT * EP accumulators), reads each
 // token's CPT values of x as one vector load and the token's dL row from
 // LDS as float4 broadcasts: CPT * EP FMAs per 1 + EP / 4 loads.  The x
 // loads run a group of 8 tokens ahead of the FMAs (two register groups;
@@ -259,13 +259,12 @@ __device__ __forceinline__ void rw_load_cols(const float* p, float (&v)[CPT]) {
 // expert's CPT sums go out as one vector store, lanes on consecutive
 // columns.  The blocks of the first column range also write
 // partial_b[chunk][e] = sum_t dL[t][e].
-template <typename ActT, int EP>
+template <typename ActT, int EP, int CPT>
 __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restrict__ x,
                                                            const float* __restrict__ dL, int N,
                                                            int C, int E,
                                                            float* __restrict__ partial,
                                                            float* __restrict__ partial_b) {
-  constexpr int CPT = 64 / EP;
   constexpr int kG = 8;   // tokens per load group
   static_assert(kRwChunk % (2 * kG) == 0, "whole group pairs per chunk");
   __shared__ float4 s_dl[kRwChunk][EP / 4];
@@ -447,16 +446,18 @@ hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int
   if (E <= 0 || E > kMaxExperts || C % 4) return hipErrorInvalidValue;
   if (N <= 0) return hipSuccess;
   const int chunks = router_wgrad_chunks(N);
-  // a block covers 256 threads x 64 / EP columns
+  // a block covers 256 threads x CPT columns; E <= 32 takes two columns per
+  // thread (at cfg3, E = 16, four columns per thread gave one wave per SIMD
+  // and 42 us)
   if (E <= 16)
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16>), dim3((C + 1023) / 1024, chunks), dim3(256),
-                       0, stream, x, dL, N, C, E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16, 2>), dim3((C + 511) / 512, chunks),
+                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b);
   else if (E <= 32)
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32>), dim3((C + 511) / 512, chunks), dim3(256),
-                       0, stream, x, dL, N, C, E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32, 2>), dim3((C + 511) / 512, chunks),
+                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b);
   else
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64>), dim3((C + 255) / 256, chunks), dim3(256),
-                       0, stream, x, dL, N, C, E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64, 1>), dim3((C + 255) / 256, chunks),
+                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b);
   const int CE = C * E;
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 15) / 16), dim3(256), 0, stream,
                      partial, partial_b, chunks, C, E, gW, gb, (int)store);
