@@ -254,7 +254,10 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
             "block": "fused block (RMSNorm + MoE + residual)",
             "decode": "decode steps in the sampling loop"}.get(mode, "forward")
     w, k = b["warmup"], b["steps"]
-    runs = {"train": f"{w + 2 * k} training steps ({w} warmup, {k} timed, {k} profiled)",
+    runs = {"train": f"{w + 2 * k} training steps ({w} warmup, {k} timed, {k} profiled); "
+                     "outside the profiled steps the d(act) product (on 5/8 of the CUs) and the "
+                     "down weight gradient run concurrently on two streams, so their averages "
+                     "mix those launches with the serial ones of the profiled steps",
             "block": f"{w + 2 * k} fused block forwards ({w} warmup, {k} timed, {k} profiled) "
                      f"and {w + k} unfused ({w} warmup, {k} timed)",
             "decode": f"{w + 1} growing loops of {b.get('growing_phase_steps')} steps "
