@@ -201,7 +201,7 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens,
  * graph replays the mode it was captured in): zeros still pending from an
  * eager mgpt_moe_zero_grad are written into the graph first, so each replay
  * of a graph captured right after zero_grad starts from zero.  Part of the
- * work (the down weight gradient, bf16 large-M shapes) runs on a second
+ * work (the weight gradients, bf16 large-M shapes) runs on a second
  * stream the handle owns, forked from and joined back into `stream` with
  * events; every result is ordered on `stream` when the call's work there is
  * done, as if it had all run there. */

@@ -150,6 +150,9 @@ struct Layout {
   // partials of the expert weight gradients' row chunks (their tile
   // partials reuse the split-K partial region)
   size_t probs, gu, dgo, dtp, dlog, rw_part, rw_part_b, wg_bpart;
+  // the gate/up weight gradient's row-chunk partials while it runs beside
+  // the dX product (which holds the split-K region)
+  size_t wg_part2;
   size_t dypad, dxpad;   // padded width: dy and dx at width C
   size_t total;
 };
@@ -261,6 +264,7 @@ struct mgpt_moe {
   hipStream_t side = nullptr;
   hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   int dact_cus = 0;   // persistent blocks of the d(act) product when forked
+  int dx_cus = 0;     // persistent blocks of the dX product beside the gate/up weight gradient (0: serial)
   const int32_t* last_counts = nullptr;
 
   size_t act_bytes() const { return act == MGPT_DTYPE_BF16 ? 2 : 4; }
@@ -330,6 +334,7 @@ struct mgpt_moe {
       L.rw_part = take(chunks * C * E * 4);
       L.rw_part_b = take(chunks * E * 4);
       L.wg_bpart = take(uses_gemm_dma(N) ? wg_bpart_bytes() : 0);
+      L.wg_part2 = take(uses_gemm_dma(N) && dx_cus > 0 ? (size_t)num_cus * kGemmPartialBytes : 0);
       L.dypad = take(pad_rows);
       L.dxpad = take(pad_rows);
     }
@@ -482,6 +487,11 @@ int mgpt_moe_create(const mgpt_moe_config* cfg, mgpt_moe** out) {
   h->dact_cus = std::max(kNumXcd, h->num_cus * 5 / 8 / kNumXcd * kNumXcd);
   if (const char* t = std::getenv("MGPT_MOE_DACT_CUS"))
     h->dact_cus = std::min(h->num_cus, std::max(kNumXcd, std::atoi(t) / kNumXcd * kNumXcd));
+  // ... and the dX product beside the gate/up weight gradient: half the CUs
+  // (MGPT_MOE_DX_CUS; 0 keeps the two serial)
+  h->dx_cus = std::max(kNumXcd, h->num_cus / 2 / kNumXcd * kNumXcd);
+  if (const char* t = std::getenv("MGPT_MOE_DX_CUS"))
+    h->dx_cus = std::min(h->num_cus, std::max(0, std::atoi(t) / kNumXcd * kNumXcd));
   if (e == hipSuccess) {
     // Stage events only time: without the system-scope fence their record
     // does not write back and invalidate the caches, which otherwise leaves
@@ -941,7 +951,7 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   // After zero_grad the gradients are written, not added to; the experts
   // without rows are cleared instead (before either weight gradient).
   const bool store = h->grad_zero;
-  bool down_done = false;
+  bool down_done = false, gateup_done = false;
   auto down_wgrad = [&](hipStream_t s) -> int {
     if (store) {
       IdleSlices z{};
@@ -998,9 +1008,26 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
       down_done = true;
     }
     HIP_TRY(mark(2));
+    const bool fork2 = fork && h->dx_cus > 0;
+    if (fork2) {
+      // The gate/up weight gradient (it needs d(gate), d(up)) beside the dX
+      // product, with its row-chunk partials in a region of its own: the two
+      // fill each other's last rounds and reduce kernels (cfg3 step 2.24-2.25
+      // -> 2.22-2.23 ms with dX on 128 of 256 CUs; 96: 2.26, 160: 2.23).
+      HIP_TRY(hipEventRecord(h->fork_ev, st));
+      HIP_TRY(hipStreamWaitEvent(h->side, h->fork_ev, 0));
+      HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
+                                     g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
+                                     g + h->g_off[5], (size_t)H, A, (float*)(ws + L.wg_part2),
+                                     wpart_bytes, wbpart, wbpart_bytes, h->num_cus, store,
+                                     h->side)));
+      HIP_TRY(hipEventRecord(h->join_ev, h->side));
+      gateup_done = true;
+    }
     HIP_TRY(launch_gemm_dma<kEpiDown>((const bf16_t*)gu, (const bf16_t*)wgub, nullptr, nullptr,
                                       counts, E, 2 * Hp, Cp, C, 0, (bf16_t*)ob, C, mt,
-                                      (float*)(ws + L.partials), h->num_cus, nullptr, 0, st));
+                                      (float*)(ws + L.partials), fork2 ? h->dx_cus : h->num_cus,
+                                      nullptr, 0, st));
   } else if (small_m(h, N)) {
     const int mt = (A + 31) / 32 + E;
     HIP_TRY((launch_grouped_gemm<32, 256, 1, 4, bf16_t, bf16_t, kEpiSwigluBwd, bf16_t>(
@@ -1024,10 +1051,11 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   if (!down_done)
     if (int rc = down_wgrad(st)) return rc;
   HIP_TRY(mark(4));
-  HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
-                                 g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
-                                 g + h->g_off[5], (size_t)H, A, wpart, wpart_bytes, wbpart,
-                                 wbpart_bytes, h->num_cus, store, st)));
+  if (!gateup_done)
+    HIP_TRY((launch_wgrad<ActT, 1>(xg, C, C, gu, 2 * Hp, 2 * Hp, counts, E, g + h->g_off[2],
+                                   g + h->g_off[4], H, (size_t)C * H, C, H, g + h->g_off[3],
+                                   g + h->g_off[5], (size_t)H, A, wpart, wpart_bytes, wbpart,
+                                   wbpart_bytes, h->num_cus, store, st)));
   HIP_TRY(mark(5));
   HIP_TRY(launch_token_bwd<ActT>(ob, slot_of, idx, dtp, probs, counts, h->wrt, N, C, E, k, dx,
                                  dlog, st));
@@ -1035,6 +1063,7 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
                                     (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
                                     store, st));
+  if (gateup_done) HIP_TRY(hipStreamWaitEvent(st, h->join_ev, 0));
   h->grad_zero = false;
   if (h->padded()) HIP_TRY(launch_copy_cols<ActT>(dx, C, dx_out, Cx, N, Cx, Cx, st));
   HIP_TRY(mark(7));
