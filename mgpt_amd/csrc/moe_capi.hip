@@ -259,8 +259,8 @@ struct mgpt_moe {
   hipEvent_t done = nullptr;
   bool done_valid = false;
   // The backward's second stream (default priority) and its fork / join
-  // events, created with the gradient buffer: the down weight gradient runs
-  // beside the d(act) product.
+  // events, created with the gradient buffer: the weight gradients run
+  // beside the d(act) and dX products.
   hipStream_t side = nullptr;
   hipEvent_t fork_ev = nullptr, join_ev = nullptr;
   int dact_cus = 0;   // persistent blocks of the d(act) product when forked
@@ -943,7 +943,9 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   // dW_down [H][C] and db_down from (h, dgo); dW_gate/up [C][H] and their
   // biases from (gathered x, d(gate)/d(up))
   // (an expert's long contraction is cut into row chunks whose partial
-  // tiles go to the split-K region, free again once the dX product is done)
+  // tiles go to the split-K region when the dX product is not using it: the
+  // down weight gradient runs before dX, the gate/up one after it or, beside
+  // it, with a region of its own)
   float* wpart = h->uses_gemm_dma(N) ? (float*)(ws + L.partials) : nullptr;
   const size_t wpart_bytes = wpart ? (size_t)h->num_cus * kGemmPartialBytes : 0;
   float* wbpart = h->uses_gemm_dma(N) ? (float*)(ws + L.wg_bpart) : nullptr;
@@ -994,7 +996,7 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
     // them, and the down weight gradient (which does not depend on it) runs
     // from the second stream on the rest; the dX product waits for both.
     // Stage timing keeps the launches serial.
-    const bool fork = !prof && h->side != nullptr;
+    const bool fork = !prof && h->side && h->fork_ev && h->join_ev;
     if (fork) HIP_TRY(hipEventRecord(h->fork_ev, st));
     HIP_TRY(launch_gemm_dma<kEpiSwigluBwd>((const bf16_t*)dgo, (const bf16_t*)wdb, nullptr,
                                            nullptr, counts, E, C, h->Hq, Hp, 0, (bf16_t*)gu,
