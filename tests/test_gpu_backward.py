@@ -141,6 +141,42 @@ def test_backward_accumulates_and_is_deterministic(act):
         assert np.array_equal(c[n], a[n]), n
 
 
+def test_two_stream_backward_repeats_and_matches_serial():
+    """At cfg3's shape the bf16 backward runs part of its work on a second
+    stream (the weight gradients beside the d(act) and dX products, which run
+    on part of the CUs).  Twenty steps must repeat every gradient and dx bit
+    for bit (a missing fork or join dependency would show as a difference),
+    and a step with stage timing (every launch serial on one stream, all CUs)
+    must give the same weight gradients; dx may differ within bf16 rounding,
+    since dX on fewer CUs splits a different last round along K."""
+    from mgpt_amd import workload as wl
+    cfg = wl.CONFIGS["cfg3"]
+    inp = wl.make_inputs(cfg, seed=7)
+    dy = wl.bf16_round(np.random.default_rng(3).standard_normal((cfg.N, cfg.C)).astype(np.float32))
+    layer = make_layer(inp)
+    x = torch.from_numpy(np.ascontiguousarray(inp.x)).to("cuda").to(torch.bfloat16)
+    d = torch.from_numpy(dy).to("cuda").to(torch.bfloat16)
+
+    def step():
+        layer.zero_grad()
+        layer.forward(x, train=True)
+        dx = layer.backward(d)
+        torch.cuda.synchronize()
+        return dx.clone(), [t.clone() for t in layer.get_gradients()]
+
+    dx0, g0 = step()
+    for i in range(20):
+        dx, g = step()
+        assert torch.equal(dx, dx0), i
+        assert all(torch.equal(a, b) for a, b in zip(g, g0)), i
+    layer.set_profiling(True)
+    dxs, gs = step()
+    layer.set_profiling(False)
+    assert all(torch.equal(a, b) for a, b in zip(gs, g0))
+    rel, mx = rel_errors(dxs.float().cpu().numpy(), dx0.float().cpu().numpy())
+    assert rel <= 4e-3 and mx <= 4e-3, (rel, mx)
+
+
 @pytest.mark.parametrize("act", ["f32", "bf16"])
 def test_backward_after_zero_grad_overwrites_stale_gradients(act):
     """zero_grad only marks the gradients zero; the next backward writes
