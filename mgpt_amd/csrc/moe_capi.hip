@@ -400,8 +400,10 @@ int ensure_grad(mgpt_moe* h) {
   h->grad_zero = true;
   if (!h->side) {
     HIP_TRY(hipStreamCreateWithFlags(&h->side, hipStreamNonBlocking));
-    HIP_TRY(hipEventCreateWithFlags(&h->fork_ev, hipEventDisableTiming));
-    HIP_TRY(hipEventCreateWithFlags(&h->join_ev, hipEventDisableTiming));
+    // device-scope ordering between the two streams only: no system-scope
+    // fence (cache write-back and invalidate) at each record
+    HIP_TRY(hipEventCreateWithFlags(&h->fork_ev, hipEventDisableTiming | hipEventDisableSystemFence));
+    HIP_TRY(hipEventCreateWithFlags(&h->join_ev, hipEventDisableTiming | hipEventDisableSystemFence));
   }
   return MGPT_OK;
 }
