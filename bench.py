@@ -209,6 +209,19 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
     drv = os.path.join(ROOT, "oracle", "_ref", "ref_driver")
     if not os.path.exists(drv):
         return None
+    # the x86-64-v4 (AVX-512) build where this host has every v4 feature
+    build = "x86-64-v3 (AVX2) build"
+    try:
+        flags = set()
+        for l in open("/proc/cpuinfo"):
+            if l.startswith("flags"):
+                flags = set(l.split(":", 1)[1].split())
+                break
+        v4 = os.path.join(ROOT, "oracle", "_ref", "ref_driver_v4")
+        if {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags and os.path.exists(v4):
+            drv, build = v4, "x86-64-v4 (AVX-512) build"
+    except OSError:
+        pass
     sub = {"forward": "bench", "train": "bench_train", "block": "bench_block"}[mode]
     what = {"forward": "MoELayer::forward_into",
             "train": "Tensor::zero_grad + MoELayer::forward_into + backward_into",
@@ -229,7 +242,7 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
         "kind": "reference",
         "sample": (f"{sample_tokens} of {cfg.N} tokens at the workload's shape "
                    f"(C={cfg.C}, E={cfg.E}, k={cfg.k}, H={cfg.H}), fp32 reference CPU path "
-                   f"({what}), "
+                   f"({what}), {build}, "
                    f"1 warmup + median of {reps}; "
                    f"1 thread of {os.cpu_count()} visible cores, {model}"),
         "median_s": res["median_s"],
