@@ -330,6 +330,53 @@ def test_bf16_gemm_shapes(N, Cm, H, E, k):
     check_close(y[rows], O.tokens(inp, ref["idx"], ref["topp"], rows), TOL["bf16"], cfg.name)
 
 
+FORCED_ROUTING = [
+    # (name, N, E, k): routing forced through the router weights so that every
+    # expert segment ends exactly on a 256-row tile boundary, or all rows go to
+    # one expert and the others get none; bf16 on the direct-to-LDS GEMMs
+    ("exact_tiles_k1", 4096, 8, 1),     # 512 rows per expert
+    ("exact_tiles_k2", 4096, 8, 2),     # 4096, 1024 and 512 rows (second choice: lowest tied id)
+    ("one_expert", 4096, 8, 1),         # 4096 rows for expert 5, none for the rest
+]
+
+
+@pytest.mark.parametrize("name,N,E,k", FORCED_ROUTING)
+def test_forced_routing_tile_boundaries(name, N, E, k):
+    """Segments that fill whole 256-row tiles (no ragged last tile) and a
+    single non-empty expert: the tile bookkeeping's boundary cases.  Token
+    t's first E features are the one-hot vector of t % E (the rest random),
+    and W_r = 10 * I on those features, so its logits are exactly 10 for
+    expert t % E and exactly 0 for the others (ties broken by the lower id);
+    for one_expert W_r = 0 and the bias picks expert 5."""
+    Cm, H = 256, 256
+    cfg = wl.MoEConfig(f"forced_{name}", N, Cm, E, k, H, "bf16", "bf16", "zero")
+    inp = wl.make_inputs(cfg, C.SEED + 7, bias_std=0.02)
+    inp.x[:] = wl.bf16_round(inp.x)
+    inp.Wr[:] = 0.0
+    inp.br[:] = 0.0
+    if name == "one_expert":
+        inp.br[5] = 5.0
+        want = np.zeros(E, np.int64)
+        want[5] = N
+    else:
+        t = np.arange(N)
+        inp.x[:, :E] = 0.0
+        inp.x[t, t % E] = 1.0
+        inp.Wr[np.arange(E), np.arange(E)] = 10.0
+        want = np.bincount(t % E, minlength=E)
+        if k == 2:
+            second = np.where(t % E == 0, 1, 0)
+            want = want + np.bincount(second, minlength=E)
+    layer, y, r, _, _ = run_gpu(inp)
+    ref = O.forward(inp, with_y=False)
+    assert np.array_equal(ref["counts"], want), ref["counts"]
+    assert np.array_equal(r["counts"], ref["counts"]), "counts"
+    assert np.array_equal(r["topk_idx"], ref["idx"]), "topk_idx"
+    assert np.array_equal(r["perm"], ref["perm"]), "perm"
+    rows = C.sample_rows(N, 128)
+    check_close(y[rows], O.tokens(inp, ref["idx"], ref["topp"], rows), TOL["bf16"], cfg.name)
+
+
 DECODE_SHAPES = [
     # (N, C, H, E, k): fp8-weight decode shapes (N*k < 64*E), on the
     # weight-streaming GEMM where C % 128 == 0: experts with more than one 32-row m-tile, many
