@@ -99,6 +99,32 @@ def test_backward_parity(name):
     check_all(out, ref, TOL[case.cfg.act], name)
 
 
+@pytest.mark.parametrize("name,k", [("exact_tiles_k2", 2), ("one_expert", 1)])
+def test_backward_forced_routing(name, k):
+    """The backward on routing forced as in the forward's tile-boundary test
+    (tests/test_gpu_parity.py): expert segments that end on 256-row tile
+    boundaries, or every row in one expert, which the weight gradients then
+    cut into several row chunks alone.  Against the oracle's backward."""
+    from mgpt_amd import workload as wl
+    N, Cm, H, E = 4096, 256, 256, 8
+    cfg = wl.MoEConfig(f"forced_bwd_{name}", N, Cm, E, k, H, "bf16", "bf16", "zero")
+    inp = wl.make_inputs(cfg, C.SEED + 7, bias_std=0.02)
+    inp.x[:] = wl.bf16_round(inp.x)
+    inp.Wr[:] = 0.0
+    inp.br[:] = 0.0
+    if name == "one_expert":
+        inp.br[5] = 5.0
+    else:
+        t = np.arange(N)
+        inp.x[:, :E] = 0.0
+        inp.x[t, t % E] = 1.0
+        inp.Wr[np.arange(E), np.arange(E)] = 10.0
+    dy = wl.bf16_round(np.random.default_rng(9).standard_normal((N, Cm)).astype(np.float32))
+    out = run_backward(make_layer(inp), inp, dy)
+    ref = O.backward(inp, dy)
+    check_all(out, ref, TOL["bf16"], cfg.name)
+
+
 def test_backward_cfg2_against_reference_fixture():
     """cfg2 (bf16, 8192 tokens, 8 experts, H = 1376): sampled dx rows and
     gradient entries against the reference's own backward."""
