@@ -18,9 +18,13 @@
  *     of the differentiated loss, plus softmax-Jacobian and routing
  *     invariants.  The ORACLE_PLANT_* macros each build a copy with one
  *     plausible mistake (dropped load-balance term, wrong sign in the SiLU
- *     derivative, ungated expert gradient); the tests build those copies
+ *     derivative, ungated expert gradient, dgamma without x_hat, the RMSNorm
+ *     backward without its projection term); the tests build those copies
  *     and show that both the golden and the finite-difference checks
- *     reject them.  The shipped build defines none of them.
+ *     reject them.  The shipped build defines none of them;
+ *   - block backward (tests/test_oracle_block.py): bit-for-bit against the
+ *     reference's TransformerBlock MoE half (ln2 + MoE + residual backward),
+ *     and dx1 / dgamma against float64 finite differences.
  */
 #include "moe_oracle.h"
 #include <math.h>
@@ -459,6 +463,40 @@ void oracle_rmsnorm_scaled(int N, int C, float eps, const float* x, const float*
   }
 }
 
+/* utils/Tensor.cpp:1665-1689 (rms_norm_backward_into, CPU branch), as
+ * called by RMSNormLayer::backward_into (layers/RMSNormLayer.cpp:30-33):
+ * per token, in column order, dh = dout*scale; dscale += dout*x_hat (added
+ * token by token); s = sum dh*x_hat; then dx = r*(dh - x_hat*s/C).  dx may
+ * alias dout (the engine passes the same buffer): every column of a row is
+ * read before any is written. */
+void oracle_rmsnorm_backward(int N, int C, const float* dout, const float* x_hat,
+                             const float* scale, const float* rstd, float* dx, float* dscale) {
+  for (int i = 0; i < N; ++i) {
+    const float* d = dout + (size_t)i * C;
+    const float* xh = x_hat + (size_t)i * C;
+    float* o = dx + (size_t)i * C;
+    const float r = rstd[i];
+    float s = 0.0f;
+    for (int c = 0; c < C; ++c) {
+      const float dh = d[c] * scale[c];
+#ifndef ORACLE_PLANT_DSCALE_UNHATTED
+      dscale[c] += d[c] * xh[c];
+#else
+      dscale[c] += d[c];
+#endif
+      s += dh * xh[c];
+    }
+    for (int c = 0; c < C; ++c) {
+      const float dh = d[c] * scale[c];
+#ifndef ORACLE_PLANT_NORM_NO_PROJECTION
+      o[c] = r * (dh - xh[c] * s / C);
+#else
+      o[c] = r * dh;
+#endif
+    }
+  }
+}
+
 /* layers/TransformerBlock.cpp:42-46: ln2.forward_into(x1, xn),
  * mlp.forward_into(xn, y), Tensor::add_into(x1, y, out) (utils/Tensor.cpp:
  * 1579-1597: out = x1 + y elementwise). */
@@ -477,5 +515,38 @@ int oracle_moe_block(int N, int C, int H, int E, int k, float eps, const float* 
     for (size_t i = 0; i < (size_t)N * C; ++i) out[i] = x1[i] + Y[i];
   if (!xn) free(XN);
   free(Y);
+  return rc;
+}
+
+/* layers/TransformerBlock.cpp:81-85 (backward_into, the MoE half): with
+ * xn = ln2(x1) from the forward, mlp.backward_into(dout, d_ln2),
+ * ln2.backward_into(d_ln2, d_ln2) and Tensor::add_into(dout, d_ln2, d_x1)
+ * (utils/Tensor.cpp:1579-1597: a + b elementwise).  x_hat = x1 * r as
+ * rms_norm_into caches it (utils/Tensor.cpp:796-797).  The MoE parameter
+ * gradients and dgamma are ACCUMULATED (add_grad / scale.grad +=), as in
+ * oracle_moe_backward; dx1 is written. */
+int oracle_moe_block_backward(int N, int C, int H, int E, int k, float eps, const float* x1,
+                              const float* gamma, const float* Wr, const float* br,
+                              const float* Wg, const float* bg, const float* Wu,
+                              const float* bu, const float* Wd, const float* bd,
+                              const float* dout, float* dx1, float* dgamma, float* dWr,
+                              float* dbr, float* dWg, float* dbg, float* dWu, float* dbu,
+                              float* dWd, float* dbd) {
+  if (N < 0 || C <= 0) return 1;
+  const size_t NC = (size_t)N * C;
+  float* XN = (float*)malloc(sizeof(float) * (NC + 1));
+  float* XH = (float*)malloc(sizeof(float) * (NC + 1));
+  float* R = (float*)malloc(sizeof(float) * ((size_t)N + 1));
+  float* D = (float*)malloc(sizeof(float) * (NC + 1));
+  oracle_rmsnorm_scaled(N, C, eps, x1, gamma, XN, R);
+  for (int i = 0; i < N; ++i)
+    for (int c = 0; c < C; ++c) XH[(size_t)i * C + c] = x1[(size_t)i * C + c] * R[i];
+  int rc = oracle_moe_backward(N, C, H, E, k, XN, Wr, br, Wg, bg, Wu, bu, Wd, bd, dout, D, dWr,
+                               dbr, dWg, dbg, dWu, dbu, dWd, dbd);
+  if (rc == 0) {
+    oracle_rmsnorm_backward(N, C, D, XH, gamma, R, D, dgamma);
+    for (size_t i = 0; i < NC; ++i) dx1[i] = dout[i] + D[i];
+  }
+  free(XN); free(XH); free(R); free(D);
   return rc;
 }

@@ -91,6 +91,23 @@ int oracle_moe_block(int N, int C, int H, int E, int k, float eps, const float* 
                      const float* bd, float* out, float* xn, float* rstd, int32_t* idx,
                      float* topp, int32_t* counts, int32_t* perm);
 
+/* RMSNormLayer backward (eps-independent): dx[N,C] from dout, the cached
+ * x_hat = x * rstd and scale; dscale[C] is ACCUMULATED.  dx may alias
+ * dout. */
+void oracle_rmsnorm_backward(int N, int C, const float* dout, const float* x_hat,
+                             const float* scale, const float* rstd, float* dx, float* dscale);
+
+/* Backward of oracle_moe_block for the upstream gradient dout of out:
+ * dx1[N,C] is written (dout + the ln2 branch); dgamma[C] and the MoE
+ * parameter gradients are ACCUMULATED as in oracle_moe_backward. */
+int oracle_moe_block_backward(int N, int C, int H, int E, int k, float eps, const float* x1,
+                              const float* gamma, const float* Wr, const float* br,
+                              const float* Wg, const float* bg, const float* Wu,
+                              const float* bu, const float* Wd, const float* bd,
+                              const float* dout, float* dx1, float* dgamma, float* dWr,
+                              float* dbr, float* dWg, float* dbg, float* dWu, float* dbu,
+                              float* dWd, float* dbd);
+
 /* x_hat[N,C] = RMSNorm(x) with gamma = 1 (input preparation, a1). */
 void oracle_rmsnorm(int N, int C, float eps, const float* x, float* out);
 

@@ -9,6 +9,7 @@
 //   ref_driver run  <in.bin> <out.bin>
 //   ref_driver backward <in.bin> <dy.bin> <grad.bin>
 //   ref_driver block <in.bin> <gamma.bin> <out.bin>
+//   ref_driver block_backward <in.bin> <gamma.bin> <dy.bin> <grad.bin>
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
 //   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (zero_grad + forward + backward)
 //   ref_driver bench_block <N> <C> <H> <E> <k> <reps>   (ln2 + MoE + residual)
@@ -29,6 +30,10 @@
 //          (x1 + MoE(ln2(x1)), layers/TransformerBlock.cpp:42-46), float32
 //          xn[N*C] (ln2's output), float32 rstd[N] (its cached_rsqrt),
 //          int32 idx[N*k], float32 topp[N*k], int32 counts[E], int32 perm[N*k].
+// block_backward: x of in.bin is x1 and dy.bin the upstream gradient of
+//          out; grad.bin: "MGPTBBK1", int32 N C H E k, float32 dx1[N*C],
+//          the ln2 scale's .grad [C], then the MoE parameters' .grad as in
+//          grad.bin below.
 // grad.bin: "MGPTGRD1", int32 N C H E k, float32 dx[N*C], then the .grad of
 //          every parameter in get_parameters() order (sizes as in in.bin),
 //          after one forward_into and one backward_into
@@ -254,6 +259,59 @@ int block(const char* in_path, const char* g_path, const char* out_path) {
   return 0;
 }
 
+// The MoE half of TransformerBlock::backward_into (layers/TransformerBlock.
+// cpp:81-85) after its forward (:42-46) on a fresh ln2 RMSNormLayer and
+// MoELayer: mlp.backward_into(dout, d_ln2), ln2.backward_into(d_ln2, d_ln2)
+// (the same buffer, as there), Tensor::add_into(dout, d_ln2, d_x1).
+int block_backward(const char* in_path, const char* g_path, const char* dy_path,
+                   const char* out_path) {
+  int32_t dims[5];
+  Tensor x1;
+  std::unique_ptr<MoELayer> owner;
+  if (int rc = load(in_path, dims, x1, owner)) return rc;
+  MoELayer& layer = *owner;
+  const int N = dims[0], C = dims[1];
+  RMSNormLayer ln2(C);
+  Tensor& scale = *ln2.get_parameters()[0];
+  FILE* f = std::fopen(g_path, "rb");
+  if (!f) { std::perror(g_path); return 2; }
+  if (!read_exact(f, scale.data.data(), sizeof(float) * C)) return 3;
+  std::fclose(f);
+  Tensor dout({1, N, C}, 0.0f, Device::CPU);
+  f = std::fopen(dy_path, "rb");
+  if (!f) { std::perror(dy_path); return 2; }
+  if (!read_exact(f, dout.data.data(), sizeof(float) * (size_t)N * C)) return 3;
+  std::fclose(f);
+
+  Tensor xn, y, out, d_ln2, d_x1;
+  ln2.forward_into(x1, xn);
+  layer.forward_into(xn, y);
+  Tensor::add_into(x1, y, out);
+  layer.backward_into(dout, d_ln2);
+  ln2.backward_into(d_ln2, d_ln2);
+  Tensor::add_into(dout, d_ln2, d_x1);
+
+  if (scale.grad.size() != scale.size()) {
+    std::fprintf(stderr, "ln2 scale without a gradient buffer\n");
+    return 4;
+  }
+  FILE* o = std::fopen(out_path, "wb");
+  if (!o) { std::perror(out_path); return 2; }
+  std::fwrite("MGPTBBK1", 1, 8, o);
+  std::fwrite(dims, sizeof(int32_t), 5, o);
+  std::fwrite(d_x1.data.data(), sizeof(float), (size_t)N * C, o);
+  std::fwrite(scale.grad.data(), sizeof(float), C, o);
+  for (Tensor* p : layer.get_parameters()) {
+    if (p->grad.size() != p->size()) {
+      std::fprintf(stderr, "parameter without a gradient buffer\n");
+      return 4;
+    }
+    std::fwrite(p->grad.data(), sizeof(float), p->size(), o);
+  }
+  std::fclose(o);
+  return 0;
+}
+
 // Times MoELayer::forward_into (train: forward_into then backward_into with
 // dout ~ N(0,1); block: ln2 RMSNormLayer, MoELayer and the residual
 // Tensor::add_into of layers/TransformerBlock.cpp:42-46) on one fresh layer
@@ -393,6 +451,8 @@ int main(int argc, char** argv) {
   if (argc == 4 && std::string(argv[1]) == "run") return run(argv[2], argv[3]);
   if (argc == 5 && std::string(argv[1]) == "backward") return backward(argv[2], argv[3], argv[4]);
   if (argc == 5 && std::string(argv[1]) == "block") return block(argv[2], argv[3], argv[4]);
+  if (argc == 6 && std::string(argv[1]) == "block_backward")
+    return block_backward(argv[2], argv[3], argv[4], argv[5]);
   if (argc == 7 && std::string(argv[1]) == "train")
     return train(argv[2], argv[3], argv[4], std::atoi(argv[5]), (float)std::atof(argv[6]));
   if (argc == 9 && std::string(argv[1]) == "gptlogits")

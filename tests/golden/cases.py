@@ -124,6 +124,9 @@ TRAIN_LR = 1e-3
 BLOCK_CASES = ["small_f32", "ragged_k3", "k8_bf16", "bf16_large_m", "fp8_small", "cfg1", "cfg3",
                "cfg5"]
 BLOCK_EPS = 1e-5   # the engine's RMSNormLayer default (layers/RMSNormLayer.h:23)
+# Cases of the fused block's backward (tests/golden/block_backward/): the
+# trainable block cases (weights in the activation dtype), dout = build_dy.
+BLOCK_BACKWARD_CASES = ["small_f32", "ragged_k3", "k8_bf16", "bf16_large_m", "cfg1"]
 
 
 def build_block_inputs(case: Case):

@@ -29,6 +29,13 @@ Tensor::add_into (ref_driver block) on cases.BLOCK_CASES with
 tests/golden/block/<case>.npz with sha256 digests of out, xn, rstd, idx,
 topp, perm, the counts, sampled rows of out and xn, and rstd in full.
 
+With --block-backward it runs the MoE half of the reference's
+TransformerBlock::backward_into after its forward (ref_driver block_backward:
+mlp.backward_into, ln2.backward_into, Tensor::add_into) on
+cases.BLOCK_BACKWARD_CASES with dout = cases.build_dy(case), and stores
+tests/golden/block_backward/<case>.npz with sha256 digests and samples of
+dx1, the ln2 scale gradient (in full) and the 2 + 6E MoE gradients.
+
 With --gptbin it has the reference write a small MoE GPT checkpoint with its
 own GPT::save_weights_bin (ref_driver gptbin; cases.GPTBIN's dimensions,
 seeded parameters) and stores tests/golden/gptbin/small.npz with the file's
@@ -45,7 +52,8 @@ tests/golden/train/<case>.npz with the outputs y of every forward in full
 and, per step, sha256 digests and sampled flat entries of every parameter
 after the step (at the flat indices cases.sample_flat(size, 64)).
 
-Usage: python tests/golden/make_golden.py [--backward | --block | --gptbin | --train] [case ...]
+Usage: python tests/golden/make_golden.py [--backward | --block | --block-backward | --gptbin |
+       --train] [case ...]
 (default: all cases)
 """
 from __future__ import annotations
@@ -229,6 +237,72 @@ def make_block(case: C.Case) -> None:
     print(f"{case.name} block ({time.time() - t0:.1f}s)", flush=True)
 
 
+def run_reference_block_backward(inp: wl.MoEInputs, gamma: np.ndarray,
+                                 dy: np.ndarray) -> dict:
+    cfg = inp.cfg
+    N, Cc, H, E = cfg.N, cfg.C, cfg.H, cfg.E
+    with tempfile.TemporaryDirectory() as d:
+        ip, gp, dp, op = (os.path.join(d, n) for n in ("in.bin", "gamma.bin", "dy.bin",
+                                                        "grad.bin"))
+        write_input(ip, inp)
+        np.ascontiguousarray(gamma, np.float32).tofile(gp)
+        np.ascontiguousarray(dy, dtype=np.float32).tofile(dp)
+        subprocess.run([REF, "block_backward", ip, gp, dp, op], check=True)
+        raw = open(op, "rb").read()
+    assert raw[:8] == b"MGPTBBK1", "bad reference block gradient file"
+    off = 8 + 5 * 4
+
+    def take(n):
+        nonlocal off
+        a = np.frombuffer(raw, dtype=np.float32, count=n, offset=off).copy()
+        off += 4 * n
+        return a
+
+    out = {"dx": take(N * Cc).reshape(N, Cc), "dgamma": take(Cc),
+           "dWr": take(Cc * E).reshape(Cc, E), "dbr": take(E)}
+    per = {n: [] for n in GRAD_NAMES[2:]}
+    for _ in range(E):
+        per["dWg"].append(take(Cc * H).reshape(Cc, H))
+        per["dbg"].append(take(H))
+        per["dWu"].append(take(Cc * H).reshape(Cc, H))
+        per["dbu"].append(take(H))
+        per["dWd"].append(take(H * Cc).reshape(H, Cc))
+        per["dbd"].append(take(Cc))
+    assert off == len(raw), "trailing bytes in the reference block gradient file"
+    for n, v in per.items():
+        out[n] = np.stack(v)
+    return out
+
+
+def make_block_backward(case: C.Case) -> None:
+    """tests/golden/block_backward/<case>.npz: digests and samples of dx1,
+    dgamma and the 2 + 6E MoE gradients of the reference's block backward
+    (ref_driver block_backward) on (x1, gamma) = cases.build_block_inputs
+    and dout = cases.build_dy."""
+    t0 = time.time()
+    inp, x1, gamma = C.build_block_inputs(case)
+    cfg = inp.cfg
+    blk_inp = wl.MoEInputs(cfg, x1, inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu, inp.Wd,
+                           inp.bd, inp.raw)
+    ref = run_reference_block_backward(blk_inp, gamma, C.build_dy(case))
+    rows = C.sample_rows(cfg.N)
+    fx = {"rows": rows, "dx_rows": ref["dx"][rows], "dgamma": ref["dgamma"],
+          "sha_dx": np.array(canonical_digest(ref["dx"])),
+          "sha_dgamma": np.array(canonical_digest(ref["dgamma"]))}
+    total = 0
+    for n in GRAD_NAMES:
+        g = ref[n]
+        total += g.size
+        at = C.sample_flat(g.size)
+        fx["sha_" + n] = np.array(canonical_digest(g))
+        fx[n + "_at"] = at
+        fx[n + "_val"] = g.reshape(-1)[at]
+    os.makedirs(os.path.join(HERE, "block_backward"), exist_ok=True)
+    np.savez_compressed(os.path.join(HERE, "block_backward", case.name + ".npz"), **fx)
+    print(f"{case.name} block backward: {total} gradient values ({time.time() - t0:.1f}s)",
+          flush=True)
+
+
 def make_gptbin() -> None:
     g = C.GPTBIN
     with tempfile.TemporaryDirectory() as d:
@@ -340,6 +414,10 @@ def main(argv):
     if argv and argv[0] == "--block":
         for n in argv[1:] or C.BLOCK_CASES:
             make_block(C.ALL_CASES[n])
+        return
+    if argv and argv[0] == "--block-backward":
+        for n in argv[1:] or C.BLOCK_BACKWARD_CASES:
+            make_block_backward(C.ALL_CASES[n])
         return
     names = argv or list(C.ALL_CASES)
     for n in names:

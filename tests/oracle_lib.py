@@ -44,6 +44,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_rmsnorm_scaled.argtypes = [i, i, ctypes.c_float, vp, vp, vp, vp]
         L.oracle_moe_block.argtypes = [i] * 5 + [ctypes.c_float] + [vp] * 17
         L.oracle_moe_block.restype = i
+        L.oracle_rmsnorm_backward.argtypes = [i, i] + [vp] * 6
+        L.oracle_moe_block_backward.argtypes = [i] * 5 + [ctypes.c_float] + [vp] * 21
+        L.oracle_moe_block_backward.restype = i
         _LIB = L
     return _LIB
 
@@ -154,6 +157,9 @@ def load_variant(path: str) -> ctypes.CDLL:
     L = ctypes.CDLL(path)
     L.oracle_moe_backward.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p] * 19
     L.oracle_moe_backward.restype = ctypes.c_int
+    L.oracle_moe_block_backward.argtypes = ([ctypes.c_int] * 5 + [ctypes.c_float] +
+                                            [ctypes.c_void_p] * 21)
+    L.oracle_moe_block_backward.restype = ctypes.c_int
     return L
 
 
@@ -198,6 +204,34 @@ def block(inp, x1, gamma, eps=1e-5) -> dict:
     rc = lib().oracle_moe_block(N, C, H, E, k, eps, _p(x1), _p(gamma), *[_p(a) for a in arrs],
                                 *[_p(out[n]) for n in ("out", "xn", "rstd", "idx", "topp",
                                                        "counts", "perm")])
+    assert rc == 0
+    return out
+
+
+def rmsnorm_backward(dout, x_hat, gamma, rstd):
+    """(dx, dgamma) of the engine's RMSNormLayer backward (dgamma from zero)."""
+    dout, x_hat, gamma, rstd = _f32(dout), _f32(x_hat), _f32(gamma), _f32(rstd)
+    N, C = dout.shape
+    dx = np.empty_like(dout)
+    dgamma = np.zeros(C, np.float32)
+    lib().oracle_rmsnorm_backward(N, C, _p(dout), _p(x_hat), _p(gamma), _p(rstd), _p(dx),
+                                  _p(dgamma))
+    return dx, dgamma
+
+
+def block_backward(inp, x1, gamma, dout, eps=1e-5, library=None) -> dict:
+    """Backward of the fused block for upstream dout: dx [N,C] (= dx1),
+    dgamma [C] and the MoE parameter gradients of one call (zero-started)."""
+    cfg = inp.cfg
+    N, C, H, E, k = cfg.N, cfg.C, cfg.H, cfg.E, cfg.k
+    x1, gamma, dout = _f32(x1), _f32(gamma), _f32(dout)
+    arrs = [_f32(a) for a in (inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu, inp.Wd, inp.bd)]
+    out = {"dx": np.empty((N, C), np.float32), "dgamma": np.zeros(C, np.float32)}
+    for name, a in zip(GRAD_NAMES, arrs):
+        out[name] = np.zeros(a.shape, np.float32)
+    rc = (library or lib()).oracle_moe_block_backward(
+        N, C, H, E, k, eps, _p(x1), _p(gamma), *[_p(a) for a in arrs], _p(dout), _p(out["dx"]),
+        _p(out["dgamma"]), *[_p(out[n]) for n in GRAD_NAMES])
     assert rc == 0
     return out
 

@@ -11,7 +11,22 @@ trusted.
 2. Mathematics: gamma = 1 equals the unscaled restatement; a power-of-two
    gamma scales the output exactly; a constant row a has 1/rms =
    1/sqrt(a^2 + eps); rows of any scale normalise to RMS 1 (up to eps).
+
+The block backward (oracle_moe_block_backward: the MoE half of
+TransformerBlock::backward_into, layers/TransformerBlock.cpp:81-85) and its
+RMSNorm backward (oracle_rmsnorm_backward, utils/Tensor.cpp:1665-1689):
+
+3. Golden vectors: bit-for-bit agreement of dx1, the ln2 scale gradient and
+   every MoE gradient with the reference (ref_driver block_backward) on
+   every fixture in tests/golden/block_backward/.
+4. Mathematics: float64 central finite differences of the block's loss
+   sum(dout * out) + the MoE load-balance term (the loss the reference
+   differentiates) in x1 and gamma; the scale invariance of RMSNorm makes
+   the normalisation's input gradient orthogonal to x up to eps.
+5. Planted mistakes (dgamma without x_hat; the backward without its
+   projection term) fail both checks.
 """
+import subprocess
 import glob
 import os
 
@@ -24,6 +39,9 @@ from mgpt_amd import workload as wl
 
 BLK = os.path.join(os.path.dirname(__file__), "golden", "block")
 FIXTURES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(BLK, "*.npz")))
+BBK = os.path.join(os.path.dirname(__file__), "golden", "block_backward")
+BWD_FIXTURES = sorted(os.path.basename(p)[:-4] for p in glob.glob(os.path.join(BBK, "*.npz")))
+BWD_NAMES = ("dx", "dgamma") + O.GRAD_NAMES
 
 
 def canonical_digest(a):
@@ -98,3 +116,111 @@ def test_rmsnorm_closed_forms():
     rms = np.sqrt(np.mean(n1.astype(np.float64) ** 2, axis=1))
     ms = np.mean(xs.astype(np.float64) ** 2, axis=1)
     assert np.allclose(rms, np.sqrt(ms / (ms + 1e-5)), rtol=1e-5)
+
+
+# ------------------------------------------------------------ block backward
+def _block_backward_case(name, library=None):
+    case = C.ALL_CASES[name]
+    inp, x1, gamma = C.build_block_inputs(case)
+    return O.block_backward(inp, x1, gamma, C.build_dy(case), C.BLOCK_EPS, library)
+
+
+def test_every_block_backward_case_has_a_fixture():
+    assert sorted(C.BLOCK_BACKWARD_CASES) == BWD_FIXTURES
+
+
+@pytest.mark.parametrize("name", BWD_FIXTURES)
+def test_block_backward_matches_reference(name):
+    fx = np.load(os.path.join(BBK, name + ".npz"), allow_pickle=False)
+    out = _block_backward_case(name)
+    for n in BWD_NAMES:
+        assert canonical_digest(out[n]) == str(fx["sha_" + n]), n
+    assert same_bits(out["dgamma"], fx["dgamma"])
+    assert same_bits(out["dx"][fx["rows"]], fx["dx_rows"])
+    for n in O.GRAD_NAMES:
+        assert same_bits(out[n].reshape(-1)[fx[n + "_at"]], fx[n + "_val"]), n
+
+
+def _fd_block_mismatches(library=None):
+    """Names among dx, dgamma and dWr on which the oracle (or a planted
+    copy) disagrees with float64 central differences of the block loss."""
+    from test_oracle_backward import _loss64, _small_problem
+    inp, dout = _small_problem(seed=11)
+    cfg = inp.cfg
+    N, Cc = inp.x.shape
+    rng = np.random.default_rng(12)
+    x1 = (inp.x * rng.uniform(0.5, 3.0, (N, 1))).astype(np.float32)
+    gamma = (1.0 + 0.2 * rng.standard_normal(Cc)).astype(np.float32)
+    eps = 1e-5
+    fwd = O.block(inp, x1, gamma, eps)
+    out = O.block_backward(inp, x1, gamma, dout, eps, library)
+    counts = fwd["counts"].astype(np.float64)
+    W = [np.asarray(a, np.float64) for a in (inp.Wr, inp.br, inp.Wg, inp.bg, inp.Wu, inp.bu,
+                                            inp.Wd, inp.bd)]
+    d64 = dout.astype(np.float64)
+
+    def loss(xv, gv, Wr):
+        r = 1.0 / np.sqrt(np.mean(xv * xv, axis=1, keepdims=True) + eps)
+        moe, P, idx = _loss64([xv * r * gv, Wr] + W[1:], d64, cfg.k, counts)
+        return float(np.sum(d64 * xv)) + moe, P, idx
+
+    x64, g64, wr64 = x1.astype(np.float64), gamma.astype(np.float64), W[0].copy()
+    _, P, idx = loss(x64, g64, wr64)
+    assert np.array_equal(np.sort(idx, 1), np.sort(fwd["idx"], 1))
+    srt = -np.sort(-P, axis=1)
+    assert np.min(srt[:, cfg.k - 1] - srt[:, cfg.k]) > 1e-3   # no routing flip under h
+    h = 1e-6
+    bad = []
+    for name, arr in (("dx", x64), ("dgamma", g64), ("dWr", wr64)):
+        flat = arr.reshape(-1)
+        fd = np.empty(flat.size)
+        for i in range(flat.size):
+            keep = flat[i]
+            flat[i] = keep + h
+            lp = loss(x64, g64, wr64)[0]
+            flat[i] = keep - h
+            lm = loss(x64, g64, wr64)[0]
+            flat[i] = keep
+            fd[i] = (lp - lm) / (2 * h)
+        got = np.asarray(out[name], np.float64).reshape(-1)
+        scale = max(1.0, float(np.max(np.abs(fd))))
+        if not np.allclose(got, fd, rtol=2e-4, atol=2e-5 * scale):
+            bad.append(name)
+    return bad
+
+
+def test_block_backward_matches_finite_differences():
+    assert _fd_block_mismatches() == []
+
+
+def test_rmsnorm_backward_is_orthogonal_to_the_input():
+    # RMSNorm(a x) = RMSNorm(x) up to eps, so the input gradient has no
+    # component along x: sum_c dx_c x_c = r (sum_c dh_c x_c) eps / (ms + eps).
+    x = wl.normal_f32(8, 1, 16 * 256).reshape(16, 256) * np.float32(2.0)
+    g = np.float32(1.0) + np.float32(0.2) * wl.normal_f32(9, 1, 256)
+    d = wl.normal_f32(10, 1, 16 * 256).reshape(16, 256)
+    _, r = O.rmsnorm_scaled(x, g)
+    xh = x * r[:, None]
+    dx, _ = O.rmsnorm_backward(d, xh, g, r)
+    along = np.sum(dx.astype(np.float64) * x, axis=1)
+    size = np.sum(np.abs(dx.astype(np.float64) * x), axis=1)
+    assert np.all(np.abs(along) < 1e-4 * size)
+    # and with the projection term dropped (a planted slip) it is not
+    assert np.max(np.abs(np.sum((d * g * r[:, None]).astype(np.float64) * x, axis=1))) > 1.0
+
+
+PLANTS_BLOCK = {"ORACLE_PLANT_DSCALE_UNHATTED": "dgamma", "ORACLE_PLANT_NORM_NO_PROJECTION": "dx"}
+
+
+@pytest.mark.parametrize("macro", sorted(PLANTS_BLOCK))
+def test_block_planted_mistakes_are_detected(macro, tmp_path):
+    so = tmp_path / "planted.so"
+    subprocess.run(["gcc", "-O2", "-ffp-contract=off", "-std=c11", "-fPIC", "-shared",
+                    "-D" + macro, "-o", str(so), os.path.join(O.ORACLE_DIR, "moe_oracle.c"),
+                    "-lm"], check=True)
+    planted = O.load_variant(str(so))
+    name = PLANTS_BLOCK[macro]
+    assert name in _fd_block_mismatches(planted)
+    fx = np.load(os.path.join(BBK, "ragged_k3.npz"), allow_pickle=False)
+    out = _block_backward_case("ragged_k3", planted)
+    assert canonical_digest(out[name]) != str(fx["sha_" + name])
