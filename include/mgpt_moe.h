@@ -208,6 +208,33 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens,
 int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* Training forward of the fused block: mgpt_moe_forward_block (out = x +
+ * MoE(RMSNorm(x) * gamma)) that also keeps the training caches of
+ * mgpt_moe_forward_train in `workspace` (>= train workspace bytes), next to
+ * the per-token 1/rms.  Replaces, for training, the ln2.forward_into,
+ * mlp.forward_into, Tensor::add_into sequence of
+ * TransformerBlock::forward_into (layers/TransformerBlock.cpp:42-46). */
+int mgpt_moe_forward_block_train(mgpt_moe* h, const void* x, const float* gamma, float eps,
+                                 void* out, int num_tokens, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/* Backward of the fused block after mgpt_moe_forward_block_train on the same
+ * x and gamma (passed again, unchanged) and the same num_tokens: for the
+ * upstream gradient dout of out, writes dx = dL/dx = dout + ln2's backward
+ * of the MoE input gradient, adds the ln2 scale's gradient into dgamma
+ * [C] fp32 (device; dgamma[c] += sum over tokens, as the reference adds
+ * into scale.grad) and the 2 + 6E MoE gradients into the handle's buffers
+ * as mgpt_moe_backward does (the router's weight gradient from the
+ * normalised rows).  Replaces mlp.backward_into, ln2.backward_into and
+ * Tensor::add_into(dout, d_ln2, d_x1) of TransformerBlock::backward_into
+ * (layers/TransformerBlock.cpp:81-85; RMSNormLayer::backward_into,
+ * utils/Tensor.cpp:1665-1689).  x, dout, dx are act_dtype [N,C]; dx must not
+ * overlap x or dout.  The sums over columns and tokens run in a fixed order
+ * of their own (deterministic), not the reference's sequential one. */
+int mgpt_moe_backward_block(mgpt_moe* h, const void* x, const float* gamma, const void* dout,
+                            void* dx, float* dgamma, int num_tokens, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Sets every gradient to zero on `stream`.  Replaces Tensor::zero_grad
  * (utils/Tensor.cpp:181-187) over this layer's parameters.  Eagerly, before
  * any backward has been captured, no memory is written: the gradients are

@@ -98,6 +98,8 @@ def lib() -> ctypes.CDLL:
         "mgpt_moe_backward_stage_times": [vp, vp, i],
         "mgpt_moe_forward_block": [vp, vp, vp, ctypes.c_float, vp, i, vp, sz, vp],
         "mgpt_moe_get_rstd": [vp, i, vp, ctypes.POINTER(vp)],
+        "mgpt_moe_forward_block_train": [vp, vp, vp, ctypes.c_float, vp, i, vp, sz, vp],
+        "mgpt_moe_backward_block": [vp, vp, vp, vp, vp, vp, i, vp, sz, vp],
         "mgpt_gpt_bin_inspect": [ctypes.c_char_p, i, i, ctypes.POINTER(GptBinInfo)],
         "mgpt_gpt_bin_read_block": [ctypes.c_char_p, i, i, i, vp, vp, sz],
         "mgpt_moe_load_gpt_bin": [vp, ctypes.c_char_p, i, vp, vp],

@@ -258,13 +258,17 @@ __device__ __forceinline__ void rw_load_cols(const float* p, float (&v)[CPT]) {
 // values are then zeroed, so the wait counts stay exact), and each
 // expert's CPT sums go out as one vector store, lanes on consecutive
 // columns.  The blocks of the first column range also write
-// partial_b[chunk][e] = sum_t dL[t][e].
-template <typename ActT, int EP, int CPT>
+// partial_b[chunk][e] = sum_t dL[t][e].  NRM (fused block): the router's
+// input is the normalised row, so x[t][c] is taken as (x[t][c] * rstd[t]) *
+// gamma[c], the fp32 values the router formed its logits from.
+template <typename ActT, int EP, int CPT, bool NRM>
 __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restrict__ x,
                                                            const float* __restrict__ dL, int N,
                                                            int C, int E,
                                                            float* __restrict__ partial,
-                                                           float* __restrict__ partial_b) {
+                                                           float* __restrict__ partial_b,
+                                                           const float* __restrict__ rstd,
+                                                           const float* __restrict__ gamma) {
   constexpr int kG = 8;   // tokens per load group
   static_assert(kRwChunk % (2 * kG) == 0, "whole group pairs per chunk");
   __shared__ float4 s_dl[kRwChunk][EP / 4];
@@ -290,9 +294,20 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
 #pragma unroll
     for (int e = 0; e < EP; ++e) acc[cc][e] = 0.0f;
   const ActT* xp = x + (size_t)t0 * C + c0;
+  float gm[CPT];
+#pragma unroll
+  for (int cc = 0; cc < CPT; ++cc) gm[cc] = NRM ? gamma[c0 + cc] : 1.0f;
   auto load = [&](int r0, float (&xv)[kG][CPT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int u = 0; u < kG; ++u) rw_load_cols<CPT>(xp + (size_t)min(r0 + u, nt - 1) * C, xv[u]);
+    for (int u = 0; u < kG; ++u) {
+      const int r = min(r0 + u, nt - 1);
+      rw_load_cols<CPT>(xp + (size_t)r * C, xv[u]);
+      if constexpr (NRM) {
+        const float rs = rstd[t0 + r];
+#pragma unroll
+        for (int cc = 0; cc < CPT; ++cc) xv[u][cc] = (xv[u][cc] * rs) * gm[cc];
+      }
+    }
   };
   auto fmas = [&](int r0, float (&xv)[kG][CPT]) __attribute__((always_inline)) {
 #pragma unroll
@@ -439,28 +454,203 @@ hipError_t launch_token_bwd(const ActT* dxe, const int32_t* slot_of, const int32
 
 int router_wgrad_chunks(int N) { return (N + kRwChunk - 1) / kRwChunk; }
 
-template <typename ActT>
-hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int E,
-                               float* partial, float* partial_b, float* gW, float* gb,
-                               bool store, hipStream_t stream) {
-  if (E <= 0 || E > kMaxExperts || C % 4) return hipErrorInvalidValue;
-  if (N <= 0) return hipSuccess;
-  const int chunks = router_wgrad_chunks(N);
+template <typename ActT, bool NRM>
+void launch_router_wgrad_products(const ActT* x, const float* dL, int N, int C, int E,
+                                  float* partial, float* partial_b, const float* rstd,
+                                  const float* gamma, int chunks, hipStream_t stream) {
   // a block covers 256 threads x CPT columns; E <= 32 takes two columns per
   // thread (at cfg3, E = 16, four columns per thread gave one wave per SIMD
   // and 42 us)
   if (E <= 16)
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16, 2>), dim3((C + 511) / 512, chunks),
-                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 16, 2, NRM>), dim3((C + 511) / 512, chunks),
+                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b, rstd, gamma);
   else if (E <= 32)
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32, 2>), dim3((C + 511) / 512, chunks),
-                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32, 2, NRM>), dim3((C + 511) / 512, chunks),
+                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b, rstd, gamma);
   else
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64, 1>), dim3((C + 255) / 256, chunks),
-                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b);
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64, 1, NRM>), dim3((C + 255) / 256, chunks),
+                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b, rstd, gamma);
+}
+
+// rstd / gamma (both null, or both set): the fused block's router input,
+// (x * rstd[t]) * gamma[c].
+template <typename ActT>
+hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int E,
+                               float* partial, float* partial_b, float* gW, float* gb,
+                               bool store, const float* rstd, const float* gamma,
+                               hipStream_t stream) {
+  if (E <= 0 || E > kMaxExperts || C % 4 || (!rstd) != (!gamma)) return hipErrorInvalidValue;
+  if (N <= 0) return hipSuccess;
+  const int chunks = router_wgrad_chunks(N);
+  if (rstd)
+    launch_router_wgrad_products<ActT, true>(x, dL, N, C, E, partial, partial_b, rstd, gamma,
+                                             chunks, stream);
+  else
+    launch_router_wgrad_products<ActT, false>(x, dL, N, C, E, partial, partial_b, nullptr,
+                                              nullptr, chunks, stream);
   const int CE = C * E;
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3((CE + E + 15) / 16), dim3(256), 0, stream,
                      partial, partial_b, chunks, C, E, gW, gb, (int)store);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Backward of the fused block's ln2 RMSNorm and residual (the MoE half of
+// TransformerBlock::backward_into, layers/TransformerBlock.cpp:81-85, with
+// RMSNormLayer::backward_into, utils/Tensor.cpp:1665-1689):
+//   x_hat = x * r, dh = d * gamma, s = sum_c dh * x_hat,
+//   dx1 = dout + r * (dh - x_hat * s / C),   dgamma[c] += sum_t d * x_hat,
+// with d the gradient of the normalised rows (the MoE backward's dx).  One
+// wave per kNbRows token rows: a pass over each row for s (lanes on
+// 16-byte column pieces, a wave sum), then a pass per column piece over the
+// wave's rows that writes dx1 in place of d and adds the rows' d * x_hat
+// into registers, stored as partial[wave][c]; rmsnorm_dgamma_reduce_kernel
+// adds the partials in wave order (deterministic).  Each lane reads its own
+// elements of d before it overwrites them, so d and dx1 share the buffer.
+constexpr int kNbRows = 16;
+
+template <typename ActT, int V> struct NbVec;
+template <> struct NbVec<bf16_t, 8> {
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
+    const uint4 q = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[8]) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+};
+template <> struct NbVec<float, 4> {
+  static __device__ __forceinline__ void load(const float* p, float (&v)[4]) {
+    const float4 q = *reinterpret_cast<const float4*>(p);
+    v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+  }
+  static __device__ __forceinline__ void store(float* p, const float (&v)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+};
+template <typename ActT> struct NbVec<ActT, 1> {
+  static __device__ __forceinline__ void load(const ActT* p, float (&v)[1]) { v[0] = to_f32(*p); }
+  static __device__ __forceinline__ void store(ActT* p, const float (&v)[1]) { store_act(p, v[0]); }
+};
+
+template <typename ActT, int V>
+__global__ __launch_bounds__(64) void rmsnorm_bwd_kernel(const ActT* __restrict__ x, ActT* d,
+                                                         const ActT* __restrict__ dout,
+                                                         const float* __restrict__ rstd,
+                                                         const float* __restrict__ gamma, int N,
+                                                         int C, float* __restrict__ partial) {
+  using Vec = NbVec<ActT, V>;
+  const int lane = lane_id();
+  const int t0 = blockIdx.x * kNbRows;
+  const int nt = min(kNbRows, N - t0);
+  float s[kNbRows];
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i) {
+    s[i] = 0.0f;
+    if (i >= nt) continue;
+    const float r = rstd[t0 + i];
+    const size_t row = (size_t)(t0 + i) * C;
+    float acc = 0.0f;
+    for (int c = lane * V; c < C; c += kWave * V) {
+      float xv[V], dv[V];
+      Vec::load(x + row + c, xv);
+      Vec::load(d + row + c, dv);
+#pragma unroll
+      for (int v = 0; v < V; ++v) acc = acc + (dv[v] * gamma[c + v]) * (xv[v] * r);
+    }
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) acc = acc + __shfl_xor(acc, m, kWave);
+    s[i] = acc;
+  }
+  const float cf = (float)C;
+  for (int c = lane * V; c < C; c += kWave * V) {
+    float g[V], dg[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      g[v] = gamma[c + v];
+      dg[v] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < kNbRows; ++i) {
+      if (i >= nt) break;
+      const float r = rstd[t0 + i];
+      const size_t row = (size_t)(t0 + i) * C;
+      float xv[V], dv[V], ov[V];
+      Vec::load(x + row + c, xv);
+      Vec::load(d + row + c, dv);
+      Vec::load(dout + row + c, ov);
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const float xh = xv[v] * r;
+        const float dh = dv[v] * g[v];
+        dg[v] = dg[v] + dv[v] * xh;
+        ov[v] = ov[v] + r * (dh - xh * s[i] / cf);
+      }
+      Vec::store(d + row + c, ov);
+    }
+    float* po = partial + (size_t)blockIdx.x * C + c;
+    if constexpr (V % 4 == 0) {
+#pragma unroll
+      for (int v = 0; v < V; v += 4)
+        *reinterpret_cast<float4*>(po + v) = make_float4(dg[v], dg[v + 1], dg[v + 2], dg[v + 3]);
+    } else {
+#pragma unroll
+      for (int v = 0; v < V; ++v) po[v] = dg[v];
+    }
+  }
+}
+
+// dgamma[c] += sum over the row blocks b of partial[b][c], b ascending in
+// 16 interleaved runs (wave w adds b = w, w + 16, ...) joined in wave
+// order: a fixed order, so the result does not depend on scheduling.
+__global__ __launch_bounds__(1024) void rmsnorm_dgamma_reduce_kernel(
+    const float* __restrict__ partial, int nb, int C, float* __restrict__ dgamma) {
+  __shared__ float s_w[16][kWave];
+  const int lane = lane_id(), w = threadIdx.x / kWave;
+  const int c = blockIdx.x * kWave + lane;
+  float acc = 0.0f;
+  if (c < C)
+    for (int b = w; b < nb; b += 16) acc = acc + partial[(size_t)b * C + c];
+  s_w[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && c < C) {
+    float t = 0.0f;
+    for (int i = 0; i < 16; ++i) t = t + s_w[i][lane];
+    dgamma[c] = dgamma[c] + t;
+  }
+}
+
+int rmsnorm_bwd_blocks(int N) { return (N + kNbRows - 1) / kNbRows; }
+
+// d [N][C] (the gradient of the normalised rows) becomes dx1 in place;
+// partial: rmsnorm_bwd_blocks(N) x C floats.
+template <typename ActT>
+hipError_t launch_rmsnorm_bwd(const ActT* x, ActT* d, const ActT* dout, const float* rstd,
+                              const float* gamma, int N, int C, float* partial, float* dgamma,
+                              hipStream_t stream) {
+  if (N < 0 || C <= 0) return hipErrorInvalidValue;
+  if (N == 0) return hipSuccess;
+  constexpr int kV = 16 / (int)sizeof(ActT);
+  const int nb = rmsnorm_bwd_blocks(N);
+  // 16-byte pieces when every row starts on a 16-byte boundary
+  const bool vec = C % kV == 0 && ((uintptr_t)x | (uintptr_t)d | (uintptr_t)dout) % 16 == 0;
+  if (vec)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<ActT, kV>), dim3(nb), dim3(kWave), 0, stream, x, d,
+                       dout, rstd, gamma, N, C, partial);
+  else
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<ActT, 1>), dim3(nb), dim3(kWave), 0, stream, x, d,
+                       dout, rstd, gamma, N, C, partial);
+  hipLaunchKernelGGL(rmsnorm_dgamma_reduce_kernel, dim3((C + kWave - 1) / kWave), dim3(1024), 0,
+                     stream, partial, nb, C, dgamma);
   return hipGetLastError();
 }
 
@@ -482,7 +672,10 @@ hipError_t launch_transpose_pad(const T* src, int src_rows, int src_cols, size_t
                                           const float*, int, int, int, int, T*, float*,        \
                                           hipStream_t);                                        \
   template hipError_t launch_router_wgrad<T>(const T*, const float*, int, int, int, float*,    \
-                                             float*, float*, float*, bool, hipStream_t);       \
+                                             float*, float*, float*, bool, const float*,       \
+                                             const float*, hipStream_t);                       \
+  template hipError_t launch_rmsnorm_bwd<T>(const T*, T*, const T*, const float*, const float*, \
+                                            int, int, float*, float*, hipStream_t);            \
   template hipError_t launch_transpose_pad<T>(const T*, int, int, size_t, T*, int, int, size_t, \
                                               int, hipStream_t);
 MGPT_INST_BWD(bf16_t)

@@ -81,7 +81,11 @@ hipError_t launch_token_bwd(const ActT*, const int32_t*, const int32_t*, const f
 int router_wgrad_chunks(int N);
 template <typename ActT>
 hipError_t launch_router_wgrad(const ActT*, const float*, int, int, int, float*, float*, float*,
-                               float*, bool, hipStream_t);
+                               float*, bool, const float*, const float*, hipStream_t);
+int rmsnorm_bwd_blocks(int N);
+template <typename ActT>
+hipError_t launch_rmsnorm_bwd(const ActT*, ActT*, const ActT*, const float*, const float*, int,
+                              int, float*, float*, hipStream_t);
 template <typename T>
 hipError_t launch_transpose_pad(const T*, int, int, size_t, T*, int, int, size_t, int,
                                 hipStream_t);
@@ -154,6 +158,7 @@ struct Layout {
   // the dX product (which holds the split-K region)
   size_t wg_part2;
   size_t dypad, dxpad;   // padded width: dy and dx at width C
+  size_t nrm_part;       // fused block backward: ln2 scale-gradient partials
   size_t total;
 };
 
@@ -337,6 +342,7 @@ struct mgpt_moe {
       L.wg_part2 = take(uses_gemm_dma(N) && dx_cus > 0 ? (size_t)num_cus * kGemmPartialBytes : 0);
       L.dypad = take(pad_rows);
       L.dxpad = take(pad_rows);
+      L.nrm_part = take((size_t)rmsnorm_bwd_blocks(N) * C * 4);
     }
     L.total = off;
     return L;
@@ -903,7 +909,7 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
 
 template <typename ActT>
 int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, char* ws,
-                  hipStream_t st) {
+                  hipStream_t st, const float* gamma = nullptr) {
   const Layout L = h->layout(N, true);
   const int C = h->C, Cx = h->Cx, H = h->H, E = h->E, k = h->k, Hp = h->Hp, Cp = h->Cp;
   const int A = N * k;
@@ -918,7 +924,10 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
     dy = dyp;
     x = (const ActT*)(ws + L.xpad);
     dx = (ActT*)(ws + L.dxpad);
+    if (gamma) gamma = (const float*)(ws + L.gpad);
   }
+  // fused block (gamma set): the router's input was (x * rstd) * gamma
+  const float* rstd = gamma ? (const float*)(ws + L.rstd) : nullptr;
   const int32_t* idx = (const int32_t*)(ws + L.topk_idx);
   const float* topp = (const float*)(ws + L.topk_p);
   const int32_t* slot_of = (const int32_t*)(ws + L.slot_of);
@@ -1066,7 +1075,7 @@ int backward_impl(mgpt_moe* h, const ActT* x, const ActT* dy, ActT* dx, int N, c
   HIP_TRY(mark(6));
   HIP_TRY(launch_router_wgrad<ActT>(x, dlog, N, C, E, (float*)(ws + L.rw_part),
                                     (float*)(ws + L.rw_part_b), g + h->g_off[0], g + h->g_off[1],
-                                    store, st));
+                                    store, rstd, gamma, st));
   if (gateup_done) HIP_TRY(hipStreamWaitEvent(st, h->join_ev, 0));
   h->grad_zero = false;
   if (h->padded()) HIP_TRY(launch_copy_cols<ActT>(dx, C, dx_out, Cx, N, Cx, Cx, st));
@@ -1219,8 +1228,12 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens, 
   return dispatch_forward(h, x, y, num_tokens, (char*)workspace, true, st, BlockArgs());
 }
 
-int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
-                      void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+// mgpt_moe_backward and, with gamma / dgamma set, mgpt_moe_backward_block.
+int backward_entry(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
+                   void* workspace, size_t workspace_bytes, void* stream,
+                   const float* gamma = nullptr, float* dgamma = nullptr) {
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
   if (!trainable(h))
@@ -1254,11 +1267,60 @@ int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int 
     if (int rc = materialize_grad(h, st)) return rc;
     h->bwd_captured = true;
   }
-  if (h->act == MGPT_DTYPE_BF16)
-    return backward_impl<bf16_t>(h, (const bf16_t*)x, (const bf16_t*)dy, (bf16_t*)dx,
-                                 num_tokens, (char*)workspace, st);
-  return backward_impl<float>(h, (const float*)x, (const float*)dy, (float*)dx, num_tokens,
-                              (char*)workspace, st);
+  char* ws = (char*)workspace;
+  float* nrm_part = (float*)(ws + h->layout(num_tokens, true).nrm_part);
+  if (h->act == MGPT_DTYPE_BF16) {
+    if (int rc = backward_impl<bf16_t>(h, (const bf16_t*)x, (const bf16_t*)dy, (bf16_t*)dx,
+                                       num_tokens, ws, st, gamma))
+      return rc;
+    // dx holds the gradient of the normalised rows: ln2 backward + residual
+    if (gamma)
+      HIP_TRY(launch_rmsnorm_bwd<bf16_t>((const bf16_t*)x, (bf16_t*)dx, (const bf16_t*)dy,
+                                         (const float*)(ws + h->layout(num_tokens).rstd), gamma,
+                                         num_tokens, h->Cx, nrm_part, dgamma, st));
+    return MGPT_OK;
+  }
+  if (int rc = backward_impl<float>(h, (const float*)x, (const float*)dy, (float*)dx, num_tokens,
+                                    ws, st, gamma))
+    return rc;
+  if (gamma)
+    HIP_TRY(launch_rmsnorm_bwd<float>((const float*)x, (float*)dx, (const float*)dy,
+                                      (const float*)(ws + h->layout(num_tokens).rstd), gamma,
+                                      num_tokens, h->Cx, nrm_part, dgamma, st));
+  return MGPT_OK;
+}
+
+}  // namespace
+
+int mgpt_moe_backward(mgpt_moe* h, const void* x, const void* dy, void* dx, int num_tokens,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  return backward_entry(h, x, dy, dx, num_tokens, workspace, workspace_bytes, stream);
+}
+
+int mgpt_moe_forward_block_train(mgpt_moe* h, const void* x, const float* gamma, float eps,
+                                 void* out, int num_tokens, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+  if (int rc = check_forward_args(h, x, out, num_tokens, workspace, workspace_bytes, true))
+    return rc;
+  if (!trainable(h))
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+  if (num_tokens == 0) return MGPT_OK;
+  if (!gamma) return fail(MGPT_ERR_INVALID_ARGUMENT, "null gamma");
+  if (!(eps >= 0.0f)) return fail(MGPT_ERR_INVALID_ARGUMENT, "eps must be >= 0");
+  HIP_TRY(hipSetDevice(h->device));
+  BlockArgs blk;
+  blk.gamma = gamma;
+  blk.eps = eps;
+  return dispatch_forward(h, x, out, num_tokens, (char*)workspace, true, (hipStream_t)stream,
+                          blk);
+}
+
+int mgpt_moe_backward_block(mgpt_moe* h, const void* x, const float* gamma, const void* dout,
+                            void* dx, float* dgamma, int num_tokens, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (!gamma || !dgamma) return fail(MGPT_ERR_INVALID_ARGUMENT, "null gamma or dgamma");
+  return backward_entry(h, x, dout, dx, num_tokens, workspace, workspace_bytes, stream, gamma,
+                        dgamma);
 }
 
 int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {

@@ -44,6 +44,7 @@ class MoELayer:
         self._last_n = None
         self._loaded = False
         self._train_x = None   # input of the last training forward (cached_input)
+        self._train_block = None   # (x, gamma) of the last training forward_block
 
     def __del__(self):
         h = getattr(self, "_h", None)
@@ -143,6 +144,7 @@ class MoELayer:
         capi.check(fn(self._h, x.data_ptr(), out.data_ptr(), n, ws.data_ptr(), ws.numel(), stream))
         self._last_n = n
         self._train_x = x if train else None
+        self._train_block = None
 
     def forward(self, x: torch.Tensor, train: bool = False) -> torch.Tensor:
         out = torch.empty_like(x)
@@ -158,9 +160,10 @@ class MoELayer:
         return out
 
     def forward_block_into(self, x: torch.Tensor, gamma: torch.Tensor, eps: float,
-                           out: torch.Tensor) -> None:
+                           out: torch.Tensor, train: bool = False) -> None:
         """forward_block writing into a caller-provided `out` (same shape and
-        dtype as x); gamma is a float32 device tensor of C elements."""
+        dtype as x); gamma is a float32 device tensor of C elements.
+        train=True also keeps what backward_block_into needs."""
         if not x.is_cuda or x.dtype != self.dtype or x.shape[-1] != self.C or not x.is_contiguous():
             raise ValueError("x must be a contiguous device tensor [..., C] of the layer's dtype")
         if not out.is_cuda or out.dtype != self.dtype or out.shape != x.shape or not out.is_contiguous():
@@ -169,13 +172,15 @@ class MoELayer:
         if g.numel() != self.C:
             raise ValueError("gamma must have C elements")
         n = x.numel() // self.C
-        ws = self._workspace(n, x.device)
+        ws = self._workspace(n, x.device, train)
         stream = torch.cuda.current_stream(x.device).cuda_stream
-        capi.check(capi.lib().mgpt_moe_forward_block(self._h, x.data_ptr(), g.data_ptr(),
-                                                     float(eps), out.data_ptr(), n,
-                                                     ws.data_ptr(), ws.numel(), stream))
+        fn = (capi.lib().mgpt_moe_forward_block_train if train
+              else capi.lib().mgpt_moe_forward_block)
+        capi.check(fn(self._h, x.data_ptr(), g.data_ptr(), float(eps), out.data_ptr(), n,
+                      ws.data_ptr(), ws.numel(), stream))
         self._last_n = n
         self._train_x = None
+        self._train_block = (x, g) if train else None
 
     def rstd(self) -> torch.Tensor:
         """Device view [N] of the per-token 1/rms of the last forward_block."""
@@ -192,6 +197,8 @@ class MoELayer:
         (MoELayer::backward_into, layers/MoELayer.cpp:130-223)."""
         x = self._train_x
         if x is None:
+            if self._train_block is not None:
+                raise RuntimeError("after forward_block(..., train=True) use backward_block_into")
             raise RuntimeError("backward needs a preceding forward(x, train=True)")
         if dout.shape != x.shape or din.shape != x.shape:
             raise ValueError("dout and din must have the input's shape")
@@ -209,6 +216,43 @@ class MoELayer:
         din = torch.empty_like(dout)
         self.backward_into(dout, din)
         return din
+
+    def backward_block_into(self, dout: torch.Tensor, din: torch.Tensor,
+                            dgamma: torch.Tensor) -> None:
+        """Backward of forward_block(x, gamma, train=True) for the upstream
+        gradient dout of its output: din = dL/dx (the residual path plus the
+        ln2 RMSNorm's backward of the MoE input gradient), dgamma (float32
+        device [C]) += the ln2 scale's gradient, and the MoE parameter
+        gradients added to the layer's buffers (layers/TransformerBlock.cpp:
+        81-85 with layers/RMSNormLayer.cpp:30-33)."""
+        blk = self._train_block
+        if blk is None:
+            raise RuntimeError("backward_block needs a preceding forward_block(..., train=True)")
+        x, g = blk
+        if dout.shape != x.shape or din.shape != x.shape:
+            raise ValueError("dout and din must have the input's shape")
+        if dout.dtype != self.dtype or din.dtype != self.dtype:
+            raise TypeError(f"expected {self.dtype} gradients")
+        if not (dout.is_cuda and din.is_cuda and dout.is_contiguous() and din.is_contiguous()):
+            raise ValueError("dout and din must be contiguous device tensors")
+        if (not dgamma.is_cuda or dgamma.dtype != torch.float32 or dgamma.numel() != self.C
+                or not dgamma.is_contiguous()):
+            raise ValueError("dgamma must be a contiguous float32 device tensor of C elements")
+        n = x.numel() // self.C
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        capi.check(capi.lib().mgpt_moe_backward_block(self._h, x.data_ptr(), g.data_ptr(),
+                                                      dout.data_ptr(), din.data_ptr(),
+                                                      dgamma.data_ptr(), n, self._ws.data_ptr(),
+                                                      self._ws.numel(), stream))
+
+    def backward_block(self, dout: torch.Tensor, dgamma: torch.Tensor | None = None):
+        """(din, dgamma) of backward_block_into; dgamma starts from zero
+        unless one is passed to add into."""
+        din = torch.empty_like(dout)
+        if dgamma is None:
+            dgamma = torch.zeros(self.C, dtype=torch.float32, device=dout.device)
+        self.backward_block_into(dout, din, dgamma)
+        return din, dgamma
 
     def zero_grad(self) -> None:
         stream = torch.cuda.current_stream().cuda_stream
