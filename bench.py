@@ -56,6 +56,8 @@ METRIC_DECODE = ("MoE decode steps/s in the sampling loop (Generator B=1, no KV 
                  "context S=64, C=2048, E=64, k=8, H=1408, fp8 weights)")
 METRIC_BLOCK = ("MoE block tokens/s, out = x + MoE(RMSNorm(x) * gamma) "
                 "(N=16384,C=1024,E=16,k=2)")
+METRIC_BLOCK_TRAIN = ("MoE block training tokens/s, zero_grad + forward + backward of "
+                      "out = x + MoE(RMSNorm(x) * gamma) (N=16384,C=1024,E=16,k=2)")
 CALIB_MIB = 512               # known-size elementwise copy for counter calibration
 NUM_XCD = 8                   # MI355X: 8 XCDs; GRBM_GUI_ACTIVE is counted per XCD
 SIMD_NUM = 256 * 4            # MI355X: 256 CUs x 4 SIMDs (rocprof's MfmaUtil denominator)
@@ -74,6 +76,8 @@ def stage_of(kernel_name: str):
         return "token_bwd"
     if "router_wgrad" in short:
         return "router_wgrad"
+    if "rmsnorm_bwd" in short or "rmsnorm_dgamma" in short:
+        return "ln2_bwd"
     m = re.search(r"wgrad(?:_tr)?_kernel<(?:[^,>]*, )?(\d)>", short)
     if m:
         return ("wgrad_down", "wgrad_gateup")[int(m.group(1))]
@@ -202,7 +206,8 @@ def cpu_sample_tokens(cfg) -> int:
 
 def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
     """The reference's own CPU MoE forward (train: zero_grad + forward +
-    backward; block: ln2 RMSNormLayer + forward + residual add)
+    backward; block: ln2 RMSNormLayer + forward + residual add; block_train:
+    zero_grad, the block forward and its backward)
     (oracle/_ref/ref_driver, built from the unmodified reference sources),
     single-threaded as the reference is, on `sample_tokens` tokens of the
     workload's shape."""
@@ -222,10 +227,14 @@ def cpu_baseline(cfg, sample_tokens: int, reps: int, mode: str = "forward"):
             drv, build = v4, "x86-64-v4 (AVX-512) build"
     except OSError:
         pass
-    sub = {"forward": "bench", "train": "bench_train", "block": "bench_block"}[mode]
+    sub = {"forward": "bench", "train": "bench_train", "block": "bench_block",
+           "block_train": "bench_block_train"}[mode]
     what = {"forward": "MoELayer::forward_into",
             "train": "Tensor::zero_grad + MoELayer::forward_into + backward_into",
-            "block": "RMSNormLayer::forward_into + MoELayer::forward_into + Tensor::add_into"}[mode]
+            "block": "RMSNormLayer::forward_into + MoELayer::forward_into + Tensor::add_into",
+            "block_train": "Tensor::zero_grad, then RMSNormLayer + MoELayer forward_into and "
+                           "Tensor::add_into, then MoELayer + RMSNormLayer backward_into and "
+                           "Tensor::add_into"}[mode]
     cmd = [drv, sub, str(sample_tokens), str(cfg.C), str(cfg.H),
            str(cfg.E), str(cfg.k), str(reps)]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
@@ -257,13 +266,15 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
         b = json.loads(f.read().strip().splitlines()[-1])
     rows = list(csv.DictReader(open(stats_csv)))
     mode = str(b.get("pass", "forward")).split(" ")[0]
-    train = mode == "train"
+    train = mode in ("train", "block_train")
     extra = "" if mode == "forward" else f" --pass {mode}"
     cfg_arg = "" if mode == "decode" else f"--config {config} "
     cmd = (f"rocprofv3 --kernel-trace --stats --output-format csv -d <dir> -o run -- python bench.py "
            f"{cfg_arg}{extra.strip()} --steps {b['steps']} --warmup {b['warmup']} "
            "--no-cpu-baseline").replace("  ", " ")
     what = {"train": "training step (zero_grad + forward + backward)",
+            "block_train": "fused block training step (zero_grad + RMSNorm + MoE + residual, "
+                           "forward and backward)",
             "block": "fused block (RMSNorm + MoE + residual)",
             "decode": "decode steps in the sampling loop"}.get(mode, "forward")
     w, k = b["warmup"], b["steps"]
@@ -273,6 +284,9 @@ def summarize_stats(stats_csv: str, bench_json: str, config: str) -> str:
                      "mix those launches with the serial ones of the profiled steps",
             "block": f"{w + 2 * k} fused block forwards ({w} warmup, {k} timed, {k} profiled) "
                      f"and {w + k} unfused ({w} warmup, {k} timed)",
+            "block_train": f"{w + 2 * k} fused block training steps ({w} warmup, {k} timed, "
+                           f"{k} profiled); outside the profiled steps the backward's weight "
+                           "gradients run on a second stream beside its d(act) and dX products",
             "decode": f"{w + 1} growing loops of {b.get('growing_phase_steps')} steps "
                       f"(N = 1 .. {b['config']['N']}), then {k} eager, {k} "
                       f"profiled, 1 + {max(w, 30) + k} graph-replayed steady-state "
@@ -361,11 +375,13 @@ def main() -> int:
                          "reference's work per run, 4096 tokens at cfg3's per-token cost)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--pass", dest="mode", choices=["forward", "train", "block", "decode"],
+    ap.add_argument("--pass", dest="mode",
+                    choices=["forward", "train", "block", "block_train", "decode"],
                     default="forward",
                     help="forward (default, the headline), train (zero_grad + forward + backward), "
-                         "block (RMSNorm + MoE + residual, fused) or decode (the sampling "
-                         "loop at cfg5's shape)")
+                         "block (RMSNorm + MoE + residual, fused), block_train (zero_grad + the "
+                         "fused block's forward and backward) or decode (the sampling loop at "
+                         "cfg5's shape)")
     ap.add_argument("--calib-copy", action="store_true",
                     help=f"after the timed run, copy {CALIB_MIB} MiB with an elementwise kernel 3 "
                          "times (known-size traffic for calibrating FETCH_SIZE/WRITE_SIZE)")
@@ -423,8 +439,9 @@ def main() -> int:
     x = torch.from_numpy(inp.x).to(dev).to(dt)
     y = torch.empty_like(x)
     del inp
-    train = args.mode == "train"
-    block = args.mode == "block"
+    block_train = args.mode == "block_train"
+    train = args.mode in ("train", "block_train")
+    block = args.mode in ("block", "block_train")
     if train:
         g = torch.Generator(device="cpu").manual_seed(7)
         dy = torch.randn(x.shape, generator=g).to(dev).to(dt)
@@ -436,9 +453,16 @@ def main() -> int:
         x = (x.float() * scale.to(dev)).to(dt)
         gamma = (1.0 + 0.2 * torch.randn(cfg.C, generator=g)).to(dev)
         eps = 1e-5
+        dgamma = torch.zeros(cfg.C, dtype=torch.float32, device=dev)
     print(f"setup {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
     def step():
+        if block_train:
+            layer.zero_grad()
+            dgamma.zero_()
+            layer.forward_block_into(x, gamma, eps, y, train=True)
+            layer.backward_block_into(dy, dx, dgamma)
+            return
         if block:
             layer.forward_block_into(x, gamma, eps, y)
             return
@@ -587,7 +611,13 @@ def main() -> int:
                 "peak": peak_mm, "unit": "TFLOP/s", "frac": round(rates[dom] / peak_mm, 4),
                 "traffic": None},
         })
-    if block:
+    if block_train:
+        result.update({
+            "metric": METRIC_BLOCK_TRAIN,
+            "pass": "block_train (zero_grad + mgpt_moe_forward_block_train + "
+                    "mgpt_moe_backward_block: ln2 RMSNorm backward and residual in one kernel)",
+        })
+    if block and not block_train:
         for _ in range(args.warmup):
             unfused_step()
         torch.cuda.synchronize()

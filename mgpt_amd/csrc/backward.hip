@@ -17,6 +17,8 @@
 //                 the layouts the data-gradient products read.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace mgpt {
 namespace {
 
@@ -499,33 +501,31 @@ hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int
 // TransformerBlock::backward_into, layers/TransformerBlock.cpp:81-85, with
 // RMSNormLayer::backward_into, utils/Tensor.cpp:1665-1689):
 //   x_hat = x * r, dh = d * gamma, s = sum_c dh * x_hat,
-//   dx1 = dout + r * (dh - x_hat * s / C),   dgamma[c] += sum_t d * x_hat,
-// with d the gradient of the normalised rows (the MoE backward's dx).  One
-// wave per kNbRows token rows: a pass over each row for s (lanes on
-// 16-byte column pieces, a wave sum), then a pass per column piece over the
-// wave's rows that writes dx1 in place of d and adds the rows' d * x_hat
-// into registers, stored as partial[wave][c]; rmsnorm_dgamma_reduce_kernel
-// adds the partials in wave order (deterministic).  Each lane reads its own
-// elements of d before it overwrites them, so d and dx1 share the buffer.
+//   dx1 = dout + r * (dh - x_hat * (s / C)),   dgamma[c] += sum_t d * x_hat,
+// with d the gradient of the normalised rows (the MoE backward's dx).  A
+// block of 256 threads takes kNbRows token rows, each thread the same
+// column pieces (V consecutive columns) of every row: a first pass forms
+// each row's s (per-thread partial sums, a wave sum, the four waves' sums
+// added in wave order), a second writes dx1 in place of d and adds the
+// rows' d * x_hat per column in registers, stored as partial[block][c];
+// rmsnorm_dgamma_reduce_kernel adds the blocks' partials in a fixed order
+// (deterministic).  Each thread reads its own elements of d before it
+// overwrites them, so d and dx1 share the buffer.
 constexpr int kNbRows = 16;
 
 template <typename ActT, int V> struct NbVec;
-template <> struct NbVec<bf16_t, 8> {
-  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[8]) {
-    const uint4 q = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
-    }
+template <> struct NbVec<bf16_t, 4> {
+  static __device__ __forceinline__ void load(const bf16_t* p, float (&v)[4]) {
+    const uint2 q = *reinterpret_cast<const uint2*>(p);
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xFFFF0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xFFFF0000u);
   }
-  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[8]) {
-    uint32_t w[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
-    *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[4]) {
+    *reinterpret_cast<uint2*>(p) =
+        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
+                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
   }
 };
 template <> struct NbVec<float, 4> {
@@ -543,84 +543,188 @@ template <typename ActT> struct NbVec<ActT, 1> {
 };
 
 template <typename ActT, int V>
-__global__ __launch_bounds__(64) void rmsnorm_bwd_kernel(const ActT* __restrict__ x, ActT* d,
-                                                         const ActT* __restrict__ dout,
-                                                         const float* __restrict__ rstd,
-                                                         const float* __restrict__ gamma, int N,
-                                                         int C, float* __restrict__ partial) {
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const ActT* __restrict__ x, ActT* d,
+                                                          const ActT* __restrict__ dout,
+                                                          const float* __restrict__ rstd,
+                                                          const float* __restrict__ gamma, int N,
+                                                          int C, float* __restrict__ partial) {
   using Vec = NbVec<ActT, V>;
-  const int lane = lane_id();
+  __shared__ float s_part[4][kNbRows];
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
   const int t0 = blockIdx.x * kNbRows;
   const int nt = min(kNbRows, N - t0);
-  float s[kNbRows];
+  float r[kNbRows], acc[kNbRows];
 #pragma unroll
   for (int i = 0; i < kNbRows; ++i) {
-    s[i] = 0.0f;
-    if (i >= nt) continue;
-    const float r = rstd[t0 + i];
-    const size_t row = (size_t)(t0 + i) * C;
-    float acc = 0.0f;
-    for (int c = lane * V; c < C; c += kWave * V) {
+    r[i] = rstd[t0 + min(i, nt - 1)];
+    acc[i] = 0.0f;
+  }
+  for (int c = tid * V; c < C; c += 256 * V) {
+    float g[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) g[v] = gamma[c + v];
+    // rows past the block's last token re-read that token (in bounds) and
+    // their sums are never used, so every load is issued unconditionally
+#pragma unroll
+    for (int i = 0; i < kNbRows; ++i) {
+      const size_t row = (size_t)(t0 + min(i, nt - 1)) * C;
       float xv[V], dv[V];
       Vec::load(x + row + c, xv);
       Vec::load(d + row + c, dv);
 #pragma unroll
-      for (int v = 0; v < V; ++v) acc = acc + (dv[v] * gamma[c + v]) * (xv[v] * r);
+      for (int v = 0; v < V; ++v) acc[i] = acc[i] + (dv[v] * g[v]) * (xv[v] * r[i]);
     }
-#pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) acc = acc + __shfl_xor(acc, m, kWave);
-    s[i] = acc;
   }
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i) {
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) acc[i] = acc[i] + __shfl_xor(acc[i], m, kWave);
+    if (lane == 0) s_part[w][i] = acc[i];
+  }
+  __syncthreads();
   const float cf = (float)C;
-  for (int c = lane * V; c < C; c += kWave * V) {
+  float q[kNbRows];
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i)
+    q[i] = (((s_part[0][i] + s_part[1][i]) + s_part[2][i]) + s_part[3][i]) / cf;
+  for (int c = tid * V; c < C; c += 256 * V) {
     float g[V], dg[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       g[v] = gamma[c + v];
       dg[v] = 0.0f;
     }
+    float xv[kNbRows][V], dv[kNbRows][V], ov[kNbRows][V];
 #pragma unroll
     for (int i = 0; i < kNbRows; ++i) {
-      if (i >= nt) break;
-      const float r = rstd[t0 + i];
-      const size_t row = (size_t)(t0 + i) * C;
-      float xv[V], dv[V], ov[V];
-      Vec::load(x + row + c, xv);
-      Vec::load(d + row + c, dv);
-      Vec::load(dout + row + c, ov);
+      const size_t row = (size_t)(t0 + min(i, nt - 1)) * C;
+      Vec::load(x + row + c, xv[i]);
+      Vec::load(d + row + c, dv[i]);
+      Vec::load(dout + row + c, ov[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kNbRows; ++i) {
+      const bool live = i < nt;
 #pragma unroll
       for (int v = 0; v < V; ++v) {
-        const float xh = xv[v] * r;
-        const float dh = dv[v] * g[v];
-        dg[v] = dg[v] + dv[v] * xh;
-        ov[v] = ov[v] + r * (dh - xh * s[i] / cf);
+        const float xh = xv[i][v] * r[i];
+        dg[v] = dg[v] + (live ? dv[i][v] * xh : 0.0f);
+        ov[i][v] = ov[i][v] + r[i] * (dv[i][v] * g[v] - xh * q[i]);
       }
-      Vec::store(d + row + c, ov);
+      if (live) Vec::store(d + (size_t)(t0 + i) * C + c, ov[i]);
     }
     float* po = partial + (size_t)blockIdx.x * C + c;
-    if constexpr (V % 4 == 0) {
 #pragma unroll
-      for (int v = 0; v < V; v += 4)
-        *reinterpret_cast<float4*>(po + v) = make_float4(dg[v], dg[v + 1], dg[v + 2], dg[v + 3]);
-    } else {
-#pragma unroll
-      for (int v = 0; v < V; ++v) po[v] = dg[v];
-    }
+    for (int v = 0; v < V; ++v) po[v] = dg[v];
   }
 }
 
-// dgamma[c] += sum over the row blocks b of partial[b][c], b ascending in
-// 16 interleaved runs (wave w adds b = w, w + 16, ...) joined in wave
-// order: a fixed order, so the result does not depend on scheduling.
+// The same for bf16 rows of at most 1024 columns (one 4-column piece per
+// thread): every load of the block's rows is issued first and the values
+// stay in registers for both passes, so the block makes one trip to
+// memory instead of reading x and d twice.
+__global__ __launch_bounds__(256) void rmsnorm_bwd_bf16_kernel(
+    const bf16_t* __restrict__ x, bf16_t* d, const bf16_t* __restrict__ dout,
+    const float* __restrict__ rstd, const float* __restrict__ gamma, int N, int C,
+    float* __restrict__ partial) {
+  using Vec = NbVec<bf16_t, 4>;
+  __shared__ float s_part[4][kNbRows];
+  const int tid = threadIdx.x, lane = lane_id(), w = tid / kWave;
+  const int t0 = blockIdx.x * kNbRows;
+  const int nt = min(kNbRows, N - t0);
+  const int c = tid * 4;
+  const bool has = c < C;   // this thread's piece exists
+  uint2 xr[kNbRows], dr[kNbRows], orr[kNbRows];
+  float r[kNbRows];
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i) {
+    // rows past the block's last token re-read that token (in bounds)
+    const size_t row = (size_t)(t0 + min(i, nt - 1)) * C + c;
+    r[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(rstd[t0 + min(i, nt - 1)])));
+    if (has) {
+      xr[i] = *reinterpret_cast<const uint2*>(x + row);
+      dr[i] = *reinterpret_cast<const uint2*>(d + row);
+      orr[i] = *reinterpret_cast<const uint2*>(dout + row);
+    } else {
+      xr[i] = dr[i] = orr[i] = make_uint2(0u, 0u);
+    }
+  }
+  float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (has) {
+    const float4 gv = *reinterpret_cast<const float4*>(gamma + c);
+    g[0] = gv.x; g[1] = gv.y; g[2] = gv.z; g[3] = gv.w;
+  }
+  auto unpack = [](const uint2& q, float (&v)[4]) __attribute__((always_inline)) {
+    v[0] = __uint_as_float(q.x << 16);
+    v[1] = __uint_as_float(q.x & 0xFFFF0000u);
+    v[2] = __uint_as_float(q.y << 16);
+    v[3] = __uint_as_float(q.y & 0xFFFF0000u);
+  };
+  float acc[kNbRows];
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i) {
+    float xv[4], dv[4];
+    unpack(xr[i], xv);
+    unpack(dr[i], dv);
+    acc[i] = 0.0f;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[i] = acc[i] + (dv[v] * g[v]) * (xv[v] * r[i]);
+#pragma unroll
+    for (int m = 1; m < kWave; m <<= 1) acc[i] = acc[i] + __shfl_xor(acc[i], m, kWave);
+    if (lane == 0) s_part[w][i] = acc[i];
+  }
+  __syncthreads();
+  if (!has) return;
+  // the packed rows again (not the unpacked values of the first pass, which
+  // would double the live registers)
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i) asm volatile("" : "+v"(xr[i]), "+v"(dr[i]), "+v"(orr[i]));
+  const float cf = (float)C;
+  float dg[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int i = 0; i < kNbRows; ++i) {
+    const float q = (((s_part[0][i] + s_part[1][i]) + s_part[2][i]) + s_part[3][i]) / cf;
+    const bool live = i < nt;
+    float xv[4], dv[4], ov[4];
+    unpack(xr[i], xv);
+    unpack(dr[i], dv);
+    unpack(orr[i], ov);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const float xh = xv[v] * r[i];
+      dg[v] = dg[v] + (live ? dv[v] * xh : 0.0f);
+      ov[v] = ov[v] + r[i] * (dv[v] * g[v] - xh * q);
+    }
+    if (live) Vec::store(d + (size_t)(t0 + i) * C + c, ov);
+  }
+  *reinterpret_cast<float4*>(partial + (size_t)blockIdx.x * C + c) =
+      make_float4(dg[0], dg[1], dg[2], dg[3]);
+}
+
+// dgamma[c] += sum over the row blocks b of partial[b][c] in a fixed order:
+// wave w of the block of 64 columns takes b = w + 16m, 32 loads in flight
+// at a time, into eight running sums (m mod 8) joined pairwise; wave 0 adds
+// the sixteen waves' sums in wave order.
 __global__ __launch_bounds__(1024) void rmsnorm_dgamma_reduce_kernel(
     const float* __restrict__ partial, int nb, int C, float* __restrict__ dgamma) {
   __shared__ float s_w[16][kWave];
   const int lane = lane_id(), w = threadIdx.x / kWave;
   const int c = blockIdx.x * kWave + lane;
-  float acc = 0.0f;
+  float a[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) a[u] = 0.0f;
   if (c < C)
-    for (int b = w; b < nb; b += 16) acc = acc + partial[(size_t)b * C + c];
-  s_w[w][lane] = acc;
+    for (int b0 = w; b0 < nb; b0 += 16 * 32) {
+      float v[32];
+#pragma unroll
+      for (int u = 0; u < 32; ++u) {
+        const int b = b0 + 16 * u;
+        v[u] = b < nb ? partial[(size_t)b * C + c] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 32; ++u) a[u % 8] = a[u % 8] + v[u];
+    }
+  s_w[w][lane] = ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
   __syncthreads();
   if (w == 0 && c < C) {
     float t = 0.0f;
@@ -639,15 +743,22 @@ hipError_t launch_rmsnorm_bwd(const ActT* x, ActT* d, const ActT* dout, const fl
                               hipStream_t stream) {
   if (N < 0 || C <= 0) return hipErrorInvalidValue;
   if (N == 0) return hipSuccess;
-  constexpr int kV = 16 / (int)sizeof(ActT);
   const int nb = rmsnorm_bwd_blocks(N);
-  // 16-byte pieces when every row starts on a 16-byte boundary
-  const bool vec = C % kV == 0 && ((uintptr_t)x | (uintptr_t)d | (uintptr_t)dout) % 16 == 0;
-  if (vec)
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<ActT, kV>), dim3(nb), dim3(kWave), 0, stream, x, d,
+  // pieces of 4 columns when every row starts on a piece-aligned boundary
+  const size_t piece = 4 * sizeof(ActT);
+  const bool vec = C % 4 == 0 && ((uintptr_t)x | (uintptr_t)d | (uintptr_t)dout) % piece == 0;
+  bool single_pass = false;
+  if constexpr (std::is_same<ActT, bf16_t>::value)
+    single_pass = vec && C <= 1024 && (uintptr_t)gamma % 16 == 0;
+  if (single_pass)
+    hipLaunchKernelGGL(rmsnorm_bwd_bf16_kernel, dim3(nb), dim3(256), 0, stream,
+                       reinterpret_cast<const bf16_t*>(x), reinterpret_cast<bf16_t*>(d),
+                       reinterpret_cast<const bf16_t*>(dout), rstd, gamma, N, C, partial);
+  else if (vec)
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<ActT, 4>), dim3(nb), dim3(256), 0, stream, x, d,
                        dout, rstd, gamma, N, C, partial);
   else
-    hipLaunchKernelGGL((rmsnorm_bwd_kernel<ActT, 1>), dim3(nb), dim3(kWave), 0, stream, x, d,
+    hipLaunchKernelGGL((rmsnorm_bwd_kernel<ActT, 1>), dim3(nb), dim3(256), 0, stream, x, d,
                        dout, rstd, gamma, N, C, partial);
   hipLaunchKernelGGL(rmsnorm_dgamma_reduce_kernel, dim3((C + kWave - 1) / kWave), dim3(1024), 0,
                      stream, partial, nb, C, dgamma);

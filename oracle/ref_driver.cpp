@@ -13,6 +13,8 @@
 //   ref_driver bench <N> <C> <H> <E> <k> <reps>
 //   ref_driver bench_train <N> <C> <H> <E> <k> <reps>   (zero_grad + forward + backward)
 //   ref_driver bench_block <N> <C> <H> <E> <k> <reps>   (ln2 + MoE + residual)
+//   ref_driver bench_block_train <N> <C> <H> <E> <k> <reps>
+//            (zero_grad, ln2 + MoE + residual forward, then their backward)
 //   ref_driver gptbin <out.bin> <side.bin> V S C L heads E k H steps seed
 //   ref_driver gptlogits <model.bin> <heads> <E> <k> <H> <ids.bin> <out.bin>
 //   ref_driver train <in.bin> <dy.bin> <out.bin> <steps> <lr>
@@ -318,7 +320,7 @@ int block_backward(const char* in_path, const char* g_path, const char* dy_path,
 // (its CPU caches are sized on first use and never resized,
 // layers/MoELayer.cpp:42-50): 1 warmup, then `reps` timed runs; prints one
 // JSON line with every run and the median.
-enum BenchPass { kBenchForward, kBenchTrain, kBenchBlock };
+enum BenchPass { kBenchForward, kBenchTrain, kBenchBlock, kBenchBlockTrain };
 
 int bench(int N, int C, int H, int E, int k, int reps, BenchPass pass) {
   const bool train = pass == kBenchTrain;
@@ -335,16 +337,25 @@ int bench(int N, int C, int H, int E, int k, int reps, BenchPass pass) {
   MoELayer layer(C, H, E, k);
   for (Tensor* p : layer.get_parameters())
     for (auto& v : p->data) v = 0.02f * nd(gen);
-  Tensor y, dx, xn, out;
+  Tensor y, dx, xn, out, d_ln2;
   Tensor dy({1, N, C}, 0.0f, Device::CPU);
   for (auto& v : dy.data) v = nd(gen);
   RMSNormLayer ln2(C);
   for (auto& v : ln2.get_parameters()[0]->data) v = 1.0f + 0.2f * nd(gen);
   auto step = [&]() {
-    if (pass == kBenchBlock) {
+    if (pass == kBenchBlock || pass == kBenchBlockTrain) {
+      if (pass == kBenchBlockTrain) {
+        for (Tensor* p : layer.get_parameters()) p->zero_grad();
+        ln2.get_parameters()[0]->zero_grad();
+      }
       ln2.forward_into(x, xn);
       layer.forward_into(xn, y);
       Tensor::add_into(x, y, out);
+      if (pass == kBenchBlockTrain) {   // layers/TransformerBlock.cpp:81-85
+        layer.backward_into(dy, d_ln2);
+        ln2.backward_into(d_ln2, d_ln2);
+        Tensor::add_into(dy, d_ln2, dx);
+      }
       return;
     }
     if (train)   // the Trainer's per-step order (pipeline/Trainer.cpp:303-305)
@@ -365,8 +376,11 @@ int bench(int N, int C, int H, int E, int k, int reps, BenchPass pass) {
   double med = s[s.size() / 2];
   std::printf("{\"pass\": \"%s\", \"N\": %d, \"C\": %d, \"H\": %d, \"E\": %d, \"k\": %d, "
               "\"reps\": %d, \"median_s\": %.6f, \"runs_s\": [",
-              train ? "zero_grad+forward+backward" : pass == kBenchBlock ? "block" : "forward", N, C, H,
-              E, k, reps, med);
+              train                        ? "zero_grad+forward+backward"
+              : pass == kBenchBlock        ? "block"
+              : pass == kBenchBlockTrain   ? "block zero_grad+forward+backward"
+                                           : "forward",
+              N, C, H, E, k, reps, med);
   for (size_t i = 0; i < t.size(); ++i) std::printf("%s%.6f", i ? ", " : "", t[i]);
   std::printf("], \"tokens_per_s\": %.3f, \"threads\": 1}\n", N / med);
   return 0;
@@ -463,14 +477,17 @@ int main(int argc, char** argv) {
                   std::atoi(argv[7]), std::atoi(argv[8]), std::atoi(argv[9]), std::atoi(argv[10]),
                   std::atoi(argv[11]), std::atoi(argv[12]), (unsigned)std::atol(argv[13]));
   if (argc == 8 && (std::string(argv[1]) == "bench" || std::string(argv[1]) == "bench_train" ||
-                    std::string(argv[1]) == "bench_block"))
+                    std::string(argv[1]) == "bench_block" ||
+                    std::string(argv[1]) == "bench_block_train"))
     return bench(std::atoi(argv[2]), std::atoi(argv[3]), std::atoi(argv[4]),
                  std::atoi(argv[5]), std::atoi(argv[6]), std::atoi(argv[7]),
-                 std::string(argv[1]) == "bench_train"   ? kBenchTrain
-                 : std::string(argv[1]) == "bench_block" ? kBenchBlock
-                                                         : kBenchForward);
+                 std::string(argv[1]) == "bench_train"         ? kBenchTrain
+                 : std::string(argv[1]) == "bench_block"       ? kBenchBlock
+                 : std::string(argv[1]) == "bench_block_train" ? kBenchBlockTrain
+                                                               : kBenchForward);
   std::fprintf(stderr, "usage: ref_driver run <in> <out> | backward <in> <dy> <grad> | "
-                       "block <in> <gamma> <out> | bench[_train|_block] N C H E k reps | "
+                       "block <in> <gamma> <out> | block_backward <in> <gamma> <dy> <grad> | "
+                       "bench[_train|_block|_block_train] N C H E k reps | "
                        "gptbin <out> <side> V S C L heads E k H steps seed | "
                        "gptlogits <bin> heads E k H <ids> <out>\n");
   return 1;
