@@ -157,6 +157,12 @@ __device__ __forceinline__ void drain_barrier() {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// This wave's LDS accesses completed, then the workgroup barrier (the
+// direct-to-LDS loads in flight are not waited for).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // LDS budget of the logit stage: two buffers of (x chunk + weight chunk).
 constexpr int kRouterLds = 96 * 1024;
 #ifndef MGPT_SOFTMAX_THREADS
@@ -172,12 +178,22 @@ constexpr int kRouterSplitLds = MGPT_ROUTER_SPLIT_LDS_KB * 1024;
 // LDS bytes of one group's weight chunk: whole 1 KB DMA blocks.
 __device__ __forceinline__ int wgroup_bytes(int CB, int RE) { return max(CB * RE * 4, 1024); }
 
-// Columns per chunk: the largest power of two >= 64 whose two stages fit.
+// Extra LDS a kernel that runs normalised rows provides beyond the stage
+// budget, for the chunk's kRT fp32 normalised rows.
+constexpr int kRouterNormLds = 32 * 1024;
+
+// Columns per chunk: the largest power of two >= 64 whose two stages fit
+// lds_bytes, or, with normalised rows, whose two stages and kRT x CB fp32
+// rows fit lds_bytes + kRouterNormLds.  (Every case the launchers make gives
+// bf16 rows of >= 256 bytes, 16 swizzle slots: two stages at 16 waves x 4
+// experts and CB = 128 take 96 KB.)
 template <typename ActT>
-__device__ __forceinline__ int chunk_cols(int nw, int RE, int lds_bytes) {
+__device__ __forceinline__ int chunk_cols(int nw, int RE, int lds_bytes, bool norm) {
   auto stage = [&](int cb) { return kRT * cb * (int)sizeof(ActT) + nw * wgroup_bytes(cb, RE); };
+  auto need = [&](int cb) { return 2 * stage(cb) + (norm ? kRT * cb * 4 : 0); };
+  const int budget = lds_bytes + (norm ? kRouterNormLds : 0);
   int CB = 64;
-  while (2 * stage(2 * CB) <= lds_bytes) CB *= 2;
+  while (need(2 * CB) <= budget) CB *= 2;
   return CB;
 }
 
@@ -228,14 +244,14 @@ __device__ __forceinline__ float sqrt_rn(float y) {
   return s;
 }
 
-template <typename ActT, int RE>
+template <typename ActT, int RE, bool NORM>
 __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int n_rows,
                                              const float* __restrict__ wsrc, int g_valid, int nw,
                                              int g, int C, char* smem, float (&acc)[RE],
                                              RowNorm nrm, float* r_out,
                                              int lds_bytes = kRouterLds) {
   constexpr int kPer = 16 / (int)sizeof(ActT);   // columns per 16-byte unit
-  const int CB = chunk_cols<ActT>(nw, RE, lds_bytes);
+  const int CB = chunk_cols<ActT>(nw, RE, lds_bytes, NORM);
   const int xrow_bytes = CB * (int)sizeof(ActT);   // LDS bytes per token row
   const int x_bytes = kRT * xrow_bytes;
   const int wgb = wgroup_bytes(CB, RE);
@@ -251,20 +267,24 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
   // Weights: group gg's cnum*RE floats in 1 KB blocks at a 1 KB-aligned
   // group stride; lanes past a partial block re-read the group's first
   // bytes (in bounds, never used).
-  auto chunk_dma = [&](int c0, int cnum, int b) __attribute__((always_inline)) {
-    const uint32_t st = lds0 + (uint32_t)(b * stage_bytes);
+  // the x part, rows of xrow bytes at dst
+  auto x_dma = [&](int c0, int cnum, uint32_t dst, int xrow) __attribute__((always_inline)) {
     const int units_row = cnum * (int)sizeof(ActT) / 16;   // valid units per row
-    const int x_blocks = x_bytes / 1024;
+    const int x_blocks = kRT * xrow / 1024;
     for (int q = g; q < x_blocks; q += nw) {
       const int byte = q * 1024 + lane * 16;
-      const int row = byte / xrow_bytes, slot = (byte % xrow_bytes) / 16;
+      const int row = byte / xrow, slot = (byte % xrow) / 16;
       int unit = slot ^ (row & 15);
       if (unit >= units_row) unit = 0;
       const char* src = reinterpret_cast<const char*>(xblk) +
                         (size_t)min(row, n_rows - 1) * xrow_g + (size_t)c0 * sizeof(ActT) +
                         unit * 16;
-      dma16(src, st + (uint32_t)(q * 1024));
+      dma16(src, dst + (uint32_t)(q * 1024));
     }
+  };
+  auto chunk_dma = [&](int c0, int cnum, int b) __attribute__((always_inline)) {
+    const uint32_t st = lds0 + (uint32_t)(b * stage_bytes);
+    x_dma(c0, cnum, st, xrow_bytes);
     const int gbytes = cnum * RE * 4;
     const int gblocks = (gbytes + 1023) / 1024;
     for (int q = g; q < g_valid * gblocks; q += nw) {
@@ -280,28 +300,45 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
   constexpr int kWU = kPer * RE / 4;   // float4 of weights per unit
   int b = 0;
   float r = 1.0f;
-  if (nrm.gamma) {
-    // pass 1: the row's sum of squares, columns in order
+  // fused block: kRT fp32 normalised rows of the current chunk, 16-byte
+  // units of row t at slot unit ^ (t & xn_sw), after the two stages
+  float* xn_lds = reinterpret_cast<float*>(smem + 2 * stage_bytes);
+  __shared__ float s_rr[kRT];
+  if constexpr (NORM) {
+    // pass 1: the row's sum of squares, columns in order (one chain per
+    // token, so one wave forms them while the others only keep the chunks
+    // moving; the result goes to every wave through LDS)
+    // x alone in chunks of CB1 >= CB columns, the whole budget for two
+    // stages (fewer, longer DMA rounds: this pass does little arithmetic)
+    const int budget = lds_bytes + kRouterNormLds;
+    int CB1 = CB;
+    while (CB1 < C && 2 * kRT * (2 * CB1) * (int)sizeof(ActT) <= budget) CB1 *= 2;
+    const int xrow1 = CB1 * (int)sizeof(ActT);
+    const int st1 = kRT * xrow1;
     float ms = 0.0f;
-    chunk_dma(0, min(CB, C), 0);
-    for (int c0 = 0; c0 < C; c0 += CB) {
-      const int cnum = min(CB, C - c0);
+    x_dma(0, min(CB1, C), lds0, xrow1);
+    for (int c0 = 0; c0 < C; c0 += CB1) {
+      const int cnum = min(CB1, C - c0);
       drain_barrier();
-      if (c0 + CB < C) chunk_dma(c0 + CB, min(CB, C - c0 - CB), b ^ 1);
-      const char* xr = smem + b * stage_bytes + lane * xrow_bytes;
-      for (int u = 0; u < cnum / kPer; ++u) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
+      if (c0 + CB1 < C)
+        x_dma(c0 + CB1, min(CB1, C - c0 - CB1), lds0 + (uint32_t)((b ^ 1) * st1), xrow1);
+      if (g == 0) {
+        const char* xr = smem + b * st1 + lane * xrow1;
+        for (int u = 0; u < cnum / kPer; ++u) {
+          const uint4 xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-          const float v = widen<ActT>(xv, i);
-          ms = ms + v * v;
+          for (int i = 0; i < kPer; ++i) {
+            const float v = widen<ActT>(xv, i);
+            ms = ms + v * v;
+          }
         }
       }
       b ^= 1;
     }
-    r = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ms, (float)nrm.cn) + nrm.eps));
+    if (g == 0) s_rr[lane] = __fdiv_rn(1.0f, sqrt_rn(__fdiv_rn(ms, (float)nrm.cn) + nrm.eps));
+    drain_barrier();   // r published; every wave done with the stages before they are refilled
+    r = s_rr[lane];
     if (r_out) *r_out = r;
-    drain_barrier();   // every wave done with the stages before they are refilled
     b = 0;
   }
   chunk_dma(0, min(CB, C), 0);
@@ -313,7 +350,7 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
     const char* xr = st + lane * xrow_bytes;
     const float* wq = reinterpret_cast<const float*>(st + x_bytes + g * wgb);
     const int units = cnum / kPer;
-    if (!nrm.gamma) {
+    if constexpr (!NORM) {
       // operands of unit u+1 are read while unit u is multiplied
       uint4 x0, x1;
       float4 w0[kWU], w1[kWU];
@@ -342,19 +379,44 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
         mul_add(x1, w1);
       }
     } else {
-      // normalised: x -> (x * r) * gamma[c] before each product (gamma is
-      // the same for every lane: wave-uniform loads)
+      // normalised: every thread of the block turns some of the chunk's
+      // 16-byte units into (x * r[t]) * gamma[c] in fp32 (the values each
+      // product takes), then every wave reads them; the row-to-lane and
+      // unit-to-slot maps match the x chunk's (slot = unit ^ (t & 15) for
+      // ActT, 2*unit + h ^ (t & 31) or unit ^ (t & 31) for the fp32 rows)
+      constexpr int kXnU = kPer / 4;   // fp32 units per ActT unit
+      const int xn_row = CB * 4;        // bytes
+      const int xn_sw = min(31, CB / 4 - 1);   // slot mask: 16-byte units per fp32 row - 1
+      const int nthr = nw * kWave;
+      for (int p = g * kWave + lane; p < kRT * units; p += nthr) {
+        const int t = p / units, u = p - t * units;
+        const uint4 xv = *reinterpret_cast<const uint4*>(st + t * xrow_bytes + ((u ^ (t & 15)) << 4));
+        const float rt = s_rr[t];
+        float o[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) o[i] = (widen<ActT>(xv, i) * rt) * nrm.gamma[c0 + u * kPer + i];
+#pragma unroll
+        for (int h = 0; h < kXnU; ++h)
+          *reinterpret_cast<float4*>(reinterpret_cast<char*>(xn_lds) + t * xn_row +
+                                     (((u * kXnU + h) ^ (t & xn_sw)) << 4)) =
+              make_float4(o[4 * h], o[4 * h + 1], o[4 * h + 2], o[4 * h + 3]);
+      }
+      lds_barrier();
+      const char* xnr = reinterpret_cast<const char*>(xn_lds) + lane * xn_row;
       for (int u = 0; u < units; ++u) {
-        const uint4 xv = *reinterpret_cast<const uint4*>(xr + ((u ^ (lane & 15)) << 4));
         float4 wv[kWU];
 #pragma unroll
         for (int v = 0; v < kWU; ++v)
           wv[v] = reinterpret_cast<const float4*>(wq + u * kPer * RE)[v];
         float xn[kPer];
 #pragma unroll
-        for (int i = 0; i < kPer; ++i) {
-          const float gm = nrm.gamma[c0 + u * kPer + i];
-          xn[i] = (widen<ActT>(xv, i) * r) * gm;
+        for (int h = 0; h < kXnU; ++h) {
+          const float4 q =
+              *reinterpret_cast<const float4*>(xnr + (((u * kXnU + h) ^ (lane & xn_sw)) << 4));
+          xn[4 * h] = q.x;
+          xn[4 * h + 1] = q.y;
+          xn[4 * h + 2] = q.z;
+          xn[4 * h + 3] = q.w;
         }
 #pragma unroll
         for (int v = 0; v < kWU; ++v) {
@@ -366,6 +428,7 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
           }
         }
       }
+      lds_barrier();   // every wave done with this chunk's fp32 rows
     }
     b ^= 1;
   }
@@ -538,7 +601,7 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
 // Fused router: a block owns kRT tokens (one per lane) and ceil(E/RE) waves;
 // wave g computes experts [g*RE, g*RE + RE) into LDS, then the block runs
 // softmax, top-k and its histogram.
-template <typename ActT, int RE>
+template <typename ActT, int RE, bool NORM>
 __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
     int N, int C, int E, int k, int32_t* __restrict__ topk_idx, float* __restrict__ topk_p,
@@ -547,7 +610,8 @@ __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
   __shared__ float s_l[kRT][kMaxExperts + 1];
   __shared__ float s_m[kRT];
   __shared__ int s_hist[kMaxExperts];
-  __shared__ __attribute__((aligned(1024))) char smem[kRouterLds];
+  // (NORM: nrm.gamma is set, and the normalised rows need kRouterNormLds more)
+  __shared__ __attribute__((aligned(1024))) char smem[kRouterLds + (NORM ? kRouterNormLds : 0)];
   const int tid = threadIdx.x;
   const int lane = lane_id();
   const int g = __builtin_amdgcn_readfirstlane(tid / kWave);   // expert group of this wave
@@ -556,8 +620,9 @@ __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
   if (tid < kMaxExperts) s_hist[tid] = 0;
   float acc[RE];
   float r = 1.0f;
-  logit_chains<ActT, RE>(x + (size_t)tok0 * C, N - tok0, wr_g, nw, nw, g, C, smem, acc, nrm, &r);
-  if (nrm.gamma && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
+  logit_chains<ActT, RE, NORM>(x + (size_t)tok0 * C, N - tok0, wr_g, nw, nw, g, C, smem, acc, nrm,
+                               &r);
+  if (NORM && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
 #pragma unroll
   for (int j = 0; j < RE; ++j) {
     const int e = g * RE + j;
@@ -574,21 +639,22 @@ __global__ __launch_bounds__(1024) void router_topk_uniform_kernel(
 // router_softmax_kernel finishes: the chains are as long as before, but
 // spread over more CUs.
 constexpr int kSplitExperts = 4;
-template <typename ActT>
+template <typename ActT, bool NORM>
 __global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
     const ActT* __restrict__ x, const float* __restrict__ wr1, const float* __restrict__ br,
     int N, int C, int E, float* __restrict__ logits, RowNorm nrm, float* __restrict__ rstd) {
-  __shared__ __attribute__((aligned(1024))) char smem[kRouterSplitLds];
+  __shared__ __attribute__((aligned(1024)))
+  char smem[kRouterSplitLds + (NORM ? kRouterNormLds : 0)];
   const int lane = lane_id();
   const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
   const int e0 = blockIdx.y * kSplitExperts;
   const int tok0 = blockIdx.x * kRT;
   float acc[1];
   float r = 1.0f;
-  logit_chains<ActT, 1>(x + (size_t)tok0 * C, N - tok0, wr1 + (size_t)e0 * C,
+  logit_chains<ActT, 1, NORM>(x + (size_t)tok0 * C, N - tok0, wr1 + (size_t)e0 * C,
                         min(kSplitExperts, E - e0), kSplitExperts, g, C, smem, acc, nrm, &r,
                         kRouterSplitLds);
-  if (nrm.gamma && blockIdx.y == 0 && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
+  if (NORM && blockIdx.y == 0 && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
   const int e = e0 + g;
   if (e < E && tok0 + lane < N) logits[(size_t)(tok0 + lane) * E + e] = acc[0] + br[e];
 }
@@ -1129,10 +1195,13 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
     return hipGetLastError();
   }
   if (logits) {
-    hipLaunchKernelGGL(router_logits_kernel<ActT>,
-                       dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
-                       dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits, nrm,
-                       rstd);
+    const dim3 lg(nb, (E + kSplitExperts - 1) / kSplitExperts), lb(kSplitExperts * kWave);
+    if (nrm.gamma)
+      hipLaunchKernelGGL((router_logits_kernel<ActT, true>), lg, lb, 0, stream, x, wr1, br, N, C,
+                         E, logits, nrm, rstd);
+    else
+      hipLaunchKernelGGL((router_logits_kernel<ActT, false>), lg, lb, 0, stream, x, wr1, br, N, C,
+                         E, logits, nrm, rstd);
     hipLaunchKernelGGL(router_softmax_kernel, dim3(nb), dim3(MGPT_SOFTMAX_THREADS), 0, stream,
                        logits, N, E, k,
                        topk_idx, topk_p, hist, nb, probs);
@@ -1141,18 +1210,23 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
   const int RE = router_experts_per_wave(E);
   const int waves = (E + RE - 1) / RE;
   const dim3 g(nb), b(waves * kWave);
+  auto fused = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, g, b, 0, stream, x, wr_g, br, N, C, E, k, topk_idx, topk_p, hist,
+                       nb, probs, nrm, rstd);
+  };
+  const bool norm = nrm.gamma != nullptr;
   switch (RE) {
     case 1:
-      hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 1>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb, probs, nrm, rstd);
+      norm ? fused(router_topk_uniform_kernel<ActT, 1, true>)
+           : fused(router_topk_uniform_kernel<ActT, 1, false>);
       break;
     case 2:
-      hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 2>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb, probs, nrm, rstd);
+      norm ? fused(router_topk_uniform_kernel<ActT, 2, true>)
+           : fused(router_topk_uniform_kernel<ActT, 2, false>);
       break;
     default:
-      hipLaunchKernelGGL((router_topk_uniform_kernel<ActT, 4>), g, b, 0, stream, x, wr_g, br, N,
-                         C, E, k, topk_idx, topk_p, hist, nb, probs, nrm, rstd);
+      norm ? fused(router_topk_uniform_kernel<ActT, 4, true>)
+           : fused(router_topk_uniform_kernel<ActT, 4, false>);
   }
   return hipGetLastError();
 }
