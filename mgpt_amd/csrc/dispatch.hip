@@ -72,13 +72,32 @@ __device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g
   for (int i = 0; i < 4; ++i) o.w[i] = __float_as_uint((__uint_as_float(v.w[i]) * r) * g[i]);
   return o;
 }
+// Two floats -> two bf16 in one word (v_cvt_pk_bf16_f32: nearest even,
+// fp32 denormals kept; f32_to_bf16's rounding in one instruction).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return u;
+}
+
 __device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g, bf16_t) {
+  float gv[8];
+  if (((uintptr_t)g & 15) == 0) {   // the chunk's 8 scales as two 16-byte loads
+    const float4 g0 = reinterpret_cast<const float4*>(g)[0], g1 = reinterpret_cast<const float4*>(g)[1];
+    gv[0] = g0.x; gv[1] = g0.y; gv[2] = g0.z; gv[3] = g0.w;
+    gv[4] = g1.x; gv[5] = g1.y; gv[6] = g1.z; gv[7] = g1.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) gv[i] = g[i];
+  }
   V16 o;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const float a = (__uint_as_float(v.w[i] << 16) * r) * g[2 * i];
-    const float b = (__uint_as_float(v.w[i] & 0xFFFF0000u) * r) * g[2 * i + 1];
-    o.w[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    const float a = (__uint_as_float(v.w[i] << 16) * r) * gv[2 * i];
+    const float b = (__uint_as_float(v.w[i] & 0xFFFF0000u) * r) * gv[2 * i + 1];
+    o.w[i] = pack_bf16x2(a, b);
   }
   return o;
 }
@@ -111,7 +130,7 @@ struct RowChunk {
           a = (a * r) * g[2 * i];
           b = (b * r) * g[2 * i + 1];
         }
-        o.w[i] = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+        o.w[i] = pack_bf16x2(a, b);
       }
       return o;
     }
