@@ -37,8 +37,7 @@ template <> struct Vec<bf16_t> {
   static __device__ __forceinline__ uint4 pack(const float (&v)[8]) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (uint32_t)f32_to_bf16(v[2 * i]) | ((uint32_t)f32_to_bf16(v[2 * i + 1]) << 16);
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     return make_uint4(w[0], w[1], w[2], w[3]);
   }
 };
@@ -523,9 +522,7 @@ template <> struct NbVec<bf16_t, 4> {
     v[3] = __uint_as_float(q.y & 0xFFFF0000u);
   }
   static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[4]) {
-    *reinterpret_cast<uint2*>(p) =
-        make_uint2((uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16),
-                   (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16));
+    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
   }
 };
 template <> struct NbVec<float, 4> {

@@ -28,16 +28,10 @@ struct Vec16<bf16_t> {
     }
   }
   static __device__ __forceinline__ void store(bf16_t* p, const float (&v)[8]) {
-    // v_cvt_pk_bf16_f32: nearest even, fp32 denormals kept (f32_to_bf16's
-    // rounding, one instruction per pair)
-    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
     uint4 u;
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bf16x2_t h = {(__bf16)v[2 * i], (__bf16)v[2 * i + 1]};
-      __builtin_memcpy(&w[i], &h, 4);
-    }
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
     u.x = w[0]; u.y = w[1]; u.z = w[2]; u.w = w[3];
     *reinterpret_cast<uint4*>(p) = u;
   }

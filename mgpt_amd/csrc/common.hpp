@@ -68,6 +68,17 @@ __host__ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
   return (bf16_t)(u >> 16);
 }
 
+// Two floats -> two bf16 in one word, the first in the low half
+// (v_cvt_pk_bf16_f32: nearest even, fp32 denormals kept; f32_to_bf16's
+// rounding in one instruction).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return u;
+}
+
 template <typename T> struct ActTraits;
 template <> struct ActTraits<float> {
   static __device__ __forceinline__ float load(const float* p) { return *p; }

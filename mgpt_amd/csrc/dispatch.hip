@@ -72,16 +72,6 @@ __device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g
   for (int i = 0; i < 4; ++i) o.w[i] = __float_as_uint((__uint_as_float(v.w[i]) * r) * g[i]);
   return o;
 }
-// Two floats -> two bf16 in one word (v_cvt_pk_bf16_f32: nearest even,
-// fp32 denormals kept; f32_to_bf16's rounding in one instruction).
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const bf16x2_t v = {(__bf16)a, (__bf16)b};
-  uint32_t u;
-  __builtin_memcpy(&u, &v, 4);
-  return u;
-}
-
 __device__ __forceinline__ V16 normalize16(const V16& v, float r, const float* g, bf16_t) {
   float gv[8];
   if (((uintptr_t)g & 15) == 0) {   // the chunk's 8 scales as two 16-byte loads
