@@ -19,7 +19,13 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 constexpr int kNumXcd = 8;        // MI355X: 8 accelerator complex dies, one L2 each
+// Experts the kernels that map one expert to one lane of a wave take (the
+// fused prefill and decode routers, the 256 x 256 and weight-streaming
+// GEMMs, the backward); up to kMaxExpertsWide the forward runs the split
+// router, the generic grouped GEMM and a permute that scans the experts in
+// wave-sized chunks.
 constexpr int kMaxExperts = 64;
+constexpr int kMaxExpertsWide = 256;
 constexpr int kMaxTopK = 8;
 // Tokens per router / permute block: block b owns tokens [b*64, (b+1)*64)
 // and so the flat assignment ids [b*64*k, (b+1)*64*k).
@@ -113,8 +119,8 @@ __device__ __forceinline__ int wave_sum(int v) {
 
 // Which expert segment an m-tile belongs to.  Grouped GEMMs launch a grid
 // over an upper bound of m-tiles; each block derives its expert, the
-// segment's first row and its end row from the per-expert counts (E <= 64),
-// so no host round-trip is needed.  Returns false for blocks past the last
+// segment's first row and its end row from the per-expert counts (wave 0
+// scans them 64 experts at a time, any E), so no host round-trip is needed.  Returns false for blocks past the last
 // tile.  Must be called by every thread of the block (uses shared memory);
 // it may be called repeatedly (persistent kernels).
 struct TileInfo {
@@ -130,18 +136,29 @@ __device__ __forceinline__ bool find_tile(const int32_t* __restrict__ counts, in
   __syncthreads();   // every wave has read the previous call's result
   if (threadIdx.x < kWave) {
     const int l = lane_id();
-    int cnt = (l < E) ? counts[l] : 0;
-    int tiles = (cnt + BM - 1) / BM;
-    int rows_incl = wave_incl_scan(cnt);
-    int tiles_incl = wave_incl_scan(tiles);
-    int tiles_excl = tiles_incl - tiles;
-    bool mine = (l < E) && (mtile >= tiles_excl) && (mtile < tiles_incl);
-    unsigned long long m = __ballot(mine);
-    int owner = m ? (__ffsll((long long)m) - 1) : 0;
-    int row0 = __shfl((rows_incl - cnt) + (mtile - tiles_excl) * BM, owner, kWave);
-    int rend = __shfl(rows_incl, owner, kWave);
+    int rows_carry = 0, tiles_carry = 0, found = -1, row0 = 0, rend = 0;
+    for (int e0 = 0; e0 < E && found < 0; e0 += kWave) {
+      const int e = e0 + l;
+      const int cnt = (e < E) ? counts[e] : 0;
+      const int tiles = (cnt + BM - 1) / BM;
+      const int rows_incl = wave_incl_scan(cnt) + rows_carry;
+      const int tiles_incl = wave_incl_scan(tiles) + tiles_carry;
+      const int tiles_excl = tiles_incl - tiles;
+      const bool mine = (e < E) && (mtile >= tiles_excl) && (mtile < tiles_incl);
+      const unsigned long long m = __ballot(mine);
+      const int owner = m ? (__ffsll((long long)m) - 1) : 0;
+      const int r0 = __shfl((rows_incl - cnt) + (mtile - tiles_excl) * BM, owner, kWave);
+      const int re = __shfl(rows_incl, owner, kWave);
+      if (m) {
+        found = e0 + owner;
+        row0 = r0;
+        rend = re;
+      }
+      rows_carry = __shfl(rows_incl, kWave - 1, kWave);
+      tiles_carry = __shfl(tiles_incl, kWave - 1, kWave);
+    }
     if (l == 0) {
-      s_info[0] = m ? owner : -1;
+      s_info[0] = found;
       s_info[1] = row0;
       s_info[2] = rend;
     }

@@ -13,7 +13,8 @@
 // needs itself (E x nb ints, L2-resident), so the scan costs no launch of
 // its own; large ones scan first (expert_scan_kernel).
 // The within-block rank comes from wave ballots over 64 consecutive ids at
-// a time (6 ballots give the lanes holding the same expert id, E <= 64).
+// a time (one ballot per bit of the expert ids: 6 for E <= 64, 8 for
+// E <= 256).
 // The permute kernel then copies each token's row once from HBM into all k
 // of its slots with 16-byte loads and stores.
 #include "common.hpp"
@@ -139,10 +140,10 @@ __global__ __launch_bounds__(256) void permute_kernel(
     int E, int k, int32_t* __restrict__ counts, int32_t* __restrict__ perm,
     int32_t* __restrict__ slot_of, ActT* __restrict__ xg, const float* __restrict__ rstd,
     const float* __restrict__ gamma) {
-  __shared__ int s_base[kMaxExperts];
-  __shared__ int s_pre[kMaxExperts];
-  __shared__ int s_tot[kMaxExperts];
-  __shared__ int s_run[kMaxExperts];
+  __shared__ int s_base[kMaxExpertsWide];
+  __shared__ int s_pre[kMaxExpertsWide];
+  __shared__ int s_tot[kMaxExpertsWide];
+  __shared__ int s_run[kMaxExpertsWide];
   __shared__ int s_slot[kRouterTokens * kMaxTopK];
   const int tid = threadIdx.x;
   const int b = blockIdx.x;
@@ -244,20 +245,26 @@ __global__ __launch_bounds__(256) void permute_kernel(
   __syncthreads();
   if (tid < kWave) {
     // Exclusive offsets of the experts, then this block's bases; block
-    // (0, 0) publishes the counts for the GEMMs and the caller.
-    const int l = tid;
-    const int cnt = (l < E) ? s_tot[l] : 0;
-    const int excl = wave_incl_scan(cnt) - cnt;
-    if (l < E) {
-      s_base[l] = excl + s_pre[l];
-      s_run[l] = 0;
-      if (!base && writer && b == 0) counts[l] = cnt;
+    // (0, 0) publishes the counts for the GEMMs and the caller.  A wave
+    // scans 64 experts at a time, carrying the total forward.
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += kWave) {
+      const int l = e0 + tid;
+      const int cnt = (l < E) ? s_tot[l] : 0;
+      const int incl = wave_incl_scan(cnt);
+      if (l < E) {
+        s_base[l] = carry + incl - cnt + s_pre[l];
+        s_run[l] = 0;
+        if (!base && writer && b == 0) counts[l] = cnt;
+      }
+      carry += __shfl(incl, kWave - 1, kWave);
     }
   }
   __syncthreads();
   if (tid < kWave) {
     const int l = tid;
     const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (kWave - l));
+    const int id_bits = E > kMaxExperts ? 8 : 6;
 #pragma unroll
     for (int u = 0; u < kIdPerLane; ++u) {
       const int f0 = u * kWave;
@@ -270,7 +277,8 @@ __global__ __launch_bounds__(256) void permute_kernel(
       if (!valid) e = 0;
       unsigned long long match = __ballot(valid);
 #pragma unroll
-      for (int bit = 0; bit < 6; ++bit) {
+      for (int bit = 0; bit < 8; ++bit) {
+        if (bit >= id_bits) break;   // ids < 2^id_bits
         const unsigned long long on = __ballot(valid && ((e >> bit) & 1));
         match &= ((e >> bit) & 1) ? on : ~on;
       }
@@ -342,6 +350,7 @@ hipError_t launch_permute(const InT* x, const int32_t* topk_idx, const int32_t* 
   if (nb == 0) return hipSuccess;
   const bool fold = E * nb <= kFoldScan;
   if (!hist && nb != 1) return hipErrorInvalidValue;   // counting the ids needs one block
+  if (E > kMaxExpertsWide) return hipErrorInvalidValue;
   if (!fold)
     hipLaunchKernelGGL(expert_scan_kernel, dim3(E), dim3(256), 0, stream, hist, nb, base, counts);
   // Column slices: enough blocks for ~512 in all, each slice >= 8 chunks

@@ -277,11 +277,14 @@ struct mgpt_moe {
   bool padded() const { return Cx != C; }
   // Few tokens and many experts: the router's logits are spread over more
   // blocks (one expert per wave) instead of one block per 64 tokens.
-  bool router_split(int N) const { return E > 16 && N < 4096; }
+  bool router_split(int N) const { return E > 16 && (N < 4096 || wide()); }
+  // more experts than a wave has lanes: the forward's generic paths only
+  bool wide() const { return E > kMaxExperts; }
   // one router block of tokens: logits and softmax in one launch, and the
   // permute counts the ids itself (no histogram)
   bool router_one_launch(int N, bool norm) const {
-    return wr4 && N <= kRouterTokens && !norm && C % 64 == 0 && C <= kDecodeRouterMaxC;
+    return wr4 && !wide() && N <= kRouterTokens && !norm && C % 64 == 0 &&
+           C <= kDecodeRouterMaxC;
   }
   // The bf16 large-M path (gemm_dma.hip), which may split its last round.
   // bias partials of the weight gradients' row chunks: at most 64 chunks of
@@ -291,7 +294,7 @@ struct mgpt_moe {
     return (size_t)64 * ((std::max(2 * Hp, C) + 255) / 256) * 256 * 4;
   }
   bool uses_gemm_dma(int N) const {
-    return act == MGPT_DTYPE_BF16 && wdt == MGPT_DTYPE_BF16 && gemm_tile == 256 &&
+    return act == MGPT_DTYPE_BF16 && wdt == MGPT_DTYPE_BF16 && gemm_tile == 256 && !wide() &&
            (size_t)N * k >= (size_t)64 * E;
   }
   size_t w_bytes() const { return wdt == MGPT_DTYPE_FP8_E4M3 ? 1 : (wdt == MGPT_DTYPE_BF16 ? 2 : 4); }
@@ -316,7 +319,9 @@ struct mgpt_moe {
     L.counts = take((size_t)E * 4);
     // Sized for min(N, 4095) tokens whenever E > 16, so that the workspace
     // never shrinks as N grows past the split router's range.
-    L.logits = take(E > 16 ? (size_t)std::min(N, 4095) * E * 4 : 0);
+    // (every N when E > 64: the wide forward always routes through the
+    // split logits)
+    L.logits = take(E > 16 ? (size_t)(wide() ? N : std::min(N, 4095)) * E * 4 : 0);
     L.xg = take((A + kRowPad) * C * act_bytes());
     L.hbuf = take((A + kRowPad) * Hp * act_bytes());
     L.obuf = take((A + kRowPad) * C * act_bytes());
@@ -359,8 +364,8 @@ int check_config(const mgpt_moe_config* c) {
     return fail(MGPT_ERR_INVALID_ARGUMENT,
                 "invalid shape: embed_dim=%d hidden_dim=%d num_experts=%d top_k=%d",
                 c->embed_dim, c->hidden_dim, c->num_experts, c->top_k);
-  if (c->num_experts > kMaxExperts)
-    return fail(MGPT_ERR_UNSUPPORTED, "num_experts %d > %d", c->num_experts, kMaxExperts);
+  if (c->num_experts > kMaxExpertsWide)
+    return fail(MGPT_ERR_UNSUPPORTED, "num_experts %d > %d", c->num_experts, kMaxExpertsWide);
   if (c->top_k > kMaxTopK)
     return fail(MGPT_ERR_UNSUPPORTED, "top_k %d > %d", c->top_k, kMaxTopK);
   // fp32 activations with bf16 / fp8 weights: the caller's tensors stay
@@ -389,7 +394,9 @@ void free_weights(mgpt_moe* h) {
 // Training is built for bf16 x bf16 and fp32 x fp32 handles (fp8 weights
 // are an inference format here, and fp32 tensors over bf16 products an
 // inference option).
-bool trainable(const mgpt_moe* h) { return h->wdt == h->act && h->io == h->act; }
+bool trainable(const mgpt_moe* h) {
+  return h->wdt == h->act && h->io == h->act && !h->wide();
+}
 
 // Allocates the gradient buffer on first use, its contents logically zero.
 int ensure_grad(mgpt_moe* h) {
@@ -806,7 +813,8 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
   // training caches): the gate/up weight-streaming GEMM routes the ids
   // itself and reads the caller's rows of x (bf16, or fp32 rounded as the
   // permute would), so no permute runs.
-  const bool gather_decode = !train && !gamma && h->wdt == MGPT_DTYPE_FP8_E4M3 && h->wgu_t &&
+  const bool gather_decode = !train && !gamma && !h->wide() && h->wdt == MGPT_DTYPE_FP8_E4M3 &&
+                             h->wgu_t &&
                              small_m(h, N) && A <= (size_t)kRouterTokens * kMaxTopK;
   if (!gather_decode)
     HIP_TRY((launch_permute<IoT, ActT>(xi, idx, one_launch ? nullptr : hist, base, N, C, E, k,
@@ -826,7 +834,7 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
     const bool fp8 = h->wdt == MGPT_DTYPE_FP8_E4M3;
     if (small_m(h, N)) {
       const int mt = (int)((A + 31) / 32) + E;
-      if (fp8 && h->wgu_t) {
+      if (fp8 && h->wgu_t && !h->wide()) {
         // weight streaming: the persistent direct-to-LDS decode kernel on the
         // tiled copies
         if (gather_decode)
@@ -857,7 +865,7 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
             mt, nullptr, 0, st)));
       }
-    } else if (h->gemm_tile == 256 && !fp8) {
+    } else if (h->gemm_tile == 256 && !fp8 && !h->wide()) {
       // bf16 weights, prefill-shaped segments: 256x256 direct-to-LDS kernel.
       const int mt = (int)((A + 255) / 256) + E;
       float* part = (float*)(ws + L.partials);
@@ -1149,7 +1157,7 @@ int check_grad_args(const mgpt_moe* h, float* const* grads, int num_params) {
   for (int i = 0; i < num_params; ++i)
     if (!grads[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "gradient %d is null", i);
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
   return MGPT_OK;
 }
 
@@ -1221,7 +1229,7 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens, 
   if (int rc = check_forward_args(h, x, y, num_tokens, workspace, workspace_bytes, true))
     return rc;
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
   if (num_tokens == 0) return MGPT_OK;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
@@ -1237,7 +1245,7 @@ int backward_entry(mgpt_moe* h, const void* x, const void* dy, void* dx, int num
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
   if (num_tokens < 0) return fail(MGPT_ERR_INVALID_ARGUMENT, "negative num_tokens");
   if (num_tokens == 0) return MGPT_OK;
   if (!x || !dy || !dx || !workspace)
@@ -1303,7 +1311,7 @@ int mgpt_moe_forward_block_train(mgpt_moe* h, const void* x, const float* gamma,
   if (int rc = check_forward_args(h, x, out, num_tokens, workspace, workspace_bytes, true))
     return rc;
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
   if (num_tokens == 0) return MGPT_OK;
   if (!gamma) return fail(MGPT_ERR_INVALID_ARGUMENT, "null gamma");
   if (!(eps >= 0.0f)) return fail(MGPT_ERR_INVALID_ARGUMENT, "eps must be >= 0");
@@ -1326,7 +1334,7 @@ int mgpt_moe_backward_block(mgpt_moe* h, const void* x, const float* gamma, cons
 int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
   HIP_TRY(hipSetDevice(h->device));
   if (int rc = ensure_grad(h)) return rc;
   hipStream_t st = (hipStream_t)stream;

@@ -449,8 +449,8 @@ __device__ __forceinline__ void logit_chains(const ActT* __restrict__ xblk, int 
 // LDS atomics.  (The layout used for E > 32, L lanes per token merging
 // partial maxima and top-k lists with shuffles, took 8.2 k cycles per block
 // at cfg3 against 6.2 k here, barriers included.)
-template <int EP>
-__device__ __forceinline__ void softmax_topk_group(float (*s_l)[kMaxExperts + 1], int* s_hist,
+template <int EP, int LD = kMaxExperts + 1>
+__device__ __forceinline__ void softmax_topk_group(float (*s_l)[LD], int* s_hist,
                                                    const uint64_t* tab, int tok0, int N, int E,
                                                    int k, int32_t* __restrict__ topk_idx,
                                                    float* __restrict__ topk_p,
@@ -513,7 +513,8 @@ __device__ __forceinline__ void softmax_topk_group(float (*s_l)[kMaxExperts + 1]
 // algorithm, then the sequential sum, the clamp and the top-k
 // (softmax_topk_lanes).  The histogram counts are written expert-major as
 // hist[e][block].
-__device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1], float* s_m,
+template <int LD = kMaxExperts + 1>
+__device__ __forceinline__ void softmax_topk_block(float (*s_l)[LD], float* s_m,
                                                    int* s_hist, int tok0, int N, int E, int k,
                                                    int32_t* __restrict__ topk_idx,
                                                    float* __restrict__ topk_p,
@@ -525,15 +526,15 @@ __device__ __forceinline__ void softmax_topk_block(float (*s_l)[kMaxExperts + 1]
     if (tid < 32) s_tab32[tid] = c_exp2_tab[tid];
     __syncthreads();   // the table, and the logits the caller wrote
     if (E <= 2)
-      softmax_topk_group<2>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+      softmax_topk_group<2, LD>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
     else if (E <= 4)
-      softmax_topk_group<4>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+      softmax_topk_group<4, LD>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
     else if (E <= 8)
-      softmax_topk_group<8>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+      softmax_topk_group<8, LD>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
     else if (E <= 16)
-      softmax_topk_group<16>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+      softmax_topk_group<16, LD>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
     else
-      softmax_topk_group<32>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
+      softmax_topk_group<32, LD>(s_l, s_hist, s_tab32, tok0, N, E, k, topk_idx, topk_p, probs);
     __syncthreads();
     if (tid < E) hist[(size_t)tid * num_blocks + blockIdx.x] = s_hist[tid];
     return;
@@ -678,6 +679,27 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
   }
   __syncthreads();
   softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks, probs);
+}
+
+// router_softmax_kernel for more experts than a wave has lanes (up to
+// kMaxExpertsWide): the same per-token passes over a wider row in LDS.
+__global__ __launch_bounds__(1024) void router_softmax_wide_kernel(
+    const float* __restrict__ logits, int N, int E, int k, int32_t* __restrict__ topk_idx,
+    float* __restrict__ topk_p, int32_t* __restrict__ hist, int num_blocks,
+    float* __restrict__ probs) {
+  __shared__ float s_l[kRT][kMaxExpertsWide + 1];
+  __shared__ float s_m[kRT];
+  __shared__ int s_hist[kMaxExpertsWide];
+  const int tid = threadIdx.x;
+  const int tok0 = blockIdx.x * kRT;
+  if (tid < kMaxExpertsWide) s_hist[tid] = 0;
+  for (int p = tid; p < kRT * E; p += blockDim.x) {
+    const int r = p / E, e = p % E;
+    s_l[r][e] = tok0 + r < N ? logits[(size_t)(tok0 + r) * E + e] : 0.0f;
+  }
+  __syncthreads();
+  softmax_topk_block<kMaxExpertsWide + 1>(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p,
+                                          hist, num_blocks, probs);
 }
 
 // Logits for decode shapes with the products and the chains on different
@@ -1176,6 +1198,22 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
   const RowNorm nrm{gamma, eps, cn};
   const int nb = (N + kRT - 1) / kRT;
   if (nb == 0) return hipSuccess;
+  if (E > kMaxExperts) {
+    // wide: per-expert logits (the split kernels, any E), then the block
+    // softmax / top-k over rows of up to kMaxExpertsWide
+    if (E > kMaxExpertsWide || !logits || wr4) return hipErrorInvalidValue;
+    if (gamma)
+      hipLaunchKernelGGL((router_logits_kernel<ActT, true>),
+                         dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
+                         dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits, nrm,
+                         rstd);
+    else
+      hipLaunchKernelGGL((router_logits_pc_kernel<ActT>), dim3(nb, E), dim3(256), 0, stream, x,
+                         wr1, br, N, C, E, logits, hist, nb);
+    hipLaunchKernelGGL(router_softmax_wide_kernel, dim3(nb), dim3(1024), 0, stream, logits, N, E,
+                       k, topk_idx, topk_p, hist, nb, probs);
+    return hipGetLastError();
+  }
   if (wr4) {
     if (N > kRT || E <= 16 || E > kMaxExperts || gamma || C % 64 || C > kDecodeRouterMaxC)
       return hipErrorInvalidValue;

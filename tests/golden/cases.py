@@ -55,6 +55,18 @@ UNIT_CASES = [
     Case("fp8_large_m", _c("fp8_large_m", 900, 256, 4, 2, 256, "bf16", "fp8", rb="normal"), 0.02),
 ]
 
+# More experts than a wave has lanes (E > 64): the forward's wide paths
+# (split router with the wide softmax, wave-chunked permute scan, generic
+# grouped GEMMs); training refuses these handles.
+WIDE_CASES = [
+    Case("wide_e128_k8", _c("wide_e128_k8", 96, 128, 128, 8, 64, "bf16", rb="zipf"), 0.02),
+    Case("wide_e256_f32", _c("wide_e256_f32", 80, 64, 256, 4, 48, rb="normal"), 0.05),
+    Case("wide_e96_large", _c("wide_e96_large", 3000, 128, 96, 6, 96, "bf16"), 0.02,
+         full_arrays=False),
+    Case("wide_e200_fp8", _c("wide_e200_fp8", 40, 128, 200, 8, 128, "bf16", "fp8", rb="normal"),
+         0.02),
+]
+
 CONFIG_CASES = [
     Case("cfg1", wl.CONFIGS["cfg1"], full_arrays=True),
     Case("cfg2", wl.CONFIGS["cfg2"], full_arrays=False),
@@ -63,7 +75,7 @@ CONFIG_CASES = [
     Case("cfg5", wl.CONFIGS["cfg5"], full_arrays=True),
 ]
 
-ALL_CASES = {c.name: c for c in UNIT_CASES + CONFIG_CASES}
+ALL_CASES = {c.name: c for c in UNIT_CASES + WIDE_CASES + CONFIG_CASES}
 
 
 def build_inputs(case: Case) -> wl.MoEInputs:

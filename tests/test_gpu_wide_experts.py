@@ -1,0 +1,125 @@
+"""GPU parity of the forward with more experts than a wave has lanes
+(64 < E <= 256), against the reference.
+
+The reference's layer takes any expert count (pipeline/CLIConfig.h:177-178).
+Here such handles run the split router (per-expert logits, then a block
+softmax / top-k over rows of up to 256 experts), the permute's offsets scan
+in wave-sized chunks with eight ballots on the expert ids, and the generic
+grouped GEMMs whose tile lookup scans the counts 64 experts at a time.
+Routing must be bit-exact with the committed fixtures of the compiled
+reference (full arrays for the small cases, digests for the large one);
+outputs are compared with the oracle's fp32 forward at 1e-5 (fp32), 2e-2
+(bf16), 6e-2 (fp8 weights), normwise and elementwise, as in
+tests/test_gpu_parity.py.  The fused block runs the same wide router with
+normalisation.  Training such handles is refused (the backward's kernels
+map one expert to one lane).
+"""
+import numpy as np
+import pytest
+
+import cases as C
+import oracle_lib as O
+from test_gpu_parity import TOL, check_close, check_routing, fixture, run_gpu
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+WIDE = [c.name for c in C.WIDE_CASES]
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from mgpt_amd import capi
+    capi.lib()   # fail loudly if the HIP library is missing
+    return torch.device("cuda", 0)
+
+
+@pytest.mark.parametrize("name", WIDE)
+def test_wide_forward_parity(name):
+    case = C.ALL_CASES[name]
+    print(f"case {name}: {case.cfg}", flush=True)
+    fx = fixture(name)
+    inp = C.build_inputs(case)
+    layer, y, r, counts_host, _ = run_gpu(inp)
+    check_routing(r, fx, full=case.full_arrays)
+    assert counts_host == [float(c) for c in fx["counts"]]
+    ref = O.forward(inp)   # every token (a few seconds at most)
+    check_close(y, ref["y"], TOL[case.cfg.weights], name)
+    if "rows" in fx.files:
+        check_close(y[fx["rows"]], fx["y_rows"], TOL[case.cfg.weights], name + " reference rows")
+
+
+def test_wide_fused_block():
+    """out = x + MoE(RMSNorm(x) * gamma) with E = 128: the wide router
+    normalises the rows (1/rms bit-exact), routing bit-exact with the
+    oracle's block, out at the bf16 bar."""
+    from mgpt_amd import workload as wl
+    cfg = wl.MoEConfig("wide_blk", 150, 128, 128, 4, 64, "bf16", "bf16", "normal")
+    inp = wl.make_inputs(cfg, C.SEED + 77, bias_std=0.02)
+    N = cfg.N
+    t = np.arange(N)
+    x1 = wl.bf16_round((inp.x * (np.float32(1.0) + (t % 4).astype(np.float32))[:, None])
+                       .astype(np.float32))
+    gamma = (np.float32(1.0) + wl.normal_f32(C.SEED, 4013, cfg.C, std=0.2)).astype(np.float32)
+    inp.Wr[:] = wl.bf16_round(inp.Wr)
+    from mgpt_amd.moe import MoELayer
+    layer = MoELayer(cfg.C, cfg.H, cfg.E, cfg.k, act="bf16", weights="bf16")
+    layer.load_parameters(inp.params(raw=True))
+    xd = torch.from_numpy(x1).cuda().to(torch.bfloat16)
+    out = layer.forward_block(xd, torch.from_numpy(gamma).cuda(), C.BLOCK_EPS)
+    torch.cuda.synchronize()
+    r = {k: v.cpu().numpy() for k, v in layer.routing().items()}
+    ref = O.block(inp, x1, gamma, C.BLOCK_EPS)
+    assert np.array_equal(layer.rstd().cpu().numpy().view(np.uint32), ref["rstd"].view(np.uint32))
+    assert np.array_equal(r["counts"], ref["counts"])
+    assert np.array_equal(r["topk_idx"], ref["idx"])
+    assert np.array_equal(r["topk_p"].view(np.uint32), ref["topp"].view(np.uint32))
+    assert np.array_equal(r["perm"], ref["perm"])
+    check_close(out.float().cpu().numpy(), ref["out"], TOL["bf16"], "wide block")
+
+
+def test_wide_repeats_and_graph_replay():
+    """Two eager forwards and a captured graph's replays give the same bits
+    (no state carried between calls; the histogram is rewritten each time)."""
+    case = C.ALL_CASES["wide_e128_k8"]
+    inp = C.build_inputs(case)
+    layer, y, r, _, ys = run_gpu(inp, repeat=2)
+    assert np.array_equal(ys[0], ys[1])
+    x = torch.from_numpy(np.ascontiguousarray(inp.x)).cuda().to(torch.bfloat16)
+    out = torch.empty_like(x)
+    layer.forward_into(x, out)   # workspace at this N before capture
+    s = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s), torch.cuda.graph(g, stream=s):
+        layer.forward_into(x, out)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.float().cpu().numpy(), y)
+
+
+def test_wide_training_is_refused():
+    from mgpt_amd import capi
+    from mgpt_amd.moe import MoELayer
+    case = C.ALL_CASES["wide_e256_f32"]
+    inp = C.build_inputs(case)
+    cfg = inp.cfg
+    layer = MoELayer(cfg.C, cfg.H, cfg.E, cfg.k, act=cfg.act, weights=cfg.weights)
+    layer.load_parameters(inp.params(raw=True))
+    x = torch.from_numpy(inp.x).cuda()
+    with pytest.raises(capi.MoEError) as err:
+        layer.forward(x, train=True)
+    assert err.value.status == capi.MGPT_ERR_UNSUPPORTED
+
+
+def test_more_than_256_experts_is_refused():
+    from mgpt_amd import capi
+    from mgpt_amd.moe import MoELayer
+    with pytest.raises(capi.MoEError) as err:
+        MoELayer(64, 64, 257, 2, act="f32")
+    assert err.value.status == capi.MGPT_ERR_UNSUPPORTED
