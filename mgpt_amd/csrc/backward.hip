@@ -120,26 +120,66 @@ __global__ __launch_bounds__(256) void token_dl_kernel(const int32_t* __restrict
   if (live) dL[(size_t)gid * E + e] = p * (dp - sum);
 }
 
+// token_dl_kernel for more experts than a wave has lanes: one wave per
+// token, lane l holding experts l, l + 64, ... (their terms added in that
+// order, then the same shuffle tree over the lanes).
+__global__ __launch_bounds__(256) void token_dl_wide_kernel(const int32_t* __restrict__ topk_idx,
+                                                            const float* __restrict__ dtp,
+                                                            const float* __restrict__ probs,
+                                                            const int32_t* __restrict__ counts,
+                                                            int N, int E, int k,
+                                                            float* __restrict__ dL) {
+  constexpr int kPerLane = kMaxExpertsWide / kWave;
+  const int gid = blockIdx.x * 4 + (int)threadIdx.x / kWave;
+  if (gid >= N) return;   // wave-uniform
+  const int l = lane_id();
+  float dp[kPerLane], p[kPerLane];
+  float sum = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kPerLane; ++u) {
+    const int e = l + u * kWave;
+    dp[u] = 0.0f;
+    p[u] = 0.0f;
+    if (e < E) {
+      const float fe = (float)counts[e] / (float)N;
+      const float lb = (0.01f * (float)E * fe) / (float)N;
+      float sel = 0.0f;
+      for (int j = 0; j < k; ++j)
+        if (topk_idx[(size_t)gid * k + j] == e) sel = dtp[(size_t)gid * k + j];
+      dp[u] = sel + lb;
+      p[u] = probs[(size_t)gid * E + e];
+    }
+    sum += dp[u] * p[u];
+  }
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) sum += __shfl_xor(sum, m, kWave);
+#pragma unroll
+  for (int u = 0; u < kPerLane; ++u) {
+    const int e = l + u * kWave;
+    if (e < E) dL[(size_t)gid * E + e] = p[u] * (dp[u] - sum);
+  }
+}
+
 constexpr int kDxTokens = 8;   // tokens per token_dx wave
 
 // dx of kDxTokens tokens x 512 columns per wave (8 columns per lane):
 // the sum of the tokens' slot rows of dX_e in ascending slot order (the
 // gather backward) plus dL . W_r^T (wrt = W_r as [E][C]; experts in
 // ascending order, 4 experts' weights loaded at a time, fused multiply-adds).
-template <typename ActT>
+template <typename ActT, int EMAX>
 __global__ __launch_bounds__(64) void token_dx_kernel(const ActT* __restrict__ dxe,
                                                       const int32_t* __restrict__ slot_of,
                                                       const float* __restrict__ dL,
                                                       const float* __restrict__ wrt, int N, int C,
                                                       int E, int k, ActT* __restrict__ dx) {
   using V = Vec<ActT>;
-  __shared__ float s_dl[kDxTokens][kMaxExperts];
+  __shared__ float s_dl[kDxTokens][EMAX];
   __shared__ int s_slot[kDxTokens][kMaxTopK];
   const int lane = lane_id();
   const int t0 = blockIdx.x * kDxTokens;
   const int nt = min(kDxTokens, N - t0);
-  for (int p = lane; p < kDxTokens * kMaxExperts; p += kWave) {
-    const int r = p / kMaxExperts, e = p % kMaxExperts;
+  for (int p = lane; p < kDxTokens * EMAX; p += kWave) {
+    const int r = p / EMAX, e = p % EMAX;
     s_dl[r][e] = (r < nt && e < E) ? dL[(size_t)(t0 + r) * E + e] : 0.0f;
   }
   if (lane < nt) {
@@ -277,16 +317,20 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
   const int chunk = blockIdx.y;
   const int c0 = (blockIdx.x * 256 + tid) * CPT;
   const int t0 = chunk * kRwChunk, nt = min(kRwChunk, N - t0);
+  // experts [e_base, e_base + Eg) of this block (one group of EP unless
+  // E > 64: then blockIdx.z walks the groups)
+  const int e_base = blockIdx.z * EP;
+  const int Eg = min(EP, E - e_base);
   float* sl = reinterpret_cast<float*>(s_dl);
   for (int p = tid; p < kRwChunk * EP; p += 256) {
     const int r = p / EP, e = p % EP;
-    sl[p] = (r < nt && e < E) ? dL[(size_t)(t0 + r) * E + e] : 0.0f;
+    sl[p] = (r < nt && e < Eg) ? dL[(size_t)(t0 + r) * E + e_base + e] : 0.0f;
   }
   __syncthreads();
-  if (blockIdx.x == 0 && tid < E) {
+  if (blockIdx.x == 0 && tid < Eg) {
     float bsum = 0.0f;
     for (int r = 0; r < nt; ++r) bsum += sl[r * EP + tid];
-    partial_b[(size_t)chunk * E + tid] = bsum;
+    partial_b[(size_t)chunk * E + e_base + tid] = bsum;
   }
   if (c0 >= C) return;   // C is a multiple of CPT
   float acc[CPT][EP];
@@ -338,10 +382,10 @@ __global__ __launch_bounds__(256) void router_wgrad_kernel(const ActT* __restric
     if (r0 + 2 * kG < nt) load(r0 + 2 * kG, xa);
     fmas(r0 + kG, xb);
   }
-  float* o = partial + (size_t)chunk * C * E + c0;
+  float* o = partial + (size_t)chunk * C * E + (size_t)e_base * C + c0;
 #pragma unroll
   for (int e = 0; e < EP; ++e) {
-    if (e >= E) break;
+    if (e >= Eg) break;
     if constexpr (CPT == 4) {
       *reinterpret_cast<float4*>(o + (size_t)e * C) =
           make_float4(acc[0][e], acc[1][e], acc[2][e], acc[3][e]);
@@ -438,8 +482,11 @@ hipError_t launch_token_bwd(const ActT* dxe, const int32_t* slot_of, const int32
                             const float* wrt, int N, int C, int E, int k, ActT* dx, float* dL,
                             hipStream_t stream) {
   if (N <= 0) return hipSuccess;
-  if (E > kMaxExperts || k > kMaxTopK || C % 8) return hipErrorInvalidValue;
-  if (E <= 16)
+  if (E > kMaxExpertsWide || k > kMaxTopK || C % 8) return hipErrorInvalidValue;
+  if (E > kMaxExperts)
+    hipLaunchKernelGGL(token_dl_wide_kernel, dim3((N + 3) / 4), dim3(256), 0, stream, topk_idx,
+                       dtp, probs, counts, N, E, k, dL);
+  else if (E <= 16)
     hipLaunchKernelGGL(token_dl_kernel<16>, dim3((N + 15) / 16), dim3(256), 0, stream, topk_idx,
                        dtp, probs, counts, N, E, k, dL);
   else if (E <= 32)
@@ -448,8 +495,13 @@ hipError_t launch_token_bwd(const ActT* dxe, const int32_t* slot_of, const int32
   else
     hipLaunchKernelGGL(token_dl_kernel<64>, dim3((N + 3) / 4), dim3(256), 0, stream, topk_idx,
                        dtp, probs, counts, N, E, k, dL);
-  hipLaunchKernelGGL(token_dx_kernel<ActT>, dim3((N + kDxTokens - 1) / kDxTokens, (C + 511) / 512),
-                     dim3(64), 0, stream, dxe, slot_of, dL, wrt, N, C, E, k, dx);
+  const dim3 gdx((N + kDxTokens - 1) / kDxTokens, (C + 511) / 512);
+  if (E > kMaxExperts)
+    hipLaunchKernelGGL((token_dx_kernel<ActT, kMaxExpertsWide>), gdx, dim3(64), 0, stream, dxe,
+                       slot_of, dL, wrt, N, C, E, k, dx);
+  else
+    hipLaunchKernelGGL((token_dx_kernel<ActT, kMaxExperts>), gdx, dim3(64), 0, stream, dxe,
+                       slot_of, dL, wrt, N, C, E, k, dx);
   return hipGetLastError();
 }
 
@@ -468,9 +520,10 @@ void launch_router_wgrad_products(const ActT* x, const float* dL, int N, int C, 
   else if (E <= 32)
     hipLaunchKernelGGL((router_wgrad_kernel<ActT, 32, 2, NRM>), dim3((C + 511) / 512, chunks),
                        dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b, rstd, gamma);
-  else
-    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64, 1, NRM>), dim3((C + 255) / 256, chunks),
-                       dim3(256), 0, stream, x, dL, N, C, E, partial, partial_b, rstd, gamma);
+  else   // groups of 64 experts along z (one group unless E > 64)
+    hipLaunchKernelGGL((router_wgrad_kernel<ActT, 64, 1, NRM>),
+                       dim3((C + 255) / 256, chunks, (E + 63) / 64), dim3(256), 0, stream, x, dL,
+                       N, C, E, partial, partial_b, rstd, gamma);
 }
 
 // rstd / gamma (both null, or both set): the fused block's router input,
@@ -480,7 +533,7 @@ hipError_t launch_router_wgrad(const ActT* x, const float* dL, int N, int C, int
                                float* partial, float* partial_b, float* gW, float* gb,
                                bool store, const float* rstd, const float* gamma,
                                hipStream_t stream) {
-  if (E <= 0 || E > kMaxExperts || C % 4 || (!rstd) != (!gamma)) return hipErrorInvalidValue;
+  if (E <= 0 || E > kMaxExpertsWide || C % 4 || (!rstd) != (!gamma)) return hipErrorInvalidValue;
   if (N <= 0) return hipSuccess;
   const int chunks = router_wgrad_chunks(N);
   if (rstd)

@@ -21,9 +21,10 @@ constexpr int kWave = 64;
 constexpr int kNumXcd = 8;        // MI355X: 8 accelerator complex dies, one L2 each
 // Experts the kernels that map one expert to one lane of a wave take (the
 // fused prefill and decode routers, the 256 x 256 and weight-streaming
-// GEMMs, the backward); up to kMaxExpertsWide the forward runs the split
-// router, the generic grouped GEMM and a permute that scans the experts in
-// wave-sized chunks.
+// GEMMs, the weight gradients' row chunks); up to kMaxExpertsWide the
+// layer runs the split router, the generic grouped GEMMs, a permute that
+// scans the experts in wave-sized chunks, and the backward's wide token and
+// router gradients.
 constexpr int kMaxExperts = 64;
 constexpr int kMaxExpertsWide = 256;
 constexpr int kMaxTopK = 8;

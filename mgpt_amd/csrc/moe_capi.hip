@@ -394,9 +394,7 @@ void free_weights(mgpt_moe* h) {
 // Training is built for bf16 x bf16 and fp32 x fp32 handles (fp8 weights
 // are an inference format here, and fp32 tensors over bf16 products an
 // inference option).
-bool trainable(const mgpt_moe* h) {
-  return h->wdt == h->act && h->io == h->act && !h->wide();
-}
+bool trainable(const mgpt_moe* h) { return h->wdt == h->act && h->io == h->act; }
 
 // Allocates the gradient buffer on first use, its contents logically zero.
 int ensure_grad(mgpt_moe* h) {
@@ -1157,7 +1155,7 @@ int check_grad_args(const mgpt_moe* h, float* const* grads, int num_params) {
   for (int i = 0; i < num_params; ++i)
     if (!grads[i]) return fail(MGPT_ERR_INVALID_ARGUMENT, "gradient %d is null", i);
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   return MGPT_OK;
 }
 
@@ -1229,7 +1227,7 @@ int mgpt_moe_forward_train(mgpt_moe* h, const void* x, void* y, int num_tokens, 
   if (int rc = check_forward_args(h, x, y, num_tokens, workspace, workspace_bytes, true))
     return rc;
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   if (num_tokens == 0) return MGPT_OK;
   HIP_TRY(hipSetDevice(h->device));
   hipStream_t st = (hipStream_t)stream;
@@ -1245,7 +1243,7 @@ int backward_entry(mgpt_moe* h, const void* x, const void* dy, void* dx, int num
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   if (!h->loaded) return fail(MGPT_ERR_NOT_READY, "parameters not loaded");
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   if (num_tokens < 0) return fail(MGPT_ERR_INVALID_ARGUMENT, "negative num_tokens");
   if (num_tokens == 0) return MGPT_OK;
   if (!x || !dy || !dx || !workspace)
@@ -1311,7 +1309,7 @@ int mgpt_moe_forward_block_train(mgpt_moe* h, const void* x, const float* gamma,
   if (int rc = check_forward_args(h, x, out, num_tokens, workspace, workspace_bytes, true))
     return rc;
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   if (num_tokens == 0) return MGPT_OK;
   if (!gamma) return fail(MGPT_ERR_INVALID_ARGUMENT, "null gamma");
   if (!(eps >= 0.0f)) return fail(MGPT_ERR_INVALID_ARGUMENT, "eps must be >= 0");
@@ -1334,7 +1332,7 @@ int mgpt_moe_backward_block(mgpt_moe* h, const void* x, const float* gamma, cons
 int mgpt_moe_zero_grad(mgpt_moe* h, void* stream) {
   if (!h) return fail(MGPT_ERR_INVALID_ARGUMENT, "null handle");
   if (!trainable(h))
-    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype and at most 64 experts");
+    return fail(MGPT_ERR_UNSUPPORTED, "training needs weight dtype == activation dtype");
   HIP_TRY(hipSetDevice(h->device));
   if (int rc = ensure_grad(h)) return rc;
   hipStream_t st = (hipStream_t)stream;

@@ -72,7 +72,46 @@ __device__ __forceinline__ bool wg_locate(const int32_t* __restrict__ counts, in
                                           int chunk_rows, int Iy, int Jx, int gy, int gx,
                                           WgTile* out) {
   __shared__ int s_seg[6];
-  if (threadIdx.x < kWave) {
+  if (threadIdx.x < kWave && E > kWave) {
+    // More experts than lanes (no row chunks then: chunk_rows is INT_MAX):
+    // one virtual expert per expert with rows, in expert order, found by a
+    // scan of the counts 64 experts at a time.
+    const int l = lane_id();
+    const int ngx = (Jx + gx - 1) / gx;
+    const int ng = ((Iy + gy - 1) / gy) * ngx;
+    const int b = blockIdx.x, sidx = b / kNumXcd;
+    const int j = (sidx / 16) * kNumXcd + b % kNumXcd, r = sidx % 16;
+    const int pos = j / ng, gi = j % ng;
+    int rows_carry = 0, v_carry = 0, found = -1, seg = 0, vc = 0;
+    for (int e0 = 0; e0 < E && found < 0; e0 += kWave) {
+      const int e = e0 + l;
+      const int cnt = e < E ? counts[e] : 0;
+      const int has = cnt > 0 ? 1 : 0;
+      const int rows_incl = wave_incl_scan(cnt) + rows_carry;
+      const int v_incl = wave_incl_scan(has) + v_carry;
+      const unsigned long long m = __ballot(has && v_incl - 1 == pos);
+      const int owner = m ? (__ffsll((long long)m) - 1) : 0;
+      const int sg = __shfl(rows_incl - cnt, owner, kWave);
+      const int ct = __shfl(cnt, owner, kWave);
+      if (m) {
+        found = e0 + owner;
+        seg = sg;
+        vc = ct;
+      }
+      rows_carry = __shfl(rows_incl, kWave - 1, kWave);
+      v_carry = __shfl(v_incl, kWave - 1, kWave);
+    }
+    if (l == 0) {
+      const int ty = (gi / ngx) * gy + r / gx, tx = (gi % ngx) * gx + r % gx;
+      const bool ok = found >= 0 && r < gy * gx && ty < Iy && tx < Jx;
+      s_seg[0] = seg;
+      s_seg[1] = vc;
+      s_seg[2] = ok ? ty : -1;
+      s_seg[3] = tx;
+      s_seg[4] = found;
+      s_seg[5] = -1;
+    }
+  } else if (threadIdx.x < kWave) {
     const int l = lane_id();
     const int cnt = l < E ? counts[l] : 0;
     const int incl = wave_incl_scan(cnt);
@@ -776,7 +815,8 @@ hipError_t launch_fill_zero(float* p, size_t n, hipStream_t stream) {
 // they were.
 hipError_t launch_zero_idle_experts(const int32_t* counts, int E, const IdleSlices& z,
                                     hipStream_t stream) {
-  if (E <= 0 || E > kMaxExperts || z.n < 0 || z.n > IdleSlices::kMax) return hipErrorInvalidValue;
+  if (E <= 0 || E > kMaxExpertsWide || z.n < 0 || z.n > IdleSlices::kMax)
+    return hipErrorInvalidValue;
   if (z.n == 0) return hipSuccess;
   hipLaunchKernelGGL(zero_idle_experts_kernel, dim3(256, E), dim3(256), 0, stream, counts, z);
   return hipGetLastError();
@@ -800,7 +840,7 @@ hipError_t launch_wgrad(const T* P, int ldp, int p_valid, const T* Q, int ldq, i
                         size_t part_bytes, float* bpart, size_t bpart_bytes, int num_cus,
                         bool store, hipStream_t stream) {
   constexpr int EPV = WgT<T>::EPV;
-  if (E <= 0 || E > kMaxExperts || p_valid % EPV || q_valid % EPV || ldp % EPV || ldq % EPV ||
+  if (E <= 0 || E > kMaxExpertsWide || p_valid % EPV || q_valid % EPV || ldp % EPV || ldq % EPV ||
       (reinterpret_cast<uintptr_t>(P) & 15) || (reinterpret_cast<uintptr_t>(Q) & 15) ||
       rows_total < 0 || (reinterpret_cast<uintptr_t>(part) & 15))
     return hipErrorInvalidValue;

@@ -55,9 +55,10 @@ UNIT_CASES = [
     Case("fp8_large_m", _c("fp8_large_m", 900, 256, 4, 2, 256, "bf16", "fp8", rb="normal"), 0.02),
 ]
 
-# More experts than a wave has lanes (E > 64): the forward's wide paths
-# (split router with the wide softmax, wave-chunked permute scan, generic
-# grouped GEMMs); training refuses these handles.
+# More experts than a wave has lanes (E > 64): the wide paths (split router
+# with the wide softmax, wave-chunked permute scan, generic grouped GEMMs,
+# the backward's wide token and router gradients, one weight-gradient item
+# per expert).
 WIDE_CASES = [
     Case("wide_e128_k8", _c("wide_e128_k8", 96, 128, 128, 8, 64, "bf16", rb="zipf"), 0.02),
     Case("wide_e256_f32", _c("wide_e256_f32", 80, 64, 256, 4, 48, rb="normal"), 0.05),
@@ -105,7 +106,7 @@ def build_inputs(case: Case) -> wl.MoEInputs:
 # Cases whose backward the reference is run on (tests/golden/backward/):
 # every unit case plus two benchmark shapes whose expert gradients still
 # fit a CPU run of a few seconds.
-BACKWARD_CASES = [c.name for c in UNIT_CASES] + ["cfg1", "cfg2"]
+BACKWARD_CASES = [c.name for c in UNIT_CASES] + ["wide_e128_k8", "wide_e256_f32", "cfg1", "cfg2"]
 
 
 def build_dy(case: Case) -> np.ndarray:

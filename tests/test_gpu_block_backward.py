@@ -123,14 +123,16 @@ def test_block_backward_parity(name):
 
 # (N, C, E, k, H, act): padded widths (the RMSNorm backward runs at the
 # caller's width), one not a multiple of the 16-byte piece (the scalar
-# path: 10 fp32, 100 bf16), and a large-M bf16 shape on the 256 x 256
-# GEMMs with the weight gradients on the second stream.
+# path: 10 fp32, 100 bf16), a large-M bf16 shape on the 256 x 256 GEMMs
+# with the weight gradients on the second stream, and 128 experts (the wide
+# router, token and weight gradients).
 SHAPES = [
     (40, 10, 3, 2, 24, "f32"),
     (90, 96, 5, 2, 72, "f32"),
     (77, 100, 6, 2, 64, "bf16"),
     (64, 200, 8, 2, 136, "bf16"),
     (2048, 256, 8, 2, 384, "bf16"),
+    (150, 128, 128, 4, 64, "bf16"),
 ]
 
 

@@ -11,8 +11,9 @@ reference (full arrays for the small cases, digests for the large one);
 outputs are compared with the oracle's fp32 forward at 1e-5 (fp32), 2e-2
 (bf16), 6e-2 (fp8 weights), normwise and elementwise, as in
 tests/test_gpu_parity.py.  The fused block runs the same wide router with
-normalisation.  Training such handles is refused (the backward's kernels
-map one expert to one lane).
+normalisation.  Training runs too: the small wide cases are in
+tests/test_gpu_backward.py against the reference's fixtures, a large-M one
+here against the oracle.
 """
 import numpy as np
 import pytest
@@ -103,18 +104,22 @@ def test_wide_repeats_and_graph_replay():
         assert np.array_equal(out.float().cpu().numpy(), y)
 
 
-def test_wide_training_is_refused():
-    from mgpt_amd import capi
-    from mgpt_amd.moe import MoELayer
-    case = C.ALL_CASES["wide_e256_f32"]
-    inp = C.build_inputs(case)
-    cfg = inp.cfg
-    layer = MoELayer(cfg.C, cfg.H, cfg.E, cfg.k, act=cfg.act, weights=cfg.weights)
-    layer.load_parameters(inp.params(raw=True))
-    x = torch.from_numpy(inp.x).cuda()
-    with pytest.raises(capi.MoEError) as err:
-        layer.forward(x, train=True)
-    assert err.value.status == capi.MGPT_ERR_UNSUPPORTED
+def test_wide_training_large_m():
+    """Training at E = 96 on bf16 rows with enough tokens per expert for the
+    128 x 128 grouped GEMMs: dx and the 2 + 6E gradients against the
+    oracle's backward at the bf16 bar (the small wide cases run in
+    tests/test_gpu_backward.py with the reference's fixtures)."""
+    from mgpt_amd import workload as wl
+    from test_gpu_backward import check_all, make_layer, run_backward
+    cfg = wl.MoEConfig("wide_train", 2048, 128, 96, 4, 96, "bf16", "bf16", "normal")
+    inp = wl.make_inputs(cfg, C.SEED + 91, bias_std=0.02)
+    inp.x[:] = wl.bf16_round(inp.x)
+    inp.Wr[:] = wl.bf16_round(inp.Wr)
+    dy = wl.bf16_round(np.random.default_rng(96).standard_normal((cfg.N, cfg.C))
+                       .astype(np.float32))
+    out = run_backward(make_layer(inp), inp, dy)
+    ref = O.backward(inp, dy)
+    check_all(out, ref, TOL["bf16"], "wide train")
 
 
 def test_more_than_256_experts_is_refused():
