@@ -55,8 +55,9 @@ typedef struct mgpt_moe_config {
   int embed_dim;     /* C: any width >= 1 (widths that are not a multiple of 64
                         run on zero-padded rows inside the library) */
   int hidden_dim;    /* H: > 0, or -1 for 4*C */
-  int num_experts;   /* E: 1..256 (training: 1..64; E > 64 runs the forward
-                        on its generic paths: split router, grouped GEMMs) */
+  int num_experts;   /* E: 1..256 (E > 64 runs generic paths: split router,
+                        grouped GEMMs, the backward's wide token and router
+                        gradients) */
   int top_k;         /* k: 1..min(E, 8) */
   int act_dtype;     /* x and y: MGPT_DTYPE_F32 or MGPT_DTYPE_BF16 */
   int weight_dtype;  /* F32 (act F32 only), BF16 or FP8_E4M3.  With act F32
