@@ -323,16 +323,17 @@ def _collect(layer, cfg, dx):
     return out
 
 
-@pytest.mark.parametrize("act", ["f32", "bf16"])
-def test_graph_captured_training_step(act):
+@pytest.mark.parametrize("act,E,k", [("f32", 6, 2), ("bf16", 6, 2), ("bf16", 128, 4)])
+def test_graph_captured_training_step(act, E, k):
     """forward_train + backward captured into one HIP graph.  A captured
     backward always adds.  Captured right after zero_grad, the pending zeros
     are part of the graph: every replay equals an eager zero_grad + step, bit
     for bit.  Captured with nothing pending, replays accumulate (2x after two),
     and zero_grad between replays (now a fill on the stream) restarts the
-    sum.  Eager steps between replays leave the replays unchanged."""
+    sum.  Eager steps between replays leave the replays unchanged.  E = 128
+    runs the wide router, token and weight gradients."""
     from mgpt_amd import workload as wl
-    cfg = wl.MoEConfig("cap", 300, 128, 6, 2, 192, act, act, "normal")
+    cfg = wl.MoEConfig("cap", 300, 128, E, k, 192, act, act, "normal")
     inp = wl.make_inputs(cfg, seed=11, bias_std=0.05)
     if act == "bf16":
         inp.x[:] = wl.bf16_round(inp.x)

@@ -67,6 +67,9 @@ SHAPES = [
     (200, 256, 16, 2, 384, "bf16", "bf16"),
     (300, 128, 6, 3, 192, "f32", "f32"),
     (90, 96, 5, 2, 72, "f32", "f32"),
+    # more experts than a wave has lanes (the split router and generic GEMMs)
+    (48, 512, 256, 8, 256, "bf16", "fp8"),
+    (64, 256, 128, 4, 384, "bf16", "bf16"),
 ]
 
 
