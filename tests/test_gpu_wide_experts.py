@@ -106,12 +106,13 @@ def test_wide_repeats_and_graph_replay():
 
 def test_wide_training_large_m():
     """Training at E = 96 on bf16 rows with enough tokens per expert for the
-    128 x 128 grouped GEMMs: dx and the 2 + 6E gradients against the
+    128 x 128 grouped GEMMs, the tokens spread over every expert (zero router
+    bias): dx and the 2 + 6E gradients against the
     oracle's backward at the bf16 bar (the small wide cases run in
     tests/test_gpu_backward.py with the reference's fixtures)."""
     from mgpt_amd import workload as wl
     from test_gpu_backward import check_all, make_layer, run_backward
-    cfg = wl.MoEConfig("wide_train", 2048, 128, 96, 4, 96, "bf16", "bf16", "normal")
+    cfg = wl.MoEConfig("wide_train", 2048, 128, 96, 4, 96, "bf16", "bf16", "zero")
     inp = wl.make_inputs(cfg, C.SEED + 91, bias_std=0.02)
     inp.x[:] = wl.bf16_round(inp.x)
     inp.Wr[:] = wl.bf16_round(inp.Wr)
@@ -120,6 +121,48 @@ def test_wide_training_large_m():
     out = run_backward(make_layer(inp), inp, dy)
     ref = O.backward(inp, dy)
     check_all(out, ref, TOL["bf16"], "wide train")
+
+
+# (N, C, E, k, H, act, router bias): one decode token over 65 experts, an odd
+# expert count over a width that is not a multiple of 64 (fp32), top-1 of 256,
+# and a bf16 shape with 97 experts on the small-row tiles.  With a zero router
+# bias the tokens spread over (nearly) every expert, so more than 64 experts
+# hold rows (the weight gradients' and the permute's scans past one wave).
+EDGE = [
+    (1, 64, 65, 8, 64, "bf16", "normal"),
+    (33, 100, 255, 8, 40, "f32", "zero"),
+    (64, 128, 256, 1, 64, "f32", "zero"),
+    (700, 192, 97, 3, 96, "bf16", "zero"),
+]
+
+
+@pytest.mark.parametrize("N,Cm,E,k,H,act,rb", EDGE)
+def test_wide_edge_shapes_forward_and_backward(N, Cm, E, k, H, act, rb):
+    """Routing bit-exact with the oracle's forward (counts, ids, weights,
+    permutation), y at the forward's bar, dx and every gradient at the
+    backward's."""
+    from mgpt_amd import workload as wl
+    from test_gpu_backward import check_all, make_layer, run_backward
+    cfg = wl.MoEConfig(f"wide_edge_{E}", N, Cm, E, k, H, act, act, rb)
+    inp = wl.make_inputs(cfg, C.SEED + E + N, bias_std=0.02)
+    dy = np.random.default_rng(E).standard_normal((N, Cm)).astype(np.float32)
+    if act == "bf16":
+        inp.x[:] = wl.bf16_round(inp.x)
+        inp.Wr[:] = wl.bf16_round(inp.Wr)
+        dy = wl.bf16_round(dy)
+    print(f"case {cfg}", flush=True)
+    ref = O.forward(inp)
+    _, y, _, _, _ = run_gpu(inp)
+    check_close(y, ref["y"], TOL[act], cfg.name)
+    layer = make_layer(inp)
+    out = run_backward(layer, inp, dy)
+    r = {n: v.cpu().numpy() for n, v in layer.routing().items()}
+    assert np.array_equal(r["counts"], ref["counts"])
+    assert np.array_equal(r["topk_idx"], ref["idx"])
+    assert np.array_equal(r["topk_p"].view(np.uint32), ref["topp"].view(np.uint32))
+    assert np.array_equal(r["perm"], ref["perm"])
+    print(f"{cfg.name}: {int((ref['counts'] > 0).sum())} experts with rows", flush=True)
+    check_all(out, O.backward(inp, dy), TOL[act], cfg.name)
 
 
 def test_more_than_256_experts_is_refused():
