@@ -72,7 +72,7 @@ def stage_of(kernel_name: str):
     short = kernel_name.replace("(anonymous namespace)", "").split("(")[0]
     if "scatter_bwd_kernel" in short:
         return "scatter_bwd"
-    if re.search(r"token_d[lx]_kernel", short):
+    if re.search(r"token_d[lx](?:_wide)?_kernel", short):
         return "token_bwd"
     if "router_wgrad" in short:
         return "router_wgrad"

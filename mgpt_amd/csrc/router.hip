@@ -660,6 +660,38 @@ __global__ __launch_bounds__(kSplitExperts * 64) void router_logits_kernel(
   if (e < E && tok0 + lane < N) logits[(size_t)(tok0 + lane) * E + e] = acc[0] + br[e];
 }
 
+// Logits of 64 experts per block for more experts than one router block
+// takes: 16 waves x 4 experts, the fused router's chains over the same
+// packed weights ([G][C][4]), blockIdx.y the group of 64 experts.  The
+// activation rows are read once per group instead of once per 4 experts
+// (router_logits_kernel) or per expert (router_logits_pc_kernel); the
+// chains and their rounding are the fused router's, so the logits are the
+// same bits.  router_softmax_wide_kernel follows.
+template <typename ActT, bool NORM>
+__global__ __launch_bounds__(1024) void router_logits_wide_kernel(
+    const ActT* __restrict__ x, const float* __restrict__ wr_g, const float* __restrict__ br,
+    int N, int C, int E, float* __restrict__ logits, RowNorm nrm, float* __restrict__ rstd) {
+  constexpr int RE = 4;
+  __shared__ __attribute__((aligned(1024))) char smem[kRouterLds + (NORM ? kRouterNormLds : 0)];
+  const int lane = lane_id();
+  const int g = __builtin_amdgcn_readfirstlane((int)threadIdx.x / kWave);
+  const int nw = blockDim.x / kWave;
+  const int gb = blockIdx.y * nw;   // first weight group of this block
+  const int tok0 = blockIdx.x * kRT;
+  float acc[RE];
+  float r = 1.0f;
+  logit_chains<ActT, RE, NORM>(x + (size_t)tok0 * C, N - tok0, wr_g + (size_t)gb * C * RE,
+                               min(nw, (E + RE - 1) / RE - gb), nw, g, C, smem, acc, nrm, &r);
+  if (NORM && blockIdx.y == 0 && g == 0 && tok0 + lane < N) rstd[tok0 + lane] = r;
+  if (tok0 + lane < N) {
+#pragma unroll
+    for (int j = 0; j < RE; ++j) {
+      const int e = (gb + g) * RE + j;
+      if (e < E) logits[(size_t)(tok0 + lane) * E + e] = acc[j] + br[e];
+    }
+  }
+}
+
 __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __restrict__ logits,
                                                              int N, int E, int k,
                                                              int32_t* __restrict__ topk_idx,
@@ -1202,7 +1234,16 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
     // wide: per-expert logits (the split kernels, any E), then the block
     // softmax / top-k over rows of up to kMaxExpertsWide
     if (E > kMaxExpertsWide || !logits || wr4) return hipErrorInvalidValue;
-    if (gamma)
+    const int eg = (E + kMaxExperts - 1) / kMaxExperts;
+    if (nb * eg >= 256 && router_experts_per_wave(E) == 4) {
+      // enough (token block, 64 experts) blocks to fill the chip
+      if (gamma)
+        hipLaunchKernelGGL((router_logits_wide_kernel<ActT, true>), dim3(nb, eg), dim3(1024), 0,
+                           stream, x, wr_g, br, N, C, E, logits, nrm, rstd);
+      else
+        hipLaunchKernelGGL((router_logits_wide_kernel<ActT, false>), dim3(nb, eg), dim3(1024), 0,
+                           stream, x, wr_g, br, N, C, E, logits, nrm, rstd);
+    } else if (gamma)
       hipLaunchKernelGGL((router_logits_kernel<ActT, true>),
                          dim3(nb, (E + kSplitExperts - 1) / kSplitExperts),
                          dim3(kSplitExperts * kWave), 0, stream, x, wr1, br, N, C, E, logits, nrm,

@@ -260,6 +260,10 @@ CONFIGS = {
     "cfg3": MoEConfig("cfg3", 16384, 1024, 16, 2, 2816, "bf16", "bf16", "normal", 64, 256),
     "cfg4": MoEConfig("cfg4", 32768, 2048, 64, 6, 1408, "bf16", "bf16", "zipf", 64, 512),
     "cfg5": MoEConfig("cfg5", 64, 2048, 64, 8, 1408, "bf16", "fp8", "zero", 1, 64),
+    # Beyond the benchmark: cfg3's tokens and width over 128 fine-grained
+    # experts, top-8 of H = 704 (the same expert FLOPs per token as cfg3),
+    # with a zero router bias so the tokens spread over every expert.
+    "wide128": MoEConfig("wide128", 16384, 1024, 128, 8, 704, "bf16", "bf16", "zero", 64, 256),
 }
 
 ZIPF_S = 1.1

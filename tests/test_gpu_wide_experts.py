@@ -52,12 +52,14 @@ def test_wide_forward_parity(name):
         check_close(y[fx["rows"]], fx["y_rows"], TOL[case.cfg.weights], name + " reference rows")
 
 
-def test_wide_fused_block():
-    """out = x + MoE(RMSNorm(x) * gamma) with E = 128: the wide router
-    normalises the rows (1/rms bit-exact), routing bit-exact with the
+@pytest.mark.parametrize("N,E,rb", [(150, 128, "normal"), (4096, 256, "zero")])
+def test_wide_fused_block(N, E, rb):
+    """out = x + MoE(RMSNorm(x) * gamma) with E = 128 and 256: the wide
+    router normalises the rows (1/rms bit-exact; at 4096 tokens x 256
+    experts in the 64-expert-group logits kernel), routing bit-exact with the
     oracle's block, out at the bf16 bar."""
     from mgpt_amd import workload as wl
-    cfg = wl.MoEConfig("wide_blk", 150, 128, 128, 4, 64, "bf16", "bf16", "normal")
+    cfg = wl.MoEConfig("wide_blk", N, 128, E, 4, 64, "bf16", "bf16", rb)
     inp = wl.make_inputs(cfg, C.SEED + 77, bias_std=0.02)
     N = cfg.N
     t = np.arange(N)
@@ -125,7 +127,8 @@ def test_wide_training_large_m():
 
 # (N, C, E, k, H, act, router bias): one decode token over 65 experts, an odd
 # expert count over a width that is not a multiple of 64 (fp32), top-1 of 256,
-# and a bf16 shape with 97 experts on the small-row tiles.  With a zero router
+# a bf16 shape with 97 experts on the small-row tiles, and 4096 tokens over
+# 256 experts (the router's logits in 64-expert groups).  With a zero router
 # bias the tokens spread over (nearly) every expert, so more than 64 experts
 # hold rows (the weight gradients' and the permute's scans past one wave).
 EDGE = [
@@ -133,6 +136,8 @@ EDGE = [
     (33, 100, 255, 8, 40, "f32", "zero"),
     (64, 128, 256, 1, 64, "f32", "zero"),
     (700, 192, 97, 3, 96, "bf16", "zero"),
+    # enough (64 tokens, 64 experts) blocks for the grouped logits kernel
+    (4096, 128, 256, 8, 64, "bf16", "zero"),
 ]
 
 
