@@ -107,18 +107,25 @@ struct Tile {
 constexpr int kGroupM = 4;   // m-tiles per group of the tile order
 
 // Per-expert segment bookkeeping, computed once per wave from counts[] (lane
-// e holds expert e; E <= 64), so that locating a tile needs no memory access
-// and no barrier.
+// e holds expert e_base + e of the launch's group of E <= 64 experts; more
+// experts run one launch per group, whose rows start after the earlier
+// groups' rows), so that locating a tile needs no memory access and no
+// barrier.
 struct SegScan {
   // (the exclusive counts are recomputed where needed: the kernel runs at
   // the register limit, and these live in every lane throughout)
   int cnt, rows_incl, tiles_incl, tm;
   __device__ __forceinline__ int tiles_excl() const { return tiles_incl - (cnt + kBM - 1) / kBM; }
-  __device__ __forceinline__ void init(const int32_t* __restrict__ counts, int E) {
+  __device__ __forceinline__ void init(const int32_t* __restrict__ counts, int E, int e_base) {
     const int l = lane_id();
-    cnt = (l < E) ? counts[l] : 0;
+    cnt = (l < E) ? counts[e_base + l] : 0;
     const int tiles = (cnt + kBM - 1) / kBM;
-    rows_incl = wave_incl_scan(cnt);
+    int before = 0;   // rows of the experts before the group
+    if (e_base > 0) {
+      for (int e = l; e < e_base; e += kWave) before += counts[e];
+      before = __builtin_amdgcn_readfirstlane(__shfl(wave_incl_scan(before), kWave - 1, kWave));
+    }
+    rows_incl = wave_incl_scan(cnt) + before;
     tiles_incl = wave_incl_scan(tiles);
     tm = __builtin_amdgcn_readfirstlane(__shfl(tiles_incl, kWave - 1, kWave));   // all m-tiles
   }
@@ -464,9 +471,9 @@ constexpr int kPartialFloats = 256 * 256;
 template <int EPI, int NW, bool kSave>
 __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
     const bf16_t* __restrict__ A, const bf16_t* __restrict__ B, const float* __restrict__ bias0,
-    const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
-    int n_store, int bias_ld, bf16_t* out, int ldo, float* __restrict__ partials, bf16_t* save,
-    int save_ld) {
+    const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int e_base, int K,
+    int Npad, int n_store, int bias_ld, bf16_t* out, int ldo, float* __restrict__ partials,
+    bf16_t* save, int save_ld) {
   using W = Waves<NW>;
   constexpr int kTN = W::TN, kTM = W::TM;
   constexpr int kUnits = 5;
@@ -482,7 +489,7 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
                              : blockIdx.x;
   const int KT = K / 64;
   SegScan sc;
-  sc.init(counts, E);
+  sc.init(counts, E, e_base);
   SplitPlan plan;
   plan.init(sc.tm * nbx, G, KT, partials != nullptr);
   Work cur;
@@ -696,8 +703,8 @@ __global__ __launch_bounds__(NW * 64) void gemm_ring5_kernel(
 template <int EPI, int NW>
 __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
     const float* __restrict__ partials, const float* __restrict__ bias0,
-    const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int K, int Npad,
-    int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, int G) {
+    const float* __restrict__ bias1, const int32_t* __restrict__ counts, int E, int e_base, int K,
+    int Npad, int n_store, int bias_ld, bf16_t* __restrict__ out, int ldo, int G) {
   using W = Waves<NW>;
   constexpr int kTM = W::TM, kT = W::kThreads;
   constexpr bool kGU = EPI == kEpiGateUp;
@@ -706,7 +713,7 @@ __global__ __launch_bounds__(256) void gemm_split_reduce_kernel(
   const int nbx = Npad / kBN;
   const int KT = K / 64;
   SegScan sc;
-  sc.init(counts, E);
+  sc.init(counts, E, e_base);
   SplitPlan plan;
   plan.init(sc.tm * nbx, G, KT, true);
   if (plan.s == 1) return;
@@ -792,6 +799,7 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
                            float* partials, int num_cus, bf16_t* save, int save_ld,
                            hipStream_t stream) {
   if (max_mtiles <= 0) return hipSuccess;
+  if (E <= 0 || E > kMaxExpertsWide) return hipErrorInvalidValue;
   // 16-byte output vectors: ldo and the output base must keep 8-element alignment
   if (K % 64 != 0 || Npad % kBN != 0 || n_store % 64 != 0 || num_cus <= 0 || ldo % 8 != 0 ||
       (reinterpret_cast<uintptr_t>(out) & 15) != 0)
@@ -807,26 +815,35 @@ hipError_t launch_gemm_dma(const bf16_t* A, const bf16_t* B, const float* bias0,
   if (K / 64 < kMinSplitSlabs) partials = nullptr;   // no split, no reduce launch
   const int tiles = max_mtiles * (Npad / kBN);
   const int grid = tiles < num_cus ? tiles : num_cus;
-  // the gate/up epilogue's pre-activation stores are compiled only into
-  // the training instance (fewer live registers in the inference one)
-  auto launch = [&](auto save_c) {
-    hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves, decltype(save_c)::value>), dim3(grid),
-                       dim3(kRingWaves * kWave), 0, stream, A, B, bias0, bias1, counts, E, K, Npad,
-                       n_store, bias_ld, out, ldo, partials, save, save_ld);
-  };
-  if constexpr (EPI == kEpiGateUp) {
-    if (save)
-      launch(std::true_type{});
-    else
+  // More than 64 experts: one launch (and split reduce) per group of 64, the
+  // weights and biases from the group's first expert on; the rows come in
+  // expert order, so each group's follow the earlier groups'.
+  for (int e0 = 0; e0 < E; e0 += kMaxExperts) {
+    const int Eg = std::min(kMaxExperts, E - e0);
+    const bf16_t* Bg = B + (size_t)e0 * Npad * K;
+    const float* b0 = bias0 ? bias0 + (size_t)e0 * bias_ld : nullptr;
+    const float* b1 = bias1 ? bias1 + (size_t)e0 * bias_ld : nullptr;
+    // the gate/up epilogue's pre-activation stores are compiled only into
+    // the training instance (fewer live registers in the inference one)
+    auto launch = [&](auto save_c) {
+      hipLaunchKernelGGL((gemm_ring5_kernel<EPI, kRingWaves, decltype(save_c)::value>),
+                         dim3(grid), dim3(kRingWaves * kWave), 0, stream, A, Bg, b0, b1, counts,
+                         Eg, e0, K, Npad, n_store, bias_ld, out, ldo, partials, save, save_ld);
+    };
+    if constexpr (EPI == kEpiGateUp) {
+      if (save)
+        launch(std::true_type{});
+      else
+        launch(std::false_type{});
+    } else {
       launch(std::false_type{});
-  } else {
-    launch(std::false_type{});
-  }
-  if constexpr (EPI != kEpiSwigluBwd) {
-    if (partials)
-      hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256), 0,
-                         stream, partials, bias0, bias1, counts, E, K, Npad, n_store, bias_ld, out,
-                         ldo, grid);
+    }
+    if constexpr (EPI != kEpiSwigluBwd) {
+      if (partials)
+        hipLaunchKernelGGL((gemm_split_reduce_kernel<EPI, kRingWaves>), dim3(8 * grid), dim3(256),
+                           0, stream, partials, b0, b1, counts, Eg, e0, K, Npad, n_store, bias_ld,
+                           out, ldo, grid);
+    }
   }
   return hipGetLastError();
 }

@@ -294,7 +294,7 @@ struct mgpt_moe {
     return (size_t)64 * ((std::max(2 * Hp, C) + 255) / 256) * 256 * 4;
   }
   bool uses_gemm_dma(int N) const {
-    return act == MGPT_DTYPE_BF16 && wdt == MGPT_DTYPE_BF16 && gemm_tile == 256 && !wide() &&
+    return act == MGPT_DTYPE_BF16 && wdt == MGPT_DTYPE_BF16 && gemm_tile == 256 &&
            (size_t)N * k >= (size_t)64 * E;
   }
   size_t w_bytes() const { return wdt == MGPT_DTYPE_FP8_E4M3 ? 1 : (wdt == MGPT_DTYPE_BF16 ? 2 : 4); }
@@ -863,7 +863,7 @@ int forward_impl(mgpt_moe* h, const IoT* x, IoT* y, int N, char* ws, bool train,
             hb, (const bf16_t*)h->wd, nullptr, h->bd, nullptr, counts, E, Hp, Cp, C, Cp, ob, C,
             mt, nullptr, 0, st)));
       }
-    } else if (h->gemm_tile == 256 && !fp8 && !h->wide()) {
+    } else if (h->gemm_tile == 256 && !fp8) {
       // bf16 weights, prefill-shaped segments: 256x256 direct-to-LDS kernel.
       const int mt = (int)((A + 255) / 256) + E;
       float* part = (float*)(ws + L.partials);
