@@ -20,11 +20,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kWave = 64;
 constexpr int kNumXcd = 8;        // MI355X: 8 accelerator complex dies, one L2 each
 // Experts the kernels that map one expert to one lane of a wave take (the
-// fused prefill and decode routers, the 256 x 256 and weight-streaming
-// GEMMs, the weight gradients' row chunks); up to kMaxExpertsWide the
-// layer runs the split router, the generic grouped GEMMs, a permute that
-// scans the experts in wave-sized chunks, and the backward's wide token and
-// router gradients.
+// fused prefill and decode routers, the weight-streaming GEMM, the weight
+// gradients' row chunks); up to kMaxExpertsWide the layer runs the router's
+// logits in groups of 64 experts and a wide softmax, the 256 x 256 GEMMs
+// once per group of 64, the generic grouped GEMMs, a permute that scans the
+// experts in wave-sized chunks, and the backward's wide token and router
+// gradients.
 constexpr int kMaxExperts = 64;
 constexpr int kMaxExpertsWide = 256;
 constexpr int kMaxTopK = 8;
