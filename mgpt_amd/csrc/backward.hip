@@ -123,13 +123,13 @@ __global__ __launch_bounds__(256) void token_dl_kernel(const int32_t* __restrict
 // token_dl_kernel for more experts than a wave has lanes: one wave per
 // token, lane l holding experts l, l + 64, ... (their terms added in that
 // order, then the same shuffle tree over the lanes).
+template <int kPerLane>   // experts per lane: ceil(E / 64)
 __global__ __launch_bounds__(256) void token_dl_wide_kernel(const int32_t* __restrict__ topk_idx,
                                                             const float* __restrict__ dtp,
                                                             const float* __restrict__ probs,
                                                             const int32_t* __restrict__ counts,
                                                             int N, int E, int k,
                                                             float* __restrict__ dL) {
-  constexpr int kPerLane = kMaxExpertsWide / kWave;
   const int gid = blockIdx.x * 4 + (int)threadIdx.x / kWave;
   if (gid >= N) return;   // wave-uniform
   const int l = lane_id();
@@ -483,9 +483,12 @@ hipError_t launch_token_bwd(const ActT* dxe, const int32_t* slot_of, const int32
                             hipStream_t stream) {
   if (N <= 0) return hipSuccess;
   if (E > kMaxExpertsWide || k > kMaxTopK || C % 8) return hipErrorInvalidValue;
-  if (E > kMaxExperts)
-    hipLaunchKernelGGL(token_dl_wide_kernel, dim3((N + 3) / 4), dim3(256), 0, stream, topk_idx,
-                       dtp, probs, counts, N, E, k, dL);
+  if (E > 256)
+    hipLaunchKernelGGL((token_dl_wide_kernel<kMaxExpertsWide / kWave>), dim3((N + 3) / 4),
+                       dim3(256), 0, stream, topk_idx, dtp, probs, counts, N, E, k, dL);
+  else if (E > kMaxExperts)
+    hipLaunchKernelGGL((token_dl_wide_kernel<4>), dim3((N + 3) / 4), dim3(256), 0, stream,
+                       topk_idx, dtp, probs, counts, N, E, k, dL);
   else if (E <= 16)
     hipLaunchKernelGGL(token_dl_kernel<16>, dim3((N + 15) / 16), dim3(256), 0, stream, topk_idx,
                        dtp, probs, counts, N, E, k, dL);
@@ -496,8 +499,11 @@ hipError_t launch_token_bwd(const ActT* dxe, const int32_t* slot_of, const int32
     hipLaunchKernelGGL(token_dl_kernel<64>, dim3((N + 3) / 4), dim3(256), 0, stream, topk_idx,
                        dtp, probs, counts, N, E, k, dL);
   const dim3 gdx((N + kDxTokens - 1) / kDxTokens, (C + 511) / 512);
-  if (E > kMaxExperts)
+  if (E > 256)
     hipLaunchKernelGGL((token_dx_kernel<ActT, kMaxExpertsWide>), gdx, dim3(64), 0, stream, dxe,
+                       slot_of, dL, wrt, N, C, E, k, dx);
+  else if (E > kMaxExperts)
+    hipLaunchKernelGGL((token_dx_kernel<ActT, 256>), gdx, dim3(64), 0, stream, dxe,
                        slot_of, dL, wrt, N, C, E, k, dx);
   else
     hipLaunchKernelGGL((token_dx_kernel<ActT, kMaxExperts>), gdx, dim3(64), 0, stream, dxe,

@@ -27,7 +27,7 @@ constexpr int kNumXcd = 8;        // MI355X: 8 accelerator complex dies, one L2 
 // experts in wave-sized chunks, and the backward's wide token and router
 // gradients.
 constexpr int kMaxExperts = 64;
-constexpr int kMaxExpertsWide = 256;
+constexpr int kMaxExpertsWide = 512;
 constexpr int kMaxTopK = 8;
 // Tokens per router / permute block: block b owns tokens [b*64, (b+1)*64)
 // and so the flat assignment ids [b*64*k, (b+1)*64*k).

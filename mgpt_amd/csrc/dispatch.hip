@@ -188,16 +188,16 @@ __global__ __launch_bounds__(256) void permute_kernel(
   for (int f = tid; f < kRouterTokens * kMaxTopK; f += 256) s_slot[f] = -1;
   if (base) {
     // scanned by expert_scan_kernel
-    if (tid < E) {
-      s_pre[tid] = base[(size_t)tid * nb + b];
-      s_tot[tid] = counts[tid];
+    for (int e = tid; e < E; e += 256) {
+      s_pre[e] = base[(size_t)e * nb + b];
+      s_tot[e] = counts[e];
     }
   } else if (!hist) {
     // a single router block routed without a histogram (nb == 1): count its
     // ids (LDS integer atomics; counts do not depend on their order)
-    if (tid < E) {
-      s_pre[tid] = 0;
-      s_tot[tid] = 0;
+    for (int e = tid; e < E; e += 256) {
+      s_pre[e] = 0;
+      s_tot[e] = 0;
     }
     __syncthreads();
     for (int f = tid; f < nflat; f += 256) {
@@ -207,39 +207,43 @@ __global__ __launch_bounds__(256) void permute_kernel(
   } else {
     // Per expert: the assignments of the router blocks before this one and
     // of all blocks.  G consecutive lanes of one wave share an expert (G =
-    // 256 / E rounded to a power of two, at most 64), each summing every
-    // G-th block, then reduce across the group.
+    // 256 / E rounded to a power of two, at most 64; 1 past 256 experts),
+    // each summing every G-th block, then reduce across the group; 256 / G
+    // experts per pass (one pass unless E > 256).
     int ep = 1;
     while (ep < E) ep <<= 1;
-    const int G = min(kWave, 256 / ep);
-    const int e = tid / G, part = tid % G;
-    // 16 loads per lane in flight before the first add (one L2 round trip
-    // per 16 entries instead of one per entry)
-    constexpr int kHU = 16;
-    int pre = 0, tot = 0;
-    if (e < E) {
-      const int32_t* hrow = hist + (size_t)e * nb;
-      for (int bb0 = part; bb0 < nb; bb0 += kHU * G) {
-        int v[kHU];
+    const int G = max(1, min(kWave, 256 / ep));
+    const int part = tid % G;
+    for (int e0 = 0; e0 < E; e0 += 256 / G) {
+      const int e = e0 + tid / G;
+      // 16 loads per lane in flight before the first add (one L2 round trip
+      // per 16 entries instead of one per entry)
+      constexpr int kHU = 16;
+      int pre = 0, tot = 0;
+      if (e < E) {
+        const int32_t* hrow = hist + (size_t)e * nb;
+        for (int bb0 = part; bb0 < nb; bb0 += kHU * G) {
+          int v[kHU];
 #pragma unroll
-        for (int u = 0; u < kHU; ++u) {
-          const int bb = bb0 + u * G;
-          v[u] = bb < nb ? hrow[bb] : 0;
-        }
+          for (int u = 0; u < kHU; ++u) {
+            const int bb = bb0 + u * G;
+            v[u] = bb < nb ? hrow[bb] : 0;
+          }
 #pragma unroll
-        for (int u = 0; u < kHU; ++u) {
-          tot += v[u];
-          if (bb0 + u * G < b) pre += v[u];
+          for (int u = 0; u < kHU; ++u) {
+            tot += v[u];
+            if (bb0 + u * G < b) pre += v[u];
+          }
         }
       }
-    }
-    for (int d = G / 2; d >= 1; d >>= 1) {
-      pre += __shfl_xor(pre, d, kWave);
-      tot += __shfl_xor(tot, d, kWave);
-    }
-    if (e < E && part == 0) {
-      s_pre[e] = pre;
-      s_tot[e] = tot;
+      for (int d = G / 2; d >= 1; d >>= 1) {
+        pre += __shfl_xor(pre, d, kWave);
+        tot += __shfl_xor(tot, d, kWave);
+      }
+      if (e < E && part == 0) {
+        s_pre[e] = pre;
+        s_tot[e] = tot;
+      }
     }
   }
   __syncthreads();
@@ -264,7 +268,7 @@ __global__ __launch_bounds__(256) void permute_kernel(
   if (tid < kWave) {
     const int l = tid;
     const unsigned long long lt = (l == 0) ? 0ull : (~0ull >> (kWave - l));
-    const int id_bits = E > kMaxExperts ? 8 : 6;
+    const int id_bits = E > 256 ? 9 : (E > kMaxExperts ? 8 : 6);
 #pragma unroll
     for (int u = 0; u < kIdPerLane; ++u) {
       const int f0 = u * kWave;
@@ -277,7 +281,7 @@ __global__ __launch_bounds__(256) void permute_kernel(
       if (!valid) e = 0;
       unsigned long long match = __ballot(valid);
 #pragma unroll
-      for (int bit = 0; bit < 8; ++bit) {
+      for (int bit = 0; bit < 9; ++bit) {
         if (bit >= id_bits) break;   // ids < 2^id_bits
         const unsigned long long on = __ballot(valid && ((e >> bit) & 1));
         match &= ((e >> bit) & 1) ? on : ~on;

@@ -713,25 +713,27 @@ __global__ __launch_bounds__(1024) void router_softmax_kernel(const float* __res
   softmax_topk_block(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks, probs);
 }
 
-// router_softmax_kernel for more experts than a wave has lanes (up to
-// kMaxExpertsWide): the same per-token passes over a wider row in LDS.
+// router_softmax_kernel for more experts than a wave has lanes (up to EW <=
+// kMaxExpertsWide): the same per-token passes over a wider row in LDS (EW =
+// 256 keeps the block's LDS at 66 KB, two blocks per CU; 512 takes 134 KB).
+template <int EW>
 __global__ __launch_bounds__(1024) void router_softmax_wide_kernel(
     const float* __restrict__ logits, int N, int E, int k, int32_t* __restrict__ topk_idx,
     float* __restrict__ topk_p, int32_t* __restrict__ hist, int num_blocks,
     float* __restrict__ probs) {
-  __shared__ float s_l[kRT][kMaxExpertsWide + 1];
+  __shared__ float s_l[kRT][EW + 1];
   __shared__ float s_m[kRT];
-  __shared__ int s_hist[kMaxExpertsWide];
+  __shared__ int s_hist[EW];
   const int tid = threadIdx.x;
   const int tok0 = blockIdx.x * kRT;
-  if (tid < kMaxExpertsWide) s_hist[tid] = 0;
+  if (tid < EW) s_hist[tid] = 0;
   for (int p = tid; p < kRT * E; p += blockDim.x) {
     const int r = p / E, e = p % E;
     s_l[r][e] = tok0 + r < N ? logits[(size_t)(tok0 + r) * E + e] : 0.0f;
   }
   __syncthreads();
-  softmax_topk_block<kMaxExpertsWide + 1>(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p,
-                                          hist, num_blocks, probs);
+  softmax_topk_block<EW + 1>(s_l, s_m, s_hist, tok0, N, E, k, topk_idx, topk_p, hist, num_blocks,
+                             probs);
 }
 
 // Logits for decode shapes with the products and the chains on different
@@ -1251,8 +1253,12 @@ hipError_t launch_router(const ActT* x, const float* wr_g, const float* wr1, con
     else
       hipLaunchKernelGGL((router_logits_pc_kernel<ActT>), dim3(nb, E), dim3(256), 0, stream, x,
                          wr1, br, N, C, E, logits, hist, nb);
-    hipLaunchKernelGGL(router_softmax_wide_kernel, dim3(nb), dim3(1024), 0, stream, logits, N, E,
-                       k, topk_idx, topk_p, hist, nb, probs);
+    if (E <= 256)
+      hipLaunchKernelGGL(router_softmax_wide_kernel<256>, dim3(nb), dim3(1024), 0, stream, logits,
+                         N, E, k, topk_idx, topk_p, hist, nb, probs);
+    else
+      hipLaunchKernelGGL(router_softmax_wide_kernel<kMaxExpertsWide>, dim3(nb), dim3(1024), 0,
+                         stream, logits, N, E, k, topk_idx, topk_p, hist, nb, probs);
     return hipGetLastError();
   }
   if (wr4) {

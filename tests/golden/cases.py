@@ -66,6 +66,7 @@ WIDE_CASES = [
          full_arrays=False),
     Case("wide_e200_fp8", _c("wide_e200_fp8", 40, 128, 200, 8, 128, "bf16", "fp8", rb="normal"),
          0.02),
+    Case("wide_e384_k8", _c("wide_e384_k8", 128, 64, 384, 8, 32, "bf16", rb="zero"), 0.02),
 ]
 
 CONFIG_CASES = [
@@ -106,7 +107,8 @@ def build_inputs(case: Case) -> wl.MoEInputs:
 # Cases whose backward the reference is run on (tests/golden/backward/):
 # every unit case plus two benchmark shapes whose expert gradients still
 # fit a CPU run of a few seconds.
-BACKWARD_CASES = [c.name for c in UNIT_CASES] + ["wide_e128_k8", "wide_e256_f32", "cfg1", "cfg2"]
+BACKWARD_CASES = [c.name for c in UNIT_CASES] + ["wide_e128_k8", "wide_e256_f32", "wide_e384_k8",
+                                                  "cfg1", "cfg2"]
 
 
 def build_dy(case: Case) -> np.ndarray:

@@ -47,7 +47,7 @@ def _create(C, H, E, k, act=capi.DTYPE_F32, w=capi.DTYPE_F32):
 
 @pytest.mark.parametrize("shape,expect", [
     ((64, 64, 4, 5), capi.MGPT_ERR_INVALID_ARGUMENT),    # k > E
-    ((64, 64, 257, 2), capi.MGPT_ERR_UNSUPPORTED),       # E > 256
+    ((64, 64, 513, 2), capi.MGPT_ERR_UNSUPPORTED),       # E > 512
     ((64, 64, 16, 9), capi.MGPT_ERR_UNSUPPORTED),        # k > 8
     ((0, 64, 4, 2), capi.MGPT_ERR_INVALID_ARGUMENT),
     ((64, -2, 4, 2), capi.MGPT_ERR_INVALID_ARGUMENT),

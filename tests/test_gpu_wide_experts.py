@@ -138,6 +138,10 @@ EDGE = [
     (700, 192, 97, 3, 96, "bf16", "zero"),
     # enough (64 tokens, 64 experts) blocks for the grouped logits kernel
     (4096, 128, 256, 8, 64, "bf16", "zero"),
+    # past 256 experts (nine id bits, the 512-wide softmax row and token
+    # gradients), prefill-sized with the grouped kernels and decode-sized
+    (8192, 64, 384, 8, 64, "bf16", "zero"),
+    (64, 128, 512, 4, 64, "f32", "zero"),
 ]
 
 
@@ -170,9 +174,9 @@ def test_wide_edge_shapes_forward_and_backward(N, Cm, E, k, H, act, rb):
     check_all(out, O.backward(inp, dy), TOL[act], cfg.name)
 
 
-def test_more_than_256_experts_is_refused():
+def test_more_than_512_experts_is_refused():
     from mgpt_amd import capi
     from mgpt_amd.moe import MoELayer
     with pytest.raises(capi.MoEError) as err:
-        MoELayer(64, 64, 257, 2, act="f32")
+        MoELayer(64, 64, 513, 2, act="f32")
     assert err.value.status == capi.MGPT_ERR_UNSUPPORTED
