@@ -34,7 +34,7 @@ extern "C" {
 typedef enum mgpt_status {
   MGPT_OK = 0,
   MGPT_ERR_INVALID_ARGUMENT = 1,   /* null pointer, bad size, bad shape */
-  MGPT_ERR_UNSUPPORTED = 2,        /* valid but not built for (e.g. E > 256) */
+  MGPT_ERR_UNSUPPORTED = 2,        /* valid but not built for (e.g. E > 512) */
   MGPT_ERR_WORKSPACE_TOO_SMALL = 3,
   MGPT_ERR_NOT_READY = 4,          /* forward before parameters were loaded */
   MGPT_ERR_HIP = 5,                /* a HIP runtime call failed */
@@ -55,7 +55,7 @@ typedef struct mgpt_moe_config {
   int embed_dim;     /* C: any width >= 1 (widths that are not a multiple of 64
                         run on zero-padded rows inside the library) */
   int hidden_dim;    /* H: > 0, or -1 for 4*C */
-  int num_experts;   /* E: 1..256 (E > 64 runs generic paths: split router,
+  int num_experts;   /* E: 1..512 (E > 64 runs generic paths: split router,
                         grouped GEMMs, the backward's wide token and router
                         gradients) */
   int top_k;         /* k: 1..min(E, 8) */
