@@ -14,7 +14,7 @@
 // its own; large ones scan first (expert_scan_kernel).
 // The within-block rank comes from wave ballots over 64 consecutive ids at
 // a time (one ballot per bit of the expert ids: 6 for E <= 64, 8 for
-// E <= 256).
+// E <= 256, 9 for E <= 512).
 // The permute kernel then copies each token's row once from HBM into all k
 // of its slots with 16-byte loads and stores.
 #include "common.hpp"

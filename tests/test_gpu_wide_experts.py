@@ -1,11 +1,13 @@
 """GPU parity of the forward with more experts than a wave has lanes
-(64 < E <= 256), against the reference.
+(64 < E <= 512), and of its training, against the reference.
 
 The reference's layer takes any expert count (pipeline/CLIConfig.h:177-178).
-Here such handles run the split router (per-expert logits, then a block
-softmax / top-k over rows of up to 256 experts), the permute's offsets scan
-in wave-sized chunks with eight ballots on the expert ids, and the generic
-grouped GEMMs whose tile lookup scans the counts 64 experts at a time.
+Here such handles run the split router (logits per expert or per group of
+64 experts, then a block softmax / top-k over rows of up to 512 experts),
+the permute's offsets scan in wave-sized chunks with eight or nine ballots
+on the expert ids, the 256 x 256 GEMMs once per group of 64 experts, and
+the generic grouped GEMMs whose tile lookup scans the counts 64 experts at
+a time.
 Routing must be bit-exact with the committed fixtures of the compiled
 reference (full arrays for the small cases, digests for the large one);
 outputs are compared with the oracle's fp32 forward at 1e-5 (fp32), 2e-2
